@@ -1,0 +1,253 @@
+"""MatMulNBits 4-bit benchmark on one MI355X.
+
+Headline workload ("c2"): the Llama-3-8B gate/up
+decode projection, MatMulNBits M=1 K=4096 N=14336 bits=4 block_size=128 with
+packed zero points. One step streams ROT distinct weight copies (>= 1 GiB in
+total, so the 256 MB Infinity Cache cannot hold them) through one mnb_run
+launch each; the launches of a step are captured once in a HIP graph and the
+graph is replayed K times. value = algorithmic bytes of the timed launches /
+their event-timed duration (GB/s), inputs resident in HBM.
+
+Also reported on the same line: the prefill GEMM (configs[3], M=2048
+K=N=4096 bs=128 symmetric) in TFLOP/s against the fp16 dense MFMA peak, the
+other decode shapes, and the CPU baseline: the C oracle's fused int4 GEMV
+(``kind: port``) timed on this host's cores over the same c2 inputs.
+
+Algorithmic bytes per launch = N*nb*bs/2 (packed B) + 4*N*nb (scales) +
+N*ceil(nb/2) (zero points) + 4*M*K (A) + 4*M*N (Y); FLOPs = 2*M*N*K.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import platform
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+METRIC = "MatMulNBits 4-bit: M=1 achieved HBM GB/s; M=2048 TFLOP/s; % roofline"
+ROTATION_BYTES = 1 << 30
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU baseline sampling budget (0 disables)")
+    ap.add_argument("--only", default="", help="comma list of legs: decode,gemm,sweep,cpu")
+    return ap.parse_args()
+
+
+def make_device_weights(torch, p, copies, seed, dev):
+    """`copies` independent random weight sets for projection p, generated on device."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    sets = []
+    for _ in range(copies):
+        B = torch.randint(0, 256, (p.N, p.nb, p.block_size // 2), dtype=torch.uint8,
+                          device=dev, generator=g)
+        S = (torch.rand((p.N, p.nb), device=dev, generator=g) * (p.scale_hi - p.scale_lo)
+             + p.scale_lo).to(torch.float32)
+        Z = (torch.randint(0, 256, (p.N, p.zp_row_bytes), dtype=torch.uint8, device=dev,
+                           generator=g) if p.has_zero_points else None)
+        sets.append((B, S, Z))
+    return sets
+
+
+def time_graph(torch, launches, steps, warmup, stream):
+    """Captures `launches` (a callable issuing one step) into a graph, replays it.
+    Returns (ms per step from events on `stream`, wall seconds of the timed region)."""
+    with torch.cuda.stream(stream):
+        launches()  # eager warmup outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        launches()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / steps, wall
+
+
+def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
+    """One decode shape over >= 1 GiB of rotated weight copies."""
+    rot = max(2, -(-ROTATION_BYTES // p.weight_bytes()))
+    sets = make_device_weights(torch, p, rot, seed, dev)
+    ops = [pkg.MatMulNBits(p.K, p.N, 4, p.block_size).prepare_device(*s) for s in sets]
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 1)
+    A = (torch.randn((M, p.K), device=dev, generator=g) * p.a_sigma).contiguous()
+    Y = torch.empty((M, p.N), device=dev)
+    path = ops[0].select_path(M)
+
+    def launches():
+        for op in ops:
+            op(A, out=Y, stream=torch.cuda.current_stream())
+
+    ms, wall = time_graph(torch, launches, steps, warmup, stream)
+    per_launch_us = ms * 1e3 / rot
+    nbytes = p.algorithmic_bytes(M)
+    for op in ops:
+        op.release()
+    del sets
+    torch.cuda.empty_cache()
+    return {
+        "K": p.K, "N": p.N, "M": M, "block_size": p.block_size,
+        "zero_points": p.has_zero_points, "path": path, "rotation_copies": rot,
+        "us_per_launch": per_launch_us, "bytes_per_launch": nbytes,
+        "GBps": nbytes / (per_launch_us * 1e-6) / 1e9, "ms_per_step": ms, "wall_s": wall,
+        "launches_per_step": rot,
+    }
+
+
+def gemm_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
+    sets = make_device_weights(torch, p, 1, seed, dev)
+    op = pkg.MatMulNBits(p.K, p.N, 4, p.block_size).prepare_device(*sets[0])
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 1)
+    A = (torch.randn((M, p.K), device=dev, generator=g) * p.a_sigma).contiguous()
+    Y = torch.empty((M, p.N), device=dev)
+
+    def launches():
+        op(A, out=Y, stream=torch.cuda.current_stream())
+
+    ms, wall = time_graph(torch, launches, steps, warmup, stream)
+    flops = p.flops(M)
+    tflops = flops / (ms * 1e-3) / 1e12
+    res = {"K": p.K, "N": p.N, "M": M, "block_size": p.block_size, "path": op.select_path(M),
+           "us_per_launch": ms * 1e3, "TFLOPs": tflops, "frac_fp16_peak": tflops / FP16_PEAK_TFLOPS,
+           "bytes_per_launch": p.algorithmic_bytes(M), "wall_s": wall}
+    op.release()
+    return res
+
+
+def cpu_leg(pkg, budget_s):
+    """Fused int4 GEMV of the C oracle on the c2 M=1 workload, all host threads."""
+    import __graft_entry__
+    orc = __graft_entry__.load_oracle()
+    c = pkg.workloads.CONFIGS["c2"]
+    p = c.projections[0]
+    B, S, Z = pkg.workloads.make_weights(p, pkg.workloads.weight_seed(c.index))
+    A = pkg.workloads.make_activations(1, p.K, p.a_sigma, pkg.workloads.activation_seed(c.index, 1))
+    threads = orc.default_threads()
+    try:
+        threads = min(threads, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        pass
+    samples = []
+    for _ in range(3):
+        orc.matmul_nbits_fused_f32(A, B, S, Z, p.K, p.N, p.block_size, threads)
+    t_end = time.perf_counter() + budget_s
+    while len(samples) < 7 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        orc.matmul_nbits_fused_f32(A, B, S, Z, p.K, p.N, p.block_size, threads)
+        samples.append(time.perf_counter() - t0)
+        if len(samples) >= 2000:
+            break
+    med = statistics.median(samples)
+    q = statistics.quantiles(samples, n=4) if len(samples) >= 4 else [med, med, med]
+    nbytes = p.algorithmic_bytes(1)
+    return {
+        "value": nbytes / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": (f"c2 M=1 K=4096 N=14336 bs=128 zp, full matrix, {len(samples)} calls "
+                   f"(median {med * 1e3:.2f} ms, IQR {(q[2] - q[0]) * 1e3:.2f} ms) of the C "
+                   f"oracle's fused int4 GEMV; onnx-light CpuExecutor: not available "
+                   f"(onnx-light absent); equivalent participants = {threads}"),
+        "host": platform.processor() or platform.machine(), "nproc": os.cpu_count(),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
+              "supported (the decode GEMV would shard column-parallel over N, see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(device=dev)
+    legs = set(args.only.split(",")) if args.only else {"decode", "gemm", "sweep", "cpu"}
+    W = pkg.workloads
+
+    t_start = time.perf_counter()
+    out = {}
+    head = None
+    if "decode" in legs:
+        p = W.CONFIGS["c2"].projections[0]
+        head = decode_leg(torch, pkg, dev, p, 1, args.steps, args.warmup, 11, stream)
+        print(f"# decode c2 M=1: {head['us_per_launch']:.2f} us/launch, "
+              f"{head['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
+    gemm = None
+    if "gemm" in legs:
+        p = W.CONFIGS["c4"].projections[0]
+        gemm = gemm_leg(torch, pkg, dev, p, 2048, args.steps, args.warmup, 13, stream)
+        print(f"# gemm c4 M=2048: {gemm['us_per_launch']:.1f} us, {gemm['TFLOPs']:.1f} TFLOP/s",
+              file=sys.stderr, flush=True)
+    sweep = []
+    if "sweep" in legs:
+        for cname, Ms in (("c1", (1,)), ("c2", (4, 16)), ("c3", (1, 2, 8, 16))):
+            p = W.CONFIGS[cname].projections[0]
+            for M in Ms:
+                r = decode_leg(torch, pkg, dev, p, M, max(3, args.steps // 4), 2, 17 + M, stream)
+                r["config"] = cname
+                sweep.append({k: r[k] for k in ("config", "M", "us_per_launch", "GBps", "path")})
+                print(f"# decode {cname} M={M}: {r['us_per_launch']:.2f} us, {r['GBps']:.0f} GB/s",
+                      file=sys.stderr, flush=True)
+    cpu = None
+    if "cpu" in legs and args.cpu_seconds > 0:
+        cpu = cpu_leg(pkg, args.cpu_seconds)
+        print(f"# cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads",
+              file=sys.stderr, flush=True)
+
+    if head is not None:
+        value = head["GBps"]
+        ms_per_step = head["ms_per_step"]
+        roof = {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": head["GBps"] / HBM_PEAK_GBS, "traffic": None,
+                "kernel": "GemvKernel (c2 M=1)", "us_per_launch": head["us_per_launch"],
+                "bytes_per_launch": head["bytes_per_launch"]}
+        workload = ("c2: MatMulNBits M=1 K=4096 N=14336 bits=4 block_size=128 zero_points; "
+                    f"{head['rotation_copies']} rotated weight copies per step")
+    else:
+        value, ms_per_step, roof, workload = None, None, None, "none"
+    out = {
+        "metric": METRIC, "value": value, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u4xf32 (fp32 FMA)",
+        "data": "synthetic (seeded uniform nibbles, uniform scales, N(0,1) activations)",
+        "config": {"workload": workload, "M": 1, "K": 4096, "N": 14336, "block_size": 128,
+                   "zero_points": True},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "prefill_gemm": gemm,
+        "decode_sweep": sweep,
+        "bench_wall_s": time.perf_counter() - t_start,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,124 @@
+/*
+ * mnb.h -- C ABI of the MI355X MatMulNBits (com.microsoft, bits = 4) library.
+ *
+ * The library implements the operator the onnx-light-cpu roadmap plans as
+ * `int4_gemv` / `int4_small_m` / `int4_gemm` behind a prepared weight-only plan
+ * (docs/next_steps/2026/2026_08_qwen3_inference.rst:188-230, 400-419, 530-540).
+ * The reference has no GPU and no C ABI; each entry point below names the
+ * reference interface whose role it takes over.
+ *
+ * Conventions
+ *  - Plain C types only. Streams are passed as `void*` holding a hipStream_t
+ *    (NULL = the default stream).
+ *  - Every entry point returns an mnb_status; nothing throws across the ABI.
+ *    Argument validation happens before any HIP call, so bad shapes and null
+ *    pointers are reported without touching the GPU.
+ *  - A plan is immutable after creation. mnb_run is reentrant for distinct
+ *    output and workspace buffers; the plan's device constants are shared.
+ *
+ * Operator contract (ONNX Runtime contrib op, the layout this library keeps):
+ *   A      fp32 [M, K] row-major (device memory)
+ *   B      uint8 [N, nb, block_size/2], nb = ceil(K / block_size); element
+ *          k = b*block_size + j of row n is nibble j of B[n, b, :], low nibble
+ *          first (onnx_light_cpu/impl/math/gemm/vnni/integer_gemm_vnni.h:42-51)
+ *   scales fp32 [N, nb]
+ *   zero_points uint8 [N, ceil(nb/2)], nibble b of row n, low nibble first;
+ *          absent means 8
+ *   Y      fp32 [M, N] = A * W^T, W[n,k] = (q - zp) * scale
+ */
+#ifndef MNB_H
+#define MNB_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mnb_status {
+  MNB_OK = 0,
+  MNB_ERR_NULL_POINTER = 1,     /* a required pointer is NULL */
+  MNB_ERR_BAD_SHAPE = 2,        /* K, N or M out of range */
+  MNB_ERR_BAD_ATTRIBUTE = 3,    /* block_size not a power of two >= 16, bad accuracy_level */
+  MNB_ERR_UNSUPPORTED = 4,      /* bits != 4, or an input this version rejects */
+  MNB_ERR_WORKSPACE = 5,        /* workspace smaller than mnb_workspace_bytes */
+  MNB_ERR_HIP = 6,              /* a HIP runtime call failed */
+  MNB_ERR_NO_DEVICE = 7,        /* no gfx950 device is current */
+  MNB_ERR_ALLOC = 8             /* device allocation failed */
+} mnb_status;
+
+/* Node attributes and optional-input presence of one MatMulNBits node.
+ * Replaces what KernelBase reads from the NodeProto in the reference's
+ * operator wrappers (onnx_light_cpu/kernels/math/gemm_kernel.cc:470-473 for
+ * attributes, integer_matmul_kernel.cc:375-376 for optional inputs). */
+typedef struct mnb_desc {
+  int64_t K;                /* attribute K */
+  int64_t N;                /* attribute N */
+  int32_t bits;             /* attribute bits: 4 only */
+  int32_t block_size;       /* attribute block_size: power of two >= 16 */
+  int32_t accuracy_level;   /* attribute accuracy_level: 0..4 accepted; see mnb_run */
+  int32_t has_zero_points;  /* input 3 present */
+} mnb_desc;
+
+typedef struct mnb_plan mnb_plan;
+
+/* Prepared plan: validates the attributes and uploads the constant B, scales
+ * and zero points (host pointers) to the current device once; the plan owns
+ * the device copies. Replaces the reference's prepared plan with a constant B
+ * (MatMulPlan constant_b, onnx_light_cpu/impl/math/gemm/gemm_plan.h:161-195;
+ * GemmPlanOptions::constant_b, gemm_plan.h:34-38). zero_points must be NULL
+ * when desc->has_zero_points == 0. */
+int mnb_plan_create(const mnb_desc *desc, const uint8_t *B, const float *scales,
+                    const uint8_t *zero_points, mnb_plan **out_plan);
+
+/* Same as mnb_plan_create, but B, scales and zero_points are device pointers
+ * on the current device that the plan borrows without copying: the caller
+ * keeps them alive and unchanged for the plan's lifetime. */
+int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float *dScales,
+                           const uint8_t *dZeroPoints, mnb_plan **out_plan);
+
+/* Releases the plan and the device memory it owns. NULL is accepted. */
+int mnb_plan_destroy(mnb_plan *plan);
+
+/* Device workspace mnb_run needs for M rows (0 when none). */
+int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
+
+/* Y = MatMulNBits(A, plan) for M rows; dA and dY are device pointers on the
+ * plan's device. M == 0 is a no-op. Replaces the operator's compute call,
+ * MatMulKernel::operator() -> MatMulPlan<float>::Execute
+ * (onnx_light_cpu/kernels/math/matmul_kernel.cc:117-134, gemm_plan.cc:539-570).
+ * M <= 16: fp32-FMA decode GEMV; M > 16: fp16-MFMA prefill GEMM with A
+ * rounded to fp16 (round to nearest even, half_conversion.h:42-78) and fp32
+ * accumulation. The launch is asynchronous on `stream`. */
+int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
+            size_t workspace_bytes, void *stream);
+
+/* Same as mnb_run with the kernel chosen by the caller:
+ * path 0 = automatic, 1 = decode GEMV (any M <= 16), 2 = MFMA GEMM (any M),
+ * 3 = generic fallback (any shape; slow, for cross-checks). */
+int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
+                 size_t workspace_bytes, void *stream, int path);
+
+/* Which path mnb_run takes for M rows (1, 2 or 3 as in mnb_run_path). */
+int mnb_select_path(const mnb_plan *plan, int64_t M, int *path);
+
+/* Text for a status code (static storage). */
+const char *mnb_status_str(int status);
+
+/* Text of the last HIP error seen by this thread ("" if none). */
+const char *mnb_last_error(void);
+
+/* Bytes a plan with this description reads per call beyond A and Y
+ * (packed B + fp32 scales + packed zero points): the algorithmic weight
+ * bytes of one launch. */
+int mnb_weight_bytes(const mnb_desc *desc, size_t *bytes);
+
+/* Library version string. */
+const char *mnb_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MNB_H */

@@ -1,0 +1,216 @@
+"""onnx-light-cpu_amd: MatMulNBits (com.microsoft, bits=4) for AMD MI355X.
+
+Python mirror of the operator over the C ABI in ``include/mnb.h``
+(``libmnb.so``, gfx950 HIP kernels) and of the registration entry points in
+``libolc_amd.so`` (C++ host side). The mirror follows the reference's Python
+surface: ``register_kernels()`` / ``registered_kernels()`` /
+``used_kernel_names()`` (onnx_light_cpu/_register.py:263-379) and an
+operator object whose errors are ``ValueError`` with the reference's
+``"<library>::<Kernel>: ..."`` message style
+(onnx_light_cpu/kernels/math/matmul_kernel.cc:38-41).
+
+There is no CPU fallback: if ``libmnb.so`` is missing or no gfx950 device is
+current, every compute call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+import numpy as np
+
+from . import workloads  # noqa: F401  (re-exported for bench and tests)
+
+HERE = pathlib.Path(__file__).resolve().parent
+ROOT = HERE.parent
+LIB_PATH = HERE / "libmnb.so"
+HOST_LIB_PATH = HERE / "libolc_amd.so"
+HEADER_PATH = ROOT / "include" / "mnb.h"
+
+KERNEL_PREFIX = "onnx_light_cpu_amd::MatMulNBits"
+
+STATUS = {
+    0: "MNB_OK", 1: "MNB_ERR_NULL_POINTER", 2: "MNB_ERR_BAD_SHAPE", 3: "MNB_ERR_BAD_ATTRIBUTE",
+    4: "MNB_ERR_UNSUPPORTED", 5: "MNB_ERR_WORKSPACE", 6: "MNB_ERR_HIP", 7: "MNB_ERR_NO_DEVICE",
+    8: "MNB_ERR_ALLOC",
+}
+PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GENERIC = 0, 1, 2, 3
+
+
+class MnbDesc(ctypes.Structure):
+    _fields_ = [("K", ctypes.c_int64), ("N", ctypes.c_int64), ("bits", ctypes.c_int32),
+                ("block_size", ctypes.c_int32), ("accuracy_level", ctypes.c_int32),
+                ("has_zero_points", ctypes.c_int32)]
+
+
+_lib = None
+
+
+def library():
+    """Loads libmnb.so (built in-tree by ``make -C onnx-light-cpu_amd``)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t
+        L.mnb_plan_create.argtypes = [ctypes.POINTER(MnbDesc), vp, vp, vp, ctypes.POINTER(vp)]
+        L.mnb_plan_create_device.argtypes = [ctypes.POINTER(MnbDesc), vp, vp, vp,
+                                             ctypes.POINTER(vp)]
+        L.mnb_plan_destroy.argtypes = [vp]
+        L.mnb_workspace_bytes.argtypes = [vp, i64, ctypes.POINTER(sz)]
+        L.mnb_run.argtypes = [vp, i64, vp, vp, vp, sz, vp]
+        L.mnb_run_path.argtypes = [vp, i64, vp, vp, vp, sz, vp, ctypes.c_int]
+        L.mnb_select_path.argtypes = [vp, i64, ctypes.POINTER(ctypes.c_int)]
+        L.mnb_status_str.argtypes = [ctypes.c_int]
+        L.mnb_status_str.restype = ctypes.c_char_p
+        L.mnb_last_error.restype = ctypes.c_char_p
+        L.mnb_weight_bytes.argtypes = [ctypes.POINTER(MnbDesc), ctypes.POINTER(sz)]
+        L.mnb_version.restype = ctypes.c_char_p
+        for name in ("mnb_plan_create", "mnb_plan_create_device", "mnb_plan_destroy",
+                     "mnb_workspace_bytes", "mnb_run", "mnb_run_path", "mnb_select_path",
+                     "mnb_weight_bytes"):
+            getattr(L, name).restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def header_functions():
+    """Names of the functions declared in include/mnb.h."""
+    import re
+    text = HEADER_PATH.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mnb_\w+)\s*\(", text, re.M)))
+
+
+class MatMulNBitsError(ValueError):
+    """Raised for a non-OK status (the reference throws std::invalid_argument)."""
+
+    def __init__(self, status: int, what: str):
+        self.status = status
+        L = library()
+        detail = L.mnb_last_error().decode() if status in (6, 7, 8) else ""
+        msg = f"{KERNEL_PREFIX}: {what}: {L.mnb_status_str(status).decode()}"
+        if detail:
+            msg += f" ({detail})"
+        super().__init__(msg)
+
+
+def _check(status: int, what: str):
+    if status != 0:
+        raise MatMulNBitsError(status, what)
+
+
+def _host_ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _dev_ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+class MatMulNBits:
+    """One MatMulNBits node: attributes at construction, constants at prepare().
+
+    Mirrors the operator contract of ONNX Runtime's com.microsoft::MatMulNBits
+    (attributes K, N, bits, block_size, accuracy_level; inputs A, B, scales,
+    zero_points). ``g_idx`` and ``bias`` inputs are rejected.
+    """
+
+    domain = "com.microsoft"
+    op_type = "MatMulNBits"
+
+    def __init__(self, K: int, N: int, bits: int = 4, block_size: int = 32,
+                 accuracy_level: int = 0):
+        self.desc = MnbDesc(K, N, bits, block_size, accuracy_level, 0)
+        self._plan = ctypes.c_void_p()
+        self._keep = ()
+
+    # -- constants ---------------------------------------------------------
+    def prepare(self, B, scales, zero_points=None):
+        """Uploads host (numpy) constants once; the plan owns device copies."""
+        self.release()
+        self.desc.has_zero_points = int(zero_points is not None)
+        B = np.ascontiguousarray(B, dtype=np.uint8)
+        scales = np.ascontiguousarray(scales, dtype=np.float32)
+        zp = None if zero_points is None else np.ascontiguousarray(zero_points, dtype=np.uint8)
+        self._check_sizes(B.size, scales.size, None if zp is None else zp.size)
+        _check(library().mnb_plan_create(ctypes.byref(self.desc), _host_ptr(B), _host_ptr(scales),
+                                         _host_ptr(zp), ctypes.byref(self._plan)),
+               "prepare")
+        return self
+
+    def prepare_device(self, dB, dScales, dZeroPoints=None):
+        """Borrows device (torch) constants; the tensors are kept referenced."""
+        self.release()
+        self.desc.has_zero_points = int(dZeroPoints is not None)
+        self._check_sizes(dB.numel(), dScales.numel(),
+                          None if dZeroPoints is None else dZeroPoints.numel())
+        _check(library().mnb_plan_create_device(ctypes.byref(self.desc), _dev_ptr(dB),
+                                                _dev_ptr(dScales), _dev_ptr(dZeroPoints),
+                                                ctypes.byref(self._plan)),
+               "prepare_device")
+        self._keep = (dB, dScales, dZeroPoints)
+        return self
+
+    def _check_sizes(self, b, s, z):
+        d = self.desc
+        if d.block_size <= 0 or d.K <= 0 or d.N <= 0:
+            return  # the C ABI reports the attribute error
+        nb = (d.K + d.block_size - 1) // d.block_size
+        if b != d.N * nb * (d.block_size // 2):
+            raise ValueError(f"{KERNEL_PREFIX}: B has {b} bytes, expected N*nb*bs/2 = "
+                             f"{d.N * nb * (d.block_size // 2)}")
+        if s != d.N * nb:
+            raise ValueError(f"{KERNEL_PREFIX}: scales has {s} elements, expected {d.N * nb}")
+        if z is not None and z != d.N * ((nb + 1) // 2):
+            raise ValueError(f"{KERNEL_PREFIX}: zero_points has {z} bytes, expected "
+                             f"{d.N * ((nb + 1) // 2)}")
+
+    def release(self):
+        if self._plan:
+            library().mnb_plan_destroy(self._plan)
+            self._plan = ctypes.c_void_p()
+        self._keep = ()
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    # -- compute -----------------------------------------------------------
+    def select_path(self, M: int) -> int:
+        p = ctypes.c_int()
+        _check(library().mnb_select_path(self._plan, M, ctypes.byref(p)), "select_path")
+        return p.value
+
+    def __call__(self, A, out=None, path: int = PATH_AUTO, stream=None):
+        """Y[..., M, N] = A[..., M, K] * W^T on A's device (a torch CUDA tensor)."""
+        import torch
+        if not self._plan:
+            raise ValueError(f"{KERNEL_PREFIX}: prepare() was not called")
+        if not A.is_cuda or A.dtype != torch.float32:
+            raise ValueError(f"{KERNEL_PREFIX}: A must be a float32 device tensor")
+        if A.shape[-1] != self.desc.K:
+            raise ValueError(f"{KERNEL_PREFIX}: A's last dimension {A.shape[-1]} != K "
+                             f"{self.desc.K}")
+        A2 = A.reshape(-1, self.desc.K).contiguous()
+        M = A2.shape[0]
+        if out is None:
+            out = torch.empty(*A.shape[:-1], self.desc.N, device=A.device, dtype=torch.float32)
+        if not out.is_contiguous() or out.numel() != M * self.desc.N:
+            raise ValueError(f"{KERNEL_PREFIX}: out must be contiguous [..., M, N]")
+        s = stream if stream is not None else torch.cuda.current_stream(A.device)
+        _check(library().mnb_run_path(self._plan, M, _dev_ptr(A2), _dev_ptr(out), None, 0,
+                                      ctypes.c_void_p(s.cuda_stream), path),
+               "run")
+        return out
+
+    run = __call__
+
+
+def weight_bytes(K, N, block_size, has_zero_points, bits=4) -> int:
+    d = MnbDesc(K, N, bits, block_size, 0, int(has_zero_points))
+    b = ctypes.c_size_t()
+    _check(library().mnb_weight_bytes(ctypes.byref(d), ctypes.byref(b)), "weight_bytes")
+    return b.value

@@ -1,0 +1,287 @@
+// C ABI of the MatMulNBits library: plan lifetime, validation, dispatch.
+//
+// Validation mirrors the reference operator wrappers' argument checks
+// (onnx_light_cpu/kernels/math/matmul_kernel.cc:38-41, 118-133;
+// integer_matmul_kernel.cc:153-174) but reports status codes instead of
+// throwing, and it runs before any HIP call.
+#include "../../include/mnb.h"
+#include "mnb_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <new>
+
+struct mnb_plan {
+  mnb_desc desc;
+  mnb::WeightView view;
+  int device;
+  bool owns;
+  uint8_t *dB;
+  float *dS;
+  uint8_t *dZ;
+};
+
+namespace {
+
+thread_local char g_last_error[256] = "";
+
+void SetLastError(const char *what, hipError_t e) {
+  std::snprintf(g_last_error, sizeof(g_last_error), "%s: %s", what, hipGetErrorString(e));
+}
+
+bool IsPow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+int Log2(int64_t v) {
+  int r = 0;
+  while ((int64_t{1} << r) < v) ++r;
+  return r;
+}
+
+int ValidateDesc(const mnb_desc *d) {
+  if (d == nullptr) return MNB_ERR_NULL_POINTER;
+  if (d->bits != 4) return MNB_ERR_UNSUPPORTED;
+  if (!IsPow2(d->block_size) || d->block_size < 16) return MNB_ERR_BAD_ATTRIBUTE;
+  if (d->accuracy_level < 0 || d->accuracy_level > 4) return MNB_ERR_BAD_ATTRIBUTE;
+  if (d->K <= 0 || d->N <= 0) return MNB_ERR_BAD_SHAPE;
+  if (d->K > (int64_t{1} << 30) || d->N > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
+  if (d->has_zero_points != 0 && d->has_zero_points != 1) return MNB_ERR_BAD_ATTRIBUTE;
+  return MNB_OK;
+}
+
+void Sizes(const mnb_desc *d, int64_t *nb, int64_t *row_bytes, int64_t *zp_row_bytes) {
+  *nb = (d->K + d->block_size - 1) / d->block_size;
+  *row_bytes = *nb * d->block_size / 2;
+  *zp_row_bytes = (*nb + 1) / 2;
+}
+
+int CheckDevice(int *device) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    SetLastError("hipGetDevice", e);
+    return MNB_ERR_NO_DEVICE;
+  }
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) {
+    SetLastError("hipGetDeviceProperties", e);
+    return MNB_ERR_NO_DEVICE;
+  }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    std::snprintf(g_last_error, sizeof(g_last_error), "device %d is %s, this library is gfx950",
+                  dev, prop.gcnArchName);
+    return MNB_ERR_NO_DEVICE;
+  }
+  *device = dev;
+  return MNB_OK;
+}
+
+void FillView(mnb_plan *p) {
+  int64_t nb, row_bytes, zp_row_bytes;
+  Sizes(&p->desc, &nb, &row_bytes, &zp_row_bytes);
+  p->view.B = p->dB;
+  p->view.scales = p->dS;
+  p->view.zp = p->desc.has_zero_points ? p->dZ : nullptr;
+  p->view.K = p->desc.K;
+  p->view.N = p->desc.N;
+  p->view.nb = nb;
+  p->view.row_bytes = row_bytes;
+  p->view.zp_row_bytes = zp_row_bytes;
+  p->view.block_size = p->desc.block_size;
+  p->view.log2_bs = Log2(p->desc.block_size);
+}
+
+void FreePlanMemory(mnb_plan *p) {
+  if (p->owns) {
+    if (p->dB) (void)hipFree(p->dB);
+    if (p->dS) (void)hipFree(p->dS);
+    if (p->dZ) (void)hipFree(p->dZ);
+  }
+  p->dB = nullptr;
+  p->dS = nullptr;
+  p->dZ = nullptr;
+}
+
+int CheckInputs(const mnb_desc *desc, const void *B, const void *scales, const void *zp,
+                mnb_plan **out_plan) {
+  if (out_plan == nullptr) return MNB_ERR_NULL_POINTER;
+  *out_plan = nullptr;
+  int st = ValidateDesc(desc);
+  if (st != MNB_OK) return st;
+  if (B == nullptr || scales == nullptr) return MNB_ERR_NULL_POINTER;
+  if (desc->has_zero_points && zp == nullptr) return MNB_ERR_NULL_POINTER;
+  if (!desc->has_zero_points && zp != nullptr) return MNB_ERR_UNSUPPORTED;
+  return MNB_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+const char *mnb_version(void) { return "mnb-gfx950 0.1.0"; }
+
+const char *mnb_last_error(void) { return g_last_error; }
+
+const char *mnb_status_str(int status) {
+  switch (status) {
+  case MNB_OK: return "ok";
+  case MNB_ERR_NULL_POINTER: return "null pointer";
+  case MNB_ERR_BAD_SHAPE: return "bad shape";
+  case MNB_ERR_BAD_ATTRIBUTE: return "bad attribute";
+  case MNB_ERR_UNSUPPORTED: return "unsupported";
+  case MNB_ERR_WORKSPACE: return "workspace too small";
+  case MNB_ERR_HIP: return "HIP runtime error";
+  case MNB_ERR_NO_DEVICE: return "no gfx950 device";
+  case MNB_ERR_ALLOC: return "device allocation failed";
+  default: return "unknown status";
+  }
+}
+
+int mnb_weight_bytes(const mnb_desc *desc, size_t *bytes) {
+  if (bytes == nullptr) return MNB_ERR_NULL_POINTER;
+  int st = ValidateDesc(desc);
+  if (st != MNB_OK) return st;
+  int64_t nb, row_bytes, zp_row_bytes;
+  Sizes(desc, &nb, &row_bytes, &zp_row_bytes);
+  *bytes = static_cast<size_t>(desc->N) *
+           static_cast<size_t>(row_bytes + 4 * nb + (desc->has_zero_points ? zp_row_bytes : 0));
+  return MNB_OK;
+}
+
+int mnb_plan_create(const mnb_desc *desc, const uint8_t *B, const float *scales,
+                    const uint8_t *zero_points, mnb_plan **out_plan) {
+  int st = CheckInputs(desc, B, scales, zero_points, out_plan);
+  if (st != MNB_OK) return st;
+  int dev = -1;
+  st = CheckDevice(&dev);
+  if (st != MNB_OK) return st;
+
+  mnb_plan *p = new (std::nothrow) mnb_plan();
+  if (p == nullptr) return MNB_ERR_ALLOC;
+  p->desc = *desc;
+  p->device = dev;
+  p->owns = true;
+  int64_t nb, row_bytes, zp_row_bytes;
+  Sizes(desc, &nb, &row_bytes, &zp_row_bytes);
+  const size_t b_bytes = static_cast<size_t>(desc->N) * static_cast<size_t>(row_bytes);
+  const size_t s_bytes = static_cast<size_t>(desc->N) * static_cast<size_t>(nb) * sizeof(float);
+  const size_t z_bytes = static_cast<size_t>(desc->N) * static_cast<size_t>(zp_row_bytes);
+
+  hipError_t e = hipMalloc(reinterpret_cast<void **>(&p->dB), b_bytes);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&p->dS), s_bytes);
+  if (e == hipSuccess && desc->has_zero_points)
+    e = hipMalloc(reinterpret_cast<void **>(&p->dZ), z_bytes);
+  if (e != hipSuccess) {
+    SetLastError("hipMalloc", e);
+    FreePlanMemory(p);
+    delete p;
+    return MNB_ERR_ALLOC;
+  }
+  e = hipMemcpy(p->dB, B, b_bytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(p->dS, scales, s_bytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess && desc->has_zero_points)
+    e = hipMemcpy(p->dZ, zero_points, z_bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    SetLastError("hipMemcpy", e);
+    FreePlanMemory(p);
+    delete p;
+    return MNB_ERR_HIP;
+  }
+  FillView(p);
+  *out_plan = p;
+  return MNB_OK;
+}
+
+int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float *dScales,
+                           const uint8_t *dZeroPoints, mnb_plan **out_plan) {
+  int st = CheckInputs(desc, dB, dScales, dZeroPoints, out_plan);
+  if (st != MNB_OK) return st;
+  if ((reinterpret_cast<uintptr_t>(dScales) % 4) != 0) return MNB_ERR_BAD_SHAPE;
+  int dev = -1;
+  st = CheckDevice(&dev);
+  if (st != MNB_OK) return st;
+  mnb_plan *p = new (std::nothrow) mnb_plan();
+  if (p == nullptr) return MNB_ERR_ALLOC;
+  p->desc = *desc;
+  p->device = dev;
+  p->owns = false;
+  p->dB = const_cast<uint8_t *>(dB);
+  p->dS = const_cast<float *>(dScales);
+  p->dZ = const_cast<uint8_t *>(dZeroPoints);
+  FillView(p);
+  *out_plan = p;
+  return MNB_OK;
+}
+
+int mnb_plan_destroy(mnb_plan *plan) {
+  if (plan == nullptr) return MNB_OK;
+  FreePlanMemory(plan);
+  delete plan;
+  return MNB_OK;
+}
+
+int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
+  if (plan == nullptr || bytes == nullptr) return MNB_ERR_NULL_POINTER;
+  if (M < 0) return MNB_ERR_BAD_SHAPE;
+  *bytes = 0;
+  return MNB_OK;
+}
+
+static int SelectPath(const mnb_plan *plan, int64_t M, const float *dA) {
+  const bool a_aligned = (reinterpret_cast<uintptr_t>(dA) % 16) == 0;
+  if (a_aligned && M <= 16 && mnb::GemvSupports(plan->view, M)) return 1;
+  if (a_aligned && mnb::GemmSupports(plan->view, M)) return 2;
+  return 3;
+}
+
+int mnb_select_path(const mnb_plan *plan, int64_t M, int *path) {
+  if (plan == nullptr || path == nullptr) return MNB_ERR_NULL_POINTER;
+  if (M < 0) return MNB_ERR_BAD_SHAPE;
+  // Paths are chosen for a 16-byte-aligned activation buffer, as hipMalloc returns.
+  *path = SelectPath(plan, M, nullptr);
+  return MNB_OK;
+}
+
+int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
+                 size_t workspace_bytes, void *stream, int path) {
+  (void)dWorkspace;
+  (void)workspace_bytes;
+  if (plan == nullptr) return MNB_ERR_NULL_POINTER;
+  if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
+  if (M == 0) return MNB_OK;
+  if (dA == nullptr || dY == nullptr) return MNB_ERR_NULL_POINTER;
+  if (path < 0 || path > 3) return MNB_ERR_UNSUPPORTED;
+  const bool a_aligned = (reinterpret_cast<uintptr_t>(dA) % 16) == 0;
+  if (path == 0) path = SelectPath(plan, M, dA);
+  if (path == 1 && !(a_aligned && M <= 16 && mnb::GemvSupports(plan->view, M)))
+    return MNB_ERR_UNSUPPORTED;
+  if (path == 2 && !(a_aligned && mnb::GemmSupports(plan->view, M))) return MNB_ERR_UNSUPPORTED;
+
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess || cur != plan->device) {
+    std::snprintf(g_last_error, sizeof(g_last_error), "plan lives on device %d, current is %d",
+                  plan->device, cur);
+    return MNB_ERR_NO_DEVICE;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (path) {
+  case 1: e = mnb::LaunchGemv(plan->view, M, dA, dY, s); break;
+  case 2: e = mnb::LaunchGemm(plan->view, M, dA, dY, s); break;
+  default: e = mnb::LaunchGeneric(plan->view, M, dA, dY, s); break;
+  }
+  if (e != hipSuccess) {
+    SetLastError("kernel launch", e);
+    return MNB_ERR_HIP;
+  }
+  return MNB_OK;
+}
+
+int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
+            size_t workspace_bytes, void *stream) {
+  return mnb_run_path(plan, M, dA, dY, dWorkspace, workspace_bytes, stream, 0);
+}
+
+} // extern "C"

@@ -1,0 +1,38 @@
+// Internal launch interface shared by the C ABI (mnb_capi.hip) and the kernel
+// translation units. Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace mnb {
+
+// Everything a kernel needs to address one plan's constants.
+struct WeightView {
+  const uint8_t *B;       // [N, nb, bs/2] packed nibbles, low nibble first
+  const float *scales;    // [N, nb]
+  const uint8_t *zp;      // [N, zp_row_bytes] packed nibbles, or nullptr (zp = 8)
+  int64_t K;
+  int64_t N;
+  int64_t nb;             // ceil(K / bs)
+  int64_t row_bytes;      // nb * bs / 2
+  int64_t zp_row_bytes;   // ceil(nb / 2)
+  int32_t block_size;
+  int32_t log2_bs;
+};
+
+// Decode GEMV, M in [1, 16], K % 32 == 0, block_size >= 32.
+hipError_t LaunchGemv(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s);
+bool GemvSupports(const WeightView &w, int64_t M);
+
+// Prefill GEMM on fp16 MFMA, any M, K % 32 == 0.
+hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s);
+bool GemmSupports(const WeightView &w, int64_t M);
+
+// Generic fallback: any K, any block_size, any M. Slow; for odd shapes and
+// cross-checks.
+hipError_t LaunchGeneric(const WeightView &w, int64_t M, const float *A, float *Y,
+                         hipStream_t s);
+
+} // namespace mnb

@@ -1,0 +1,138 @@
+// C entry points over the C++ host side, for the Python mirror
+// (the role of onnx_light_cpu/onnx_py/_cpuregister.cc:62-114: register,
+// inventory, usage log) plus a node runner that goes through the dispatch
+// table the way onnx-light's RunNode would. Exceptions never cross this
+// boundary: failures return -1 and leave a message for olc_amd_last_error().
+#include "kernel_registration.h"
+#include "register_kernels.h"
+
+#include <cstring>
+#include <exception>
+#include <sstream>
+#include <string>
+
+namespace {
+
+thread_local std::string g_error;
+
+size_t CopyOut(const std::string &s, char *buf, size_t cap) {
+  if (buf != nullptr && cap > 0) {
+    const size_t n = s.size() < cap - 1 ? s.size() : cap - 1;
+    std::memcpy(buf, s.data(), n);
+    buf[n] = '\0';
+  }
+  return s.size() + 1;
+}
+
+template <typename F> int Guard(F &&f) {
+  try {
+    f();
+    g_error.clear();
+    return 0;
+  } catch (const std::exception &e) {
+    g_error = e.what();
+    return -1;
+  } catch (...) {
+    g_error = "unknown exception";
+    return -1;
+  }
+}
+
+} // namespace
+
+using namespace onnx_light_cpu_amd;
+
+extern "C" {
+
+const char *olc_amd_last_error(void) { return g_error.c_str(); }
+
+int olc_amd_register_all_kernels(void) {
+  return Guard([] { RegisterAllKernels(); });
+}
+
+int olc_amd_register_matmul_nbits_kernel(void) {
+  return Guard([] { RegisterMatMulNBitsKernel(); });
+}
+
+// One line per registration: domain, op_type, device, kernel_name, types
+// (comma separated TensorProto values), since, until (-1 = none); tab separated.
+size_t olc_amd_registered_kernels(char *buf, size_t cap) {
+  std::ostringstream os;
+  try {
+    for (const auto &r : CollectRegisteredKernels()) {
+      os << r.domain << '\t' << r.op_type << '\t' << static_cast<int32_t>(r.device) << '\t'
+         << r.kernel_name << '\t';
+      for (size_t i = 0; i < r.types.size(); ++i)
+        os << (i ? "," : "") << static_cast<int32_t>(r.types[i]);
+      os << '\t' << r.since_version.value_or(-1) << '\t' << r.until_version.value_or(-1) << '\n';
+    }
+  } catch (const std::exception &e) {
+    g_error = e.what();
+    return 0;
+  }
+  return CopyOut(os.str(), buf, cap);
+}
+
+size_t olc_amd_used_kernel_names(char *buf, size_t cap) {
+  std::string s;
+  for (const auto &n : UsedKernelNames()) s += n + "\n";
+  return CopyOut(s, buf, cap);
+}
+
+void olc_amd_clear_used_kernel_names(void) { ClearUsedKernelNames(); }
+
+void olc_amd_set_usage_recording(int enabled) { SetKernelUsageRecording(enabled != 0); }
+
+size_t olc_amd_dispatch_keys(char *buf, size_t cap) {
+  std::string s;
+  for (const auto &k : DispatchTableKeys()) s += k + "\n";
+  return CopyOut(s, buf, cap);
+}
+
+void olc_amd_clear_dispatch_table(void) { ClearDispatchTable(); }
+
+// Runs one node through the dispatch table. Inputs are given as parallel
+// arrays; a NULL input pointer means the optional input is absent. dims holds
+// every input's dimensions back to back. The output is a caller-provided
+// device buffer of output_numel floats.
+int olc_amd_run_node(const char *domain, const char *op_type, int device, int n_attrs,
+                     const char *const *attr_names, const int64_t *attr_values, int n_inputs,
+                     void *const *input_ptrs, const int32_t *input_types,
+                     const int32_t *input_devices, const int32_t *input_ranks,
+                     const int64_t *dims, void *output, int64_t output_numel, void *stream) {
+  return Guard([&] {
+    NodeKernelFn fn = LookupKernel(domain ? domain : "", op_type ? op_type : "",
+                                   static_cast<Device>(device));
+    if (!fn)
+      throw std::invalid_argument(std::string("onnx_light_cpu_amd::RunNode: no kernel for '") +
+                                  (domain ? domain : "") + ":" + (op_type ? op_type : "") + "'");
+    NodeAttributes attrs;
+    for (int i = 0; i < n_attrs; ++i) attrs.ints[attr_names[i]] = attr_values[i];
+    RuntimeContext rt;
+    rt.stream = stream;
+    const int64_t *d = dims;
+    for (int i = 0; i < n_inputs; ++i) {
+      if (input_ptrs[i] == nullptr) {
+        rt.inputs.emplace_back(std::nullopt);
+        d += input_ranks[i];
+        continue;
+      }
+      TensorView t;
+      t.data = input_ptrs[i];
+      t.type = static_cast<DataType>(input_types[i]);
+      t.device = static_cast<Device>(input_devices[i]);
+      t.shape.assign(d, d + input_ranks[i]);
+      d += input_ranks[i];
+      rt.inputs.emplace_back(std::move(t));
+    }
+    TensorView y;
+    y.data = output;
+    y.type = DataType::kFloat;
+    y.shape = {output_numel};
+    rt.outputs.push_back(y);
+    std::unique_ptr<KernelBase> kernel = fn(attrs, rt);
+    kernel->Run(rt);
+  });
+}
+
+} // extern "C"
