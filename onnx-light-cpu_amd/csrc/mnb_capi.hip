@@ -78,6 +78,14 @@ int CheckDevice(int *device) {
   return MNB_OK;
 }
 
+int DeviceCUs(int dev) {
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  return cus;
+}
+
 void FillView(mnb_plan *p) {
   int64_t nb, row_bytes, zp_row_bytes;
   Sizes(&p->desc, &nb, &row_bytes, &zp_row_bytes);
@@ -91,6 +99,7 @@ void FillView(mnb_plan *p) {
   p->view.zp_row_bytes = zp_row_bytes;
   p->view.block_size = p->desc.block_size;
   p->view.log2_bs = Log2(p->desc.block_size);
+  p->view.num_cus = DeviceCUs(p->device);
 }
 
 void FreePlanMemory(mnb_plan *p) {
@@ -268,7 +277,12 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (path) {
-  case 1: e = mnb::LaunchGemv(plan->view, M, dA, dY, s); break;
+  case 1:
+    e = (M == 1 && mnb::GemvM1Supports(plan->view))
+            ? mnb::LaunchGemvM1(plan->view, dA, dY, s,
+                                plan->view.K <= 4096 ? 4 * plan->view.num_cus : plan->view.num_cus, 2)
+            : mnb::LaunchGemv(plan->view, M, dA, dY, s);
+    break;
   case 2: e = mnb::LaunchGemm(plan->view, M, dA, dY, s); break;
   default: e = mnb::LaunchGeneric(plan->view, M, dA, dY, s); break;
   }

@@ -20,11 +20,18 @@ struct WeightView {
   int64_t zp_row_bytes;   // ceil(nb / 2)
   int32_t block_size;
   int32_t log2_bs;
+  int32_t num_cus;        // compute units of the plan's device
 };
 
 // Decode GEMV, M in [1, 16], K % 32 == 0, block_size >= 32.
 hipError_t LaunchGemv(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s);
 bool GemvSupports(const WeightView &w, int64_t M);
+
+// Decode GEMV for M == 1 (fp16-subnormal mixed FMA), persistent grid of at
+// most `workgroups` workgroups of 256 threads.
+hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
+                        int workgroups, int rows_per_batch);
+bool GemvM1Supports(const WeightView &w);
 
 // Prefill GEMM on fp16 MFMA, any M, K % 32 == 0.
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s);
