@@ -214,3 +214,114 @@ def weight_bytes(K, N, block_size, has_zero_points, bits=4) -> int:
     b = ctypes.c_size_t()
     _check(library().mnb_weight_bytes(ctypes.byref(d), ctypes.byref(b)), "weight_bytes")
     return b.value
+
+
+# ---- registration mirror (onnx_light_cpu/_register.py:263-379) over libolc_amd.so ----
+
+_host = None
+
+
+def host_library():
+    """Loads libolc_amd.so, the C++ registration boundary and operator adapter."""
+    global _host
+    if _host is None:
+        if not HOST_LIB_PATH.exists():
+            raise RuntimeError(f"{HOST_LIB_PATH} is not built; run __graft_entry__.build()")
+        library()  # libmnb.so first: libolc_amd.so links against it
+        H = ctypes.CDLL(str(HOST_LIB_PATH))
+        H.olc_amd_last_error.restype = ctypes.c_char_p
+        for name in ("olc_amd_register_all_kernels", "olc_amd_register_matmul_nbits_kernel"):
+            getattr(H, name).restype = ctypes.c_int
+        H.olc_amd_register_pass.argtypes = [ctypes.c_char_p]
+        H.olc_amd_register_pass.restype = ctypes.c_int
+        for name in ("olc_amd_registered_kernels", "olc_amd_used_kernel_names",
+                     "olc_amd_dispatch_keys"):
+            getattr(H, name).argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+            getattr(H, name).restype = ctypes.c_size_t
+        H.olc_amd_set_usage_recording.argtypes = [ctypes.c_int]
+        vp, i64p, i32p = ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32)
+        H.olc_amd_run_node.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.POINTER(ctypes.c_char_p), i64p, ctypes.c_int,
+                                       ctypes.POINTER(vp), i32p, i32p, i32p, i64p, vp,
+                                       ctypes.c_int64, vp]
+        H.olc_amd_run_node.restype = ctypes.c_int
+        _host = H
+    return _host
+
+
+def _host_string(fn):
+    n = fn(None, 0)
+    buf = ctypes.create_string_buffer(n)
+    fn(buf, n)
+    return buf.value.decode()
+
+
+def _host_check(rc):
+    if rc != 0:
+        raise ValueError(host_library().olc_amd_last_error().decode())
+
+
+def register_kernels():
+    """Installs this library's kernels into the dispatch table (RegisterAllKernels)."""
+    _host_check(host_library().olc_amd_register_all_kernels())
+
+
+def register_pass(op_types):
+    """One registration pass over the listed operators; duplicates raise ValueError."""
+    _host_check(host_library().olc_amd_register_pass(",".join(op_types).encode()))
+
+
+def registered_kernels():
+    """Inventory of registrations (CollectRegisteredKernels), without installing anything."""
+    out = []
+    for line in _host_string(host_library().olc_amd_registered_kernels).splitlines():
+        domain, op, device, name, types, since, until = line.split("\t")
+        out.append({"domain": domain, "op_type": op, "device": int(device), "kernel_name": name,
+                    "types": [int(t) for t in types.split(",") if t],
+                    "since_version": None if since == "-1" else int(since),
+                    "until_version": None if until == "-1" else int(until)})
+    return out
+
+
+def dispatch_keys():
+    return _host_string(host_library().olc_amd_dispatch_keys).splitlines()
+
+
+def used_kernel_names():
+    return _host_string(host_library().olc_amd_used_kernel_names).splitlines()
+
+
+def clear_used_kernel_names():
+    host_library().olc_amd_clear_used_kernel_names()
+
+
+def set_kernel_usage_recording(enabled: bool):
+    host_library().olc_amd_set_usage_recording(int(bool(enabled)))
+
+
+DEVICE_CPU, DEVICE_GPU = 1, 2
+DTYPE_FLOAT, DTYPE_UINT8 = 1, 2
+
+
+def run_node(domain, op_type, attrs, inputs, out, stream=None, device=DEVICE_GPU):
+    """Runs one node through the dispatch table, as onnx-light's RunNode would.
+
+    inputs: list of (pointer or None, dtype, device, shape) tuples; out: a
+    contiguous float32 torch tensor receiving Y.
+    """
+    H = host_library()
+    names = (ctypes.c_char_p * len(attrs))(*[k.encode() for k in attrs])
+    vals = (ctypes.c_int64 * len(attrs))(*attrs.values())
+    n = len(inputs)
+    ptrs = (ctypes.c_void_p * n)(*[None if p is None else p for p, _, _, _ in inputs])
+    types = (ctypes.c_int32 * n)(*[t for _, t, _, _ in inputs])
+    devs = (ctypes.c_int32 * n)(*[d for _, _, d, _ in inputs])
+    ranks = (ctypes.c_int32 * n)(*[len(s) for _, _, _, s in inputs])
+    flat = [d for _, _, _, s in inputs for d in s]
+    dims = (ctypes.c_int64 * max(1, len(flat)))(*flat)
+    s = None if stream is None else ctypes.c_void_p(stream)
+    _host_check(H.olc_amd_run_node(domain.encode(), op_type.encode(), device, len(attrs), names,
+                                   vals, n, ptrs, types, devs, ranks, dims,
+                                   None if out is None else ctypes.c_void_p(out.data_ptr()),
+                                   0 if out is None else out.numel(), s))
+    return out

@@ -6,6 +6,7 @@
 #include "kernel_registration.h"
 #include "register_kernels.h"
 
+#include <algorithm>
 #include <cstring>
 #include <exception>
 #include <sstream>
@@ -52,6 +53,27 @@ int olc_amd_register_all_kernels(void) {
 
 int olc_amd_register_matmul_nbits_kernel(void) {
   return Guard([] { RegisterMatMulNBitsKernel(); });
+}
+
+// Runs one registration pass that registers the listed operators
+// (comma-separated op_type names) in order, as RegisterAllKernels does for the
+// full list; a repeated name fails the pass with the duplicate error.
+int olc_amd_register_pass(const char *op_types) {
+  return Guard([&] {
+    KernelRegistrationScope scope;
+    std::string list = op_types ? op_types : "";
+    size_t pos = 0;
+    while (pos <= list.size()) {
+      const size_t end = std::min(list.find(',', pos), list.size());
+      const std::string op = list.substr(pos, end - pos);
+      if (op == "MatMulNBits")
+        RegisterMatMulNBitsKernel();
+      else if (!op.empty())
+        throw std::invalid_argument("onnx_light_cpu_amd::RegisterKernel: unknown operator '" +
+                                    op + "'");
+      pos = end + 1;
+    }
+  });
 }
 
 // One line per registration: domain, op_type, device, kernel_name, types
@@ -104,8 +126,9 @@ int olc_amd_run_node(const char *domain, const char *op_type, int device, int n_
     NodeKernelFn fn = LookupKernel(domain ? domain : "", op_type ? op_type : "",
                                    static_cast<Device>(device));
     if (!fn)
-      throw std::invalid_argument(std::string("onnx_light_cpu_amd::RunNode: no kernel for '") +
-                                  (domain ? domain : "") + ":" + (op_type ? op_type : "") + "'");
+      throw std::invalid_argument("onnx_light_cpu_amd::RunNode: no kernel for '" +
+                                  NormaliseDomain(domain ? domain : "") + ":" +
+                                  (op_type ? op_type : "") + "'");
     NodeAttributes attrs;
     for (int i = 0; i < n_attrs; ++i) attrs.ints[attr_names[i]] = attr_values[i];
     RuntimeContext rt;
