@@ -35,6 +35,14 @@ FP16_PEAK_TFLOPS = 2500.0
 METRIC = "MatMulNBits 4-bit: M=1 achieved HBM GB/s; M=2048 TFLOP/s; % roofline"
 ROTATION_BYTES = 1 << 30
 
+# HBM bytes per launch of the headline kernel (GemvM1Kernel on c2 M=1), from
+# two rocprofv3 --pmc passes over `bench.py --only decode,gemm,copy --eager
+# --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15449.6 KiB and WRITE_SIZE
+# 56.0 KiB per dispatch, each scaled by what the same counter reads for the copy
+# leg's 512 MiB device copy (FETCH_SIZE 262157.1 KiB -> x1.99990, WRITE_SIZE
+# 524288.0 KiB -> x1.00000). Re-measure when the kernel changes.
+GEMV_M1_C2_TRAFFIC_BYTES = round((15449.6 * (524288.0 / 262157.1) + 56.0) * 1024)
+
 
 def parse_args():
     ap = argparse.ArgumentParser()
@@ -43,7 +51,11 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline sampling budget (0 disables)")
-    ap.add_argument("--only", default="", help="comma list of legs: decode,gemm,sweep,cpu")
+    ap.add_argument("--only", default="",
+                    help="comma list of legs: decode,gemm,sweep,cpu,copy (default: all but copy)")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every step directly instead of replaying a HIP graph "
+                         "(for counter collection, which serialises dispatches)")
     return ap.parse_args()
 
 
@@ -63,17 +75,30 @@ def make_device_weights(torch, p, copies, seed, dev):
     return sets
 
 
+EAGER = False
+
+
 def time_graph(torch, launches, steps, warmup, stream):
-    """Captures `launches` (a callable issuing one step) into a graph, replays it.
-    Returns (ms per step from events on `stream`, wall seconds of the timed region)."""
+    """Captures `launches` (a callable issuing one step) into a graph, replays it
+    (or, with --eager, calls it directly). Returns (ms per step from events on
+    `stream`, wall seconds of the timed region)."""
     with torch.cuda.stream(stream):
-        launches()  # eager warmup outside capture
+        launches()  # eager warmup outside capture; allocates any workspace
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        launches()
-    for _ in range(warmup):
-        graph.replay()
+    if EAGER:
+        def step():
+            with torch.cuda.stream(stream):
+                launches()
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            launches()
+        step = graph.replay
+    # graph.replay() launches on the current stream: keep `stream` current so
+    # the events bracket the replays.
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -81,11 +106,26 @@ def time_graph(torch, launches, steps, warmup, stream):
     with torch.cuda.stream(stream):
         start.record(stream)
         for _ in range(steps):
-            graph.replay()
+            step()
         end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return start.elapsed_time(end) / steps, wall
+
+
+def copy_leg(torch, dev, steps, warmup, stream):
+    """A plain device-to-device copy of 512 MiB: the calibration that HBM
+    counters (FETCH_SIZE, WRITE_SIZE) are scaled by, and a streaming ceiling."""
+    n = 512 << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+
+    def launches():
+        dst.copy_(src)
+
+    ms, wall = time_graph(torch, launches, steps, warmup, stream)
+    return {"bytes_read": n, "bytes_written": n, "us_per_launch": ms * 1e3,
+            "GBps": 2 * n / (ms * 1e-3) / 1e9, "wall_s": wall}
 
 
 def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
@@ -115,6 +155,7 @@ def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
         "zero_points": p.has_zero_points, "path": path, "rotation_copies": rot,
         "us_per_launch": per_launch_us, "bytes_per_launch": nbytes,
         "GBps": nbytes / (per_launch_us * 1e-6) / 1e9, "ms_per_step": ms, "wall_s": wall,
+        "wall_ms_per_step": wall * 1e3 / steps,
         "launches_per_step": rot,
     }
 
@@ -135,7 +176,8 @@ def gemm_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
     tflops = flops / (ms * 1e-3) / 1e12
     res = {"K": p.K, "N": p.N, "M": M, "block_size": p.block_size, "path": op.select_path(M),
            "us_per_launch": ms * 1e3, "TFLOPs": tflops, "frac_fp16_peak": tflops / FP16_PEAK_TFLOPS,
-           "bytes_per_launch": p.algorithmic_bytes(M), "wall_s": wall}
+           "bytes_per_launch": p.algorithmic_bytes(M), "wall_s": wall,
+           "wall_ms_per_step": wall * 1e3 / steps}
     op.release()
     return res
 
@@ -177,7 +219,9 @@ def cpu_leg(pkg, budget_s):
 
 
 def main():
+    global EAGER
     args = parse_args()
+    EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
               "supported (the decode GEMV would shard column-parallel over N, see DESIGN.md)",
@@ -216,6 +260,11 @@ def main():
                 sweep.append({k: r[k] for k in ("config", "M", "us_per_launch", "GBps", "path")})
                 print(f"# decode {cname} M={M}: {r['us_per_launch']:.2f} us, {r['GBps']:.0f} GB/s",
                       file=sys.stderr, flush=True)
+    copy = None
+    if "copy" in legs:
+        copy = copy_leg(torch, dev, args.steps, args.warmup, stream)
+        print(f"# copy 512 MiB: {copy['us_per_launch']:.1f} us, {copy['GBps']:.0f} GB/s",
+              file=sys.stderr, flush=True)
     cpu = None
     if "cpu" in legs and args.cpu_seconds > 0:
         cpu = cpu_leg(pkg, args.cpu_seconds)
@@ -226,8 +275,10 @@ def main():
         value = head["GBps"]
         ms_per_step = head["ms_per_step"]
         roof = {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": head["GBps"] / HBM_PEAK_GBS, "traffic": None,
-                "kernel": "GemvKernel (c2 M=1)", "us_per_launch": head["us_per_launch"],
+                "frac": head["GBps"] / HBM_PEAK_GBS, "traffic": GEMV_M1_C2_TRAFFIC_BYTES,
+                "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                "copy-calibrated)",
+                "kernel": "GemvM1Kernel (c2 M=1)", "us_per_launch": head["us_per_launch"],
                 "bytes_per_launch": head["bytes_per_launch"]}
         workload = ("c2: MatMulNBits M=1 K=4096 N=14336 bits=4 block_size=128 zero_points; "
                     f"{head['rotation_copies']} rotated weight copies per step")
@@ -244,6 +295,8 @@ def main():
         "cpu_baseline": cpu,
         "prefill_gemm": gemm,
         "decode_sweep": sweep,
+        "copy_calibration": copy,
+        "timing": "eager launches" if EAGER else "HIP graph replay",
         "bench_wall_s": time.perf_counter() - t_start,
     }
     print(json.dumps(out), flush=True)

@@ -81,7 +81,9 @@ int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float 
 /* Releases the plan and the device memory it owns. NULL is accepted. */
 int mnb_plan_destroy(mnb_plan *plan);
 
-/* Device workspace mnb_run needs for M rows (0 when none). */
+/* Device workspace (16-byte aligned) that mnb_run and mnb_run_path need for M
+ * rows, whichever path serves them (0 when none). Only the prefill GEMM uses
+ * it: A rounded to fp16 in its tile layout, ceil(M/128)*128*K*2 bytes. */
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
 
 /* Y = MatMulNBits(A, plan) for M rows; dA and dY are device pointers on the

@@ -124,6 +124,7 @@ class MatMulNBits:
         self.desc = MnbDesc(K, N, bits, block_size, accuracy_level, 0)
         self._plan = ctypes.c_void_p()
         self._keep = ()
+        self._work = None
 
     # -- constants ---------------------------------------------------------
     def prepare(self, B, scales, zero_points=None):
@@ -201,10 +202,27 @@ class MatMulNBits:
         if not out.is_contiguous() or out.numel() != M * self.desc.N:
             raise ValueError(f"{KERNEL_PREFIX}: out must be contiguous [..., M, N]")
         s = stream if stream is not None else torch.cuda.current_stream(A.device)
-        _check(library().mnb_run_path(self._plan, M, _dev_ptr(A2), _dev_ptr(out), None, 0,
+        work = self.workspace(M, A.device, path)
+        _check(library().mnb_run_path(self._plan, M, _dev_ptr(A2), _dev_ptr(out),
+                                      _dev_ptr(work), 0 if work is None else work.numel(),
                                       ctypes.c_void_p(s.cuda_stream), path),
                "run")
         return out
+
+    def workspace_bytes(self, M: int) -> int:
+        n = ctypes.c_size_t()
+        _check(library().mnb_workspace_bytes(self._plan, M, ctypes.byref(n)), "workspace_bytes")
+        return n.value
+
+    def workspace(self, M: int, device, path: int = PATH_AUTO):
+        """Device workspace for M rows, kept and grown across calls (not during capture)."""
+        import torch
+        need = self.workspace_bytes(M) if path in (PATH_AUTO, PATH_GEMM) else 0
+        if need == 0:
+            return None
+        if self._work is None or self._work.numel() < need or self._work.device != device:
+            self._work = torch.empty(need, dtype=torch.uint8, device=device)
+        return self._work
 
     run = __call__
 

@@ -233,8 +233,10 @@ int mnb_plan_destroy(mnb_plan *plan) {
 
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
   if (plan == nullptr || bytes == nullptr) return MNB_ERR_NULL_POINTER;
-  if (M < 0) return MNB_ERR_BAD_SHAPE;
-  *bytes = 0;
+  if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
+  // Only the prefill GEMM uses a workspace (A rounded to fp16, tile layout);
+  // the size covers every path mnb_run_path may be asked to take for M rows.
+  *bytes = (M > 0 && mnb::GemmSupports(plan->view, M)) ? mnb::GemmWorkspaceBytes(plan->view, M) : 0;
   return MNB_OK;
 }
 
@@ -255,8 +257,6 @@ int mnb_select_path(const mnb_plan *plan, int64_t M, int *path) {
 
 int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
                  size_t workspace_bytes, void *stream, int path) {
-  (void)dWorkspace;
-  (void)workspace_bytes;
   if (plan == nullptr) return MNB_ERR_NULL_POINTER;
   if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
   if (M == 0) return MNB_OK;
@@ -267,6 +267,12 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
   if (path == 1 && !(a_aligned && M <= 16 && mnb::GemvSupports(plan->view, M)))
     return MNB_ERR_UNSUPPORTED;
   if (path == 2 && !(a_aligned && mnb::GemmSupports(plan->view, M))) return MNB_ERR_UNSUPPORTED;
+  if (path == 2) {
+    const size_t need = mnb::GemmWorkspaceBytes(plan->view, M);
+    if (dWorkspace == nullptr || workspace_bytes < need ||
+        (reinterpret_cast<uintptr_t>(dWorkspace) % 16) != 0)
+      return MNB_ERR_WORKSPACE;
+  }
 
   int cur = -1;
   hipError_t e = hipGetDevice(&cur);
@@ -283,7 +289,7 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
                                 plan->view.K <= 4096 ? 4 * plan->view.num_cus : plan->view.num_cus, 2)
             : mnb::LaunchGemv(plan->view, M, dA, dY, s);
     break;
-  case 2: e = mnb::LaunchGemm(plan->view, M, dA, dY, s); break;
+  case 2: e = mnb::LaunchGemm(plan->view, M, dA, dY, dWorkspace, s); break;
   default: e = mnb::LaunchGeneric(plan->view, M, dA, dY, s); break;
   }
   if (e != hipSuccess) {

@@ -1,178 +1,347 @@
 // Prefill GEMM for MatMulNBits on CDNA4 fp16 MFMA (the roadmap's `int4_gemm`,
 // docs/next_steps/2026/2026_08_qwen3_inference.rst:223-225).
 //
-// Y[M, N] = A[M, K] * W[N, K]^T with W dequantized from 4-bit blocks.
+// Y[M, N] = A[M, K] * W[N, K]^T with W dequantized from 4-bit blocks; fp16
+// operands, fp32 accumulation. Two kernels per call:
 //
-// Tiling. A workgroup of 256 threads (4 wavefronts, 2 x 2) owns a 128 x 128
-// output tile and walks K in steps of 32. Per step:
-//   - A (fp32 in HBM) is loaded with 128-bit loads, rounded to fp16 (round to
-//     nearest even, as onnx_light_cpu/impl/math/half_conversion.h:42-78) and
-//     stored to LDS as [128][32] fp16;
-//   - B's packed nibbles for the tile's 128 rows are loaded (8 bytes per
-//     thread), dequantized in fp32 as (q - zp) * scale, rounded once to fp16
-//     and stored to LDS as [128][32];
-//   - each wavefront runs 4 x 4 v_mfma_f32_16x16x32_f16 on its 64 x 64
-//     sub-tile, accumulating in fp32.
-// LDS rows are padded to 40 halves (80 bytes): the 16 lanes that read one
-// 16-byte k-group of 16 consecutive rows then touch 16 disjoint 4-bank groups.
+// 1. ConvertAKernel rounds A to fp16 once (round to nearest even, as
+//    onnx_light_cpu/impl/math/half_conversion.h:42-78) into the caller's
+//    workspace, already laid out as the LDS image of each 128 x 64 A tile
+//    (tile-major, rows swizzled as below, rows past M zero). Rounding A once
+//    instead of once per N tile removes that work from the GEMM and halves the
+//    A bytes it streams.
+//
+// 2. GemmKernel: one workgroup (256 threads, 4 wavefronts as 2 x 2) owns a
+//    128 x 128 output tile; each wavefront a 64 x 64 sub-tile = 4 x 4
+//    v_mfma_f32_16x16x32_f16 tiles. K advances in k-tiles of 64. 80 KiB of LDS
+//    per workgroup lets two workgroups share a CU, so one hides the other's
+//    barrier and dequantization stalls.
+//    - A tiles (16 KiB) go global -> LDS directly (global_load_lds_dwordx4,
+//      no registers) through a 3-stage ring, two k-tiles ahead.
+//    - B tiles: each thread loads 32 nibbles of one weight row two k-tiles
+//      ahead into registers. A masked word (w >> 4i) & 0x000F000F | 0x64006400
+//      holds two fp16 values 1024 + q exactly; one packed add of -(1024 + zp)
+//      makes q - zp exact and one packed multiply by the block's fp16 scale
+//      gives the weight; the dequantized tile goes to a double-buffered LDS
+//      tile while the current k-tile is multiplied.
+//    - One barrier per k-tile.
+//    Inside every group of 8 k the LDS order is [0,4,1,5,2,6,3,7] for both A
+//    and B (the order the masked words produce); the contraction is unchanged.
+//    LDS rows are 64 fp16 = 8 units of 16 B; unit u of row r is stored at
+//    r * 8 + (u ^ ((r >> 1) & 7)), so the 16 lanes of an MFMA fragment read
+//    (16 consecutive rows, one unit) hit 16 distinct 16-byte bank groups.
+//    Tile order is XCD-aware: workgroup b runs on XCD b % 8; when the M tiles
+//    split evenly over the 8 XCDs, XCD x gets a contiguous band of M tiles with
+//    all their N tiles, so each XCD's L2 holds one slab of A.
 #include "mnb_kernels.h"
 
 namespace mnb {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 128;
 constexpr int kBN = 128;
-constexpr int kBK = 32;
-constexpr int kLdsStride = kBK + 8;  // halves
+constexpr int kBK = 64;
+constexpr int kUnits = kBK / 8;             // 16-byte units per LDS row
+constexpr int kAUnits = kBM * kUnits;       // units per A tile (16 KiB)
+constexpr int kBUnits = kBN * kUnits;       // units per B tile (16 KiB)
+constexpr int kAStages = 3;
+constexpr size_t kLdsBytes = (kAStages * kAUnits + 2 * kBUnits) * 16;  // 80 KiB
+
+__device__ __forceinline__ int Swz(int row, int unit) {
+  return row * kUnits + (unit ^ ((row >> 1) & 7));
+}
+
+__device__ __forceinline__ uint32_t PackHalf2(float lo, float hi) {
+  const half2v h = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+__device__ __forceinline__ uint32_t PkAddF16(uint32_t a, uint32_t b) {
+  const half2v r = __builtin_bit_cast(half2v, a) + __builtin_bit_cast(half2v, b);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ uint32_t PkMulF16(uint32_t a, uint32_t b) {
+  const half2v r = __builtin_bit_cast(half2v, a) * __builtin_bit_cast(half2v, b);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// One packed word of 8 nibbles (k order) -> 8 fp16 weights in [0,4,1,5,2,6,3,7] order.
+__device__ __forceinline__ uint4 DequantWord(uint32_t w, uint32_t neg_offset, uint32_t scale2) {
+  uint32_t t[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    t[i] = PkMulF16(PkAddF16(((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u, neg_offset), scale2);
+  return make_uint4(t[0], t[1], t[2], t[3]);
+}
+
+// One thread per 16-byte LDS unit of the converted A: 8 consecutive fp32 of a
+// row -> 8 fp16 in [0,4,1,5,2,6,3,7] order, written where GemmKernel's direct
+// copy expects it. Rows >= M are written as zeros.
+__global__ __launch_bounds__(256) void ConvertAKernel(const float *__restrict__ A,
+                                                      uint4 *__restrict__ Ah, int M, int K,
+                                                      int64_t total_units) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (g >= total_units) return;
+  const int units_per_row = K / 8;
+  const int64_t row = g / units_per_row;
+  const int ku = static_cast<int>(g - row * units_per_row);  // unit index along K
+  uint4 out = make_uint4(0u, 0u, 0u, 0u);
+  if (row < M) {
+    const float4 *src = reinterpret_cast<const float4 *>(A + row * K + 8 * ku);
+    const float4 x = src[0], y = src[1];
+    out = make_uint4(PackHalf2(x.x, y.x), PackHalf2(x.y, y.y), PackHalf2(x.z, y.z),
+                     PackHalf2(x.w, y.w));
+  }
+  const int ktiles = K / kBK;
+  const int64_t mt = row / kBM;
+  const int r = static_cast<int>(row - mt * kBM);
+  const int kt = ku / kUnits, u = ku % kUnits;
+  Ah[(mt * ktiles + kt) * kAUnits + Swz(r, u)] = out;
+}
+
+// s_waitcnt vmcnt(N) with the other counters left free (gfx9 encoding: vmcnt
+// in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void WaitVm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// One k-tile of B for this thread: 32 nibbles of one weight row (one
+// quantization block, block_size >= 32), its scale and zero point.
+struct BRegs {
+  uint4 b;
+  float s;
+  uint32_t z;
+};
 
 template <bool HAS_ZP>
-__global__ __launch_bounds__(256) void GemmKernel(const float *__restrict__ A,
-                                                  const uint8_t *__restrict__ B,
-                                                  const float *__restrict__ S,
-                                                  const uint8_t *__restrict__ Z,
-                                                  float *__restrict__ Y, int M, int K, int N,
-                                                  int nb, int log2_bs, int row_bytes,
-                                                  int zp_row_bytes) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[kBM * kLdsStride];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[kBN * kLdsStride];
+__global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ Ah,
+                                                     const uint8_t *__restrict__ B,
+                                                     const float *__restrict__ S,
+                                                     const uint8_t *__restrict__ Z,
+                                                     float *__restrict__ Y, int M, int K, int N,
+                                                     int nb, int log2_bs, int row_bytes,
+                                                     int zp_row_bytes) {
+  extern __shared__ uint4 lds[];
+  uint4 *Astage = lds;                        // [kAStages][kAUnits]
+  uint4 *Bbuf = lds + kAStages * kAUnits;     // [2][kBUnits]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave >> 1;
   const int wn = wave & 1;
-  const int m0 = blockIdx.y * kBM;
-  const int n0 = blockIdx.x * kBN;
 
-  floatx4 acc[4][4];
+  // XCD-aware tile order.
+  const int tiles_m = (M + kBM - 1) / kBM;
+  const int tiles_n = (N + kBN - 1) / kBN;
+  int tm, tn;
+  {
+    const int b = blockIdx.x;
+    if (tiles_m % 8 == 0 && gridDim.x == static_cast<unsigned>(tiles_m * tiles_n)) {
+      const int xcd = b & 7, local = b >> 3;
+      const int band = tiles_m / 8;
+      tm = xcd * band + local / tiles_n;
+      tn = local % tiles_n;
+    } else {
+      tm = b / tiles_n;
+      tn = b % tiles_n;
+    }
+  }
+  const int m0 = tm * kBM;
+  const int n0 = tn * kBN;
+  const int ktiles = K / kBK;
+
+  // B resources based at this tile's first weight row; rows past N read as
+  // zero and their outputs are never stored.
+  const int rows_b = min(kBN, N - n0);
+  const auto rb_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(B + static_cast<size_t>(n0) * row_bytes), 0, rows_b * row_bytes,
+      0x00020000);
+  const auto rs_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(S + static_cast<size_t>(n0) * nb), 0, rows_b * nb * 4, 0x00020000);
+  const auto rz_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(HAS_ZP ? Z + static_cast<size_t>(n0) * zp_row_bytes : B), 0,
+      HAS_ZP ? rows_b * zp_row_bytes : 0, 0x00020000);
+
+  // A: converted tile (tm, kt) is kAUnits contiguous units; instruction i of
+  // wavefront w copies units i*256 + w*64 + lane to the same LDS offsets.
+  const uint4 *a_tiles = Ah + static_cast<size_t>(tm) * ktiles * kAUnits;
+  auto issue_a = [&](int kt, int stage) {
+    const uint4 *src = a_tiles + static_cast<size_t>(kt) * kAUnits;
+    uint4 *dst = Astage + stage * kAUnits;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kAUnits / 256; ++i) {
+      const int c = i * 256 + wave * 64;  // wave-uniform; the lane offset is implicit
+      __builtin_amdgcn_global_load_lds(
+          static_cast<const void *>(src + c + lane),
+          reinterpret_cast<__attribute__((address_space(3))) void *>(
+              static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst + c))),
+          16, 0, 0);
+    }
+  };
+
+  // B: thread t -> weight row t >> 1, 32 nibbles at k offset 32 * (t & 1).
+  const int b_row = tid >> 1;
+  const int b_half = tid & 1;
+  auto load_b = [&](BRegs &r, int kt) {
+    const int kk = kt * kBK + 32 * b_half;
+    r.b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                        rb_rsrc, b_row * row_bytes + (kk >> 1), 0, 0));
+    const int blk = kk >> log2_bs;
+    r.s = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(rs_rsrc, (b_row * nb + blk) * 4, 0, 0));
+    if (HAS_ZP) {
+      const uint32_t zb =
+          __builtin_amdgcn_raw_buffer_load_b8(rz_rsrc, b_row * zp_row_bytes + (blk >> 1), 0, 0);
+      r.z = (zb >> ((blk & 1) * 4)) & 0xFu;
+    } else {
+      r.z = 8u;
+    }
+  };
+  auto store_b = [&](const BRegs &r, int buf) {
+    const uint32_t words[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    const float zf = static_cast<float>(r.z);
+    const uint32_t neg = PackHalf2(-(1024.f + zf), -(1024.f + zf));
+    const uint32_t sc = PackHalf2(r.s, r.s);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      Bbuf[buf * kBUnits + Swz(b_row, 4 * b_half + u)] = DequantWord(words[u], neg, sc);
+  };
+
+  constexpr int kMI = kBM / 32;  // 16-row MFMA tiles per wavefront along M
+  floatx4 acc[kMI][4];
+#pragma unroll
+  for (int i = 0; i < kMI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // B loader assignment: row tid/2, 16 nibbles at k offset 16*(tid&1).
-  const int b_row = tid >> 1;
-  const int b_half = tid & 1;
-  const int b_gn = n0 + b_row;
-  const bool b_valid = b_gn < N;
-  const uint8_t *b_ptr = B + static_cast<size_t>(b_valid ? b_gn : 0) * row_bytes;
-  const float *s_ptr = S + static_cast<size_t>(b_valid ? b_gn : 0) * nb;
-  const uint8_t *z_ptr = HAS_ZP ? Z + static_cast<size_t>(b_valid ? b_gn : 0) * zp_row_bytes
-                                : nullptr;
-
-  for (int k0 = 0; k0 < K; k0 += kBK) {
-    // ---- A: 128 x 32 fp32 -> fp16, four float4 per thread ----
+  auto mma_tile = [&](int stage, int buf) {
+    const uint4 *as = Astage + stage * kAUnits;
+    const uint4 *bs = Bbuf + buf * kBUnits;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i;
-      const int row = idx >> 3;
-      const int c4 = idx & 7;
-      const int gm = m0 + row;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (gm < M)
-        v = *reinterpret_cast<const float4 *>(A + static_cast<size_t>(gm) * K + k0 + 4 * c4);
-      half4 h = {static_cast<_Float16>(v.x), static_cast<_Float16>(v.y),
-                 static_cast<_Float16>(v.z), static_cast<_Float16>(v.w)};
-      *reinterpret_cast<half4 *>(&As[row * kLdsStride + 4 * c4]) = h;
-    }
-    // ---- B: 16 nibbles per thread -> fp16 ----
-    {
-      const int kk = k0 + 16 * b_half;
-      half8 h0, h1;
-      if (b_valid) {
-        const uint2 raw = *reinterpret_cast<const uint2 *>(b_ptr + (kk >> 1));
-        const int blk = kk >> log2_bs;
-        const float sc = s_ptr[blk];
-        const float zf =
-            HAS_ZP ? static_cast<float>((z_ptr[blk >> 1] >> ((blk & 1) * 4)) & 0xF) : 8.f;
-        const uint32_t words[2] = {raw.x, raw.y};
-        _Float16 w[16];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const uint32_t byte = (words[t] >> (8 * b)) & 0xFFu;
-            w[8 * t + 2 * b] = static_cast<_Float16>((static_cast<float>(byte & 0xFu) - zf) * sc);
-            w[8 * t + 2 * b + 1] = static_cast<_Float16>((static_cast<float>(byte >> 4) - zf) * sc);
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          h0[e] = w[e];
-          h1[e] = w[8 + e];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          h0[e] = static_cast<_Float16>(0.f);
-          h1[e] = static_cast<_Float16>(0.f);
-        }
-      }
-      *reinterpret_cast<half8 *>(&Bs[b_row * kLdsStride + 16 * b_half]) = h0;
-      *reinterpret_cast<half8 *>(&Bs[b_row * kLdsStride + 16 * b_half + 8]) = h1;
-    }
-    __syncthreads();
-
-    half8 af[4], bf[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      af[i] = *reinterpret_cast<const half8 *>(
-          &As[(wm * 64 + i * 16 + (lane & 15)) * kLdsStride + 8 * (lane >> 4)]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      bf[j] = *reinterpret_cast<const half8 *>(
-          &Bs[(wn * 64 + j * 16 + (lane & 15)) * kLdsStride + 8 * (lane >> 4)]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int ks = 0; ks < 2; ++ks) {
+      const int unit = 4 * ks + (lane >> 4);
+      half8 bf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        bf[j] = __builtin_bit_cast(half8, bs[Swz(wn * 64 + j * 16 + (lane & 15), unit)]);
+#pragma unroll
+      for (int i = 0; i < kMI; ++i) {
+        const half8 af =
+            __builtin_bit_cast(half8, as[Swz(wm * (kBM / 2) + i * 16 + (lane & 15), unit)]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // Prologue: A tiles 0 and 1 in flight to stages 0 and 1, B tiles 0 and 1 in
+  // registers; B tile 0 dequantized into buffer 0.
+  BRegs rb0, rb1;
+  issue_a(0, 0);
+  load_b(rb0, 0);
+  if (ktiles > 1) {
+    issue_a(1, 1);
+    load_b(rb1, 1);
+  }
+  store_b(rb0, 0);
+
+  // Iteration kt: after the wait and barrier, A tile kt (stage kt % 3) and B
+  // buffer kt % 2 are complete and visible, and every read of stage
+  // (kt+2) % 3 and of buffer (kt+1) % 2 from iteration kt-1 is retired. Then
+  // A and B of tile kt+2 are issued, tile kt is multiplied, and B tile kt+1
+  // (loaded one iteration earlier) is dequantized into the other buffer.
+  // Unrolled by two so the B register sets are static.
+  // Vector memory operations issued per k-tile and thread: 8 direct A copies
+  // and the B loads. Waiting until at most one k-tile's worth is outstanding
+  // completes tile kt and leaves tile kt+1 in flight.
+  constexpr int kOpsPerTile = kAUnits / 256 + 2 + (HAS_ZP ? 1 : 0);
+  for (int kt = 0; kt < ktiles; kt += 2) {
+    // even step: rb1 holds tile kt+1, rb0 is free
+    if (kt + 1 < ktiles)
+      WaitVm<kOpsPerTile>();
+    else
+      WaitVm<0>();
     __syncthreads();
+    if (kt + 2 < ktiles) {
+      issue_a(kt + 2, (kt + 2) % kAStages);
+      load_b(rb0, kt + 2);
+    }
+    mma_tile(kt % kAStages, 0);
+    if (kt + 1 >= ktiles) break;
+    store_b(rb1, 1);
+    // odd step: rb0 holds tile kt+2, rb1 is free
+    if (kt + 2 < ktiles)
+      WaitVm<kOpsPerTile>();
+    else
+      WaitVm<0>();
+    __syncthreads();
+    if (kt + 3 < ktiles) {
+      issue_a(kt + 3, (kt + 3) % kAStages);
+      load_b(rb1, kt + 3);
+    }
+    mma_tile((kt + 1) % kAStages, 1);
+    if (kt + 2 < ktiles) store_b(rb0, 0);
   }
 
   // Output: lane holds column (lane & 15), rows 4*(lane >> 4) + v of each 16 x 16 tile.
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kMI; ++i) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int gm = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + v;
+        const int gm = m0 + wm * (kBM / 2) + i * 16 + 4 * (lane >> 4) + v;
         if (gm < M && gn < N) Y[static_cast<size_t>(gm) * N + gn] = acc[i][j][v];
       }
     }
   }
 }
 
-} // namespace
-
-bool GemmSupports(const WeightView &w, int64_t M) {
-  return M >= 1 && M <= (int64_t{1} << 22) && (w.K % 32) == 0 && w.block_size >= 16 &&
-         w.K <= (int64_t{1} << 30) && w.N <= (int64_t{1} << 30) &&
-         w.row_bytes <= (int64_t{1} << 30) && (w.row_bytes % 8) == 0 &&
-         (reinterpret_cast<uintptr_t>(w.B) % 8) == 0;
+template <bool HAS_ZP>
+hipError_t LaunchT(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, hipStream_t s) {
+  const int tiles = static_cast<int>(((M + kBM - 1) / kBM) * ((w.N + kBN - 1) / kBN));
+  hipLaunchKernelGGL((GemmKernel<HAS_ZP>), dim3(tiles), dim3(256), kLdsBytes, s, Ah, w.B,
+                     w.scales, w.zp, Y, static_cast<int>(M), static_cast<int>(w.K),
+                     static_cast<int>(w.N), static_cast<int>(w.nb), w.log2_bs,
+                     static_cast<int>(w.row_bytes), static_cast<int>(w.zp_row_bytes));
+  return hipGetLastError();
 }
 
-hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>((w.N + kBN - 1) / kBN),
-                  static_cast<unsigned>((M + kBM - 1) / kBM));
-  if (w.zp) {
-    hipLaunchKernelGGL(GemmKernel<true>, grid, dim3(256), 0, s, A, w.B, w.scales, w.zp, Y,
-                       static_cast<int>(M), static_cast<int>(w.K), static_cast<int>(w.N),
-                       static_cast<int>(w.nb), w.log2_bs, static_cast<int>(w.row_bytes),
-                       static_cast<int>(w.zp_row_bytes));
-  } else {
-    hipLaunchKernelGGL(GemmKernel<false>, grid, dim3(256), 0, s, A, w.B, w.scales, w.zp, Y,
-                       static_cast<int>(M), static_cast<int>(w.K), static_cast<int>(w.N),
-                       static_cast<int>(w.nb), w.log2_bs, static_cast<int>(w.row_bytes),
-                       static_cast<int>(w.zp_row_bytes));
-  }
-  return hipGetLastError();
+} // namespace
+
+size_t GemmWorkspaceBytes(const WeightView &w, int64_t M) {
+  const int64_t mpad = (M + kBM - 1) / kBM * kBM;
+  return static_cast<size_t>(mpad) * static_cast<size_t>(w.K) * 2;
+}
+
+bool GemmSupports(const WeightView &w, int64_t M) {
+  // Buffer offsets are 32-bit within one tile of 128 weight rows.
+  const int64_t tiles = ((M + kBM - 1) / kBM) * ((w.N + kBN - 1) / kBN);
+  return M >= 1 && (w.K % kBK) == 0 && w.block_size >= 32 && tiles < (int64_t{1} << 31) &&
+         int64_t{kBN} * w.row_bytes < (int64_t{1} << 31) &&
+         int64_t{kBN} * w.nb * 4 < (int64_t{1} << 31) && (w.row_bytes % 16) == 0 &&
+         (reinterpret_cast<uintptr_t>(w.B) % 16) == 0 && M <= (int64_t{1} << 30) &&
+         w.N <= (int64_t{1} << 30) && w.K <= (int64_t{1} << 24);
+}
+
+hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                      hipStream_t s) {
+  uint4 *Ah = static_cast<uint4 *>(work);
+  const int64_t units = (M + kBM - 1) / kBM * kBM * (w.K / 8);
+  hipLaunchKernelGGL(ConvertAKernel, dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256),
+                     0, s, A, Ah, static_cast<int>(M), static_cast<int>(w.K), units);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return w.zp != nullptr ? LaunchT<true>(w, M, Ah, Y, s) : LaunchT<false>(w, M, Ah, Y, s);
 }
 
 } // namespace mnb

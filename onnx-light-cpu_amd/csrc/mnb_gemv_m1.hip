@@ -141,8 +141,8 @@ __device__ __forceinline__ void LoadBatch(Batch<CPL, R, FULL, HAS_ZP> &bt, const
       const int c = lane + 64 * i;
       if (FULL || c < nchunks) {
         const int blk = c >> chunk_shift;
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs.b, c * 16, row * row_bytes, 0);
-        bt.w[r][i] = make_uint4(v[0], v[1], v[2], v[3]);
+        bt.w[r][i] =
+            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.b, c * 16, row * row_bytes, 0));
         bt.s[r][i] = __builtin_bit_cast(
             float, __builtin_amdgcn_raw_buffer_load_b32(rs.s, blk * 4, row * nb * 4, 0));
         if (HAS_ZP)

@@ -33,9 +33,12 @@ hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream
                         int workgroups, int rows_per_batch);
 bool GemvM1Supports(const WeightView &w);
 
-// Prefill GEMM on fp16 MFMA, any M, K % 32 == 0.
-hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s);
+// Prefill GEMM on fp16 MFMA, any M, K % 64 == 0, block_size >= 32. `work`
+// holds GemmWorkspaceBytes(w, M) bytes of device memory (A rounded to fp16).
+hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                      hipStream_t s);
 bool GemmSupports(const WeightView &w, int64_t M);
+size_t GemmWorkspaceBytes(const WeightView &w, int64_t M);
 
 // Generic fallback: any K, any block_size, any M. Slow; for odd shapes and
 // cross-checks.

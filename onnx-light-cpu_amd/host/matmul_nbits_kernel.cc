@@ -2,6 +2,8 @@
 
 #include "register_kernels.h"
 
+#include <hip/hip_runtime_api.h>
+
 #include <stdexcept>
 #include <string>
 
@@ -48,6 +50,22 @@ MatMulNBitsKernel::MatMulNBitsKernel(const NodeAttributes &attrs) {
 
 MatMulNBitsKernel::~MatMulNBitsKernel() {
   if (plan_ != nullptr) mnb_plan_destroy(plan_);
+  if (work_ != nullptr) (void)hipFree(work_);
+}
+
+void *MatMulNBitsKernel::Workspace(int64_t M) {
+  size_t need = 0;
+  CheckStatus(mnb_workspace_bytes(plan_, M, &need), "mnb_workspace_bytes");
+  if (need == 0) return nullptr;
+  std::lock_guard<std::mutex> lock(mu_);
+  if (need > work_bytes_) {
+    if (work_ != nullptr) (void)hipFree(work_);
+    work_ = nullptr;
+    work_bytes_ = 0;
+    if (hipMalloc(&work_, need) != hipSuccess) Fail("workspace allocation failed");
+    work_bytes_ = need;
+  }
+  return work_;
 }
 
 void MatMulNBitsKernel::EnsurePlan(const TensorView &b, const TensorView &scales,
@@ -102,8 +120,9 @@ void MatMulNBitsKernel::operator()(const TensorView &a, const TensorView &b,
          " bytes");
   EnsurePlan(b, scales, zero_points);
   const int64_t M = a.numel() / K;
+  void *work = Workspace(M);
   CheckStatus(mnb_run(plan_, M, static_cast<const float *>(a.data), static_cast<float *>(y.data),
-                      nullptr, 0, stream),
+                      work, work_bytes_, stream),
               "mnb_run");
 }
 

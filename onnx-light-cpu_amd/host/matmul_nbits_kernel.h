@@ -37,8 +37,12 @@ public:
 private:
   void EnsurePlan(const TensorView &b, const TensorView &scales, const TensorView *zero_points);
 
+  void *Workspace(int64_t M);
+
   mnb_desc desc_{};
   std::mutex mu_;
+  void *work_ = nullptr;   // device workspace of the prefill path, grown on demand
+  size_t work_bytes_ = 0;
   mnb_plan *plan_ = nullptr;
   const void *plan_b_ = nullptr;
   const void *plan_s_ = nullptr;

@@ -202,3 +202,38 @@ def test_prepare_device_borrows(pkg, orc, cuda):
     Y = op(torch.from_numpy(A).to(cuda)).cpu().numpy()
     assert orc.normwise_max_error(Y, orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)) <= GEMV_TOL
     op.release()
+
+
+def test_gemm_workspace_contract(pkg, cuda):
+    """mnb_workspace_bytes is ceil(M/128)*128*K*2 for the GEMM; path 2 refuses
+    a missing, short or misaligned workspace with MNB_ERR_WORKSPACE before any
+    launch, and a reused larger workspace gives the same bits."""
+    import ctypes
+    import torch
+    K, N, bs = 512, 256, 64
+    p, B, S, Z = _case(pkg, K, N, bs, True, seed=31)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    for M in (1, 16, 17, 128, 129, 300):
+        assert op.workspace_bytes(M) == -(-M // 128) * 128 * K * 2
+    assert op.workspace_bytes(0) == 0
+    M = 200
+    print(f"case workspace K={K} N={N} bs={bs} M={M} path=2", flush=True)
+    A = torch.from_numpy(pkg.workloads.make_activations(M, K, 1.0, seed=32)).to(cuda)
+    Y = torch.empty(M, N, device=cuda)
+    need = op.workspace_bytes(M)
+    L = pkg.library()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    work = torch.empty(need + 64, dtype=torch.uint8, device=cuda)
+    for ptr, size in ((None, 0), (work.data_ptr(), need - 16), (work.data_ptr() + 8, need)):
+        rc = L.mnb_run_path(op._plan, M, ctypes.c_void_p(A.data_ptr()),
+                            ctypes.c_void_p(Y.data_ptr()), ctypes.c_void_p(ptr), size, stream, 2)
+        assert rc == 5  # MNB_ERR_WORKSPACE
+    ref = op(A, path=2).cpu()
+    big = torch.empty(4 * need, dtype=torch.uint8, device=cuda)
+    big.fill_(0xFF)  # stale contents must not leak into the result
+    rc = L.mnb_run_path(op._plan, M, ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(Y.data_ptr()),
+                        ctypes.c_void_p(big.data_ptr()), big.numel(), stream, 2)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(Y.cpu(), ref)
+    op.release()
