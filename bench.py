@@ -37,11 +37,11 @@ ROTATION_BYTES = 1 << 30
 
 # HBM bytes per launch of the headline kernel (GemvM1Kernel on c2 M=1), from
 # two rocprofv3 --pmc passes over `bench.py --only decode,gemm,copy --eager
-# --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15449.6 KiB and WRITE_SIZE
-# 56.0 KiB per dispatch, each scaled by what the same counter reads for the copy
-# leg's 512 MiB device copy (FETCH_SIZE 262157.1 KiB -> x1.99990, WRITE_SIZE
-# 524288.0 KiB -> x1.00000). Re-measure when the kernel changes.
-GEMV_M1_C2_TRAFFIC_BYTES = round((15449.6 * (524288.0 / 262157.1) + 56.0) * 1024)
+# --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15525.7 KiB and WRITE_SIZE
+# 80.0 KiB per dispatch, each scaled by what the same counter reads for the
+# copy leg's 512 MiB device copy (FETCH_SIZE 262156.7 KiB -> x1.99990,
+# WRITE_SIZE 524288.0 KiB -> x1.00000). Re-measure when the kernel changes.
+GEMV_M1_C2_TRAFFIC_BYTES = round((15525.7 * (524288.0 / 262156.7) + 80.0) * 1024)
 
 
 def parse_args():

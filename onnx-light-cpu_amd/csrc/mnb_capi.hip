@@ -285,8 +285,7 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
   switch (path) {
   case 1:
     e = (M == 1 && mnb::GemvM1Supports(plan->view))
-            ? mnb::LaunchGemvM1(plan->view, dA, dY, s,
-                                plan->view.K <= 4096 ? 4 * plan->view.num_cus : plan->view.num_cus, 2)
+            ? mnb::LaunchGemvM1(plan->view, dA, dY, s, 0, 0)
             : mnb::LaunchGemv(plan->view, M, dA, dY, s);
     break;
   case 2: e = mnb::LaunchGemm(plan->view, M, dA, dY, dWorkspace, s); break;

@@ -4,66 +4,112 @@
 // (docs/next_steps/2026/2026_08_qwen3_inference.rst:208-218): fp32
 // accumulation, weights never expanded, each weight byte streamed once.
 //
-// Mapping. The grid is persistent (a few workgroups per CU). Each wavefront
-// takes batches of R consecutive weight rows, batch b = g, g + TW, ... (g its
-// global index, TW the number of wavefronts), so at any moment the chip
-// streams a contiguous band of rows. Lane l takes the 16-byte chunks
-// c = l + 64 i (i < CPL) of each row: every load instruction of the wave reads
-// 1 KiB of one row, coalesced. Loads are buffer loads whose row offset is a
-// wave-uniform SGPR, so no per-row vector address arithmetic is spent. The
-// next batch's chunks, scales and zero points are loaded while the current
-// batch is computed. A chunk holds 32 nibbles k = 32c .. 32c+31, all in one
+// Mapping. A workgroup owns a band of G consecutive weight rows; wavefront w
+// owns band rows [w R, w R + R). Short rows (K <= 4096) use several 4-wave
+// workgroups per CU, long rows one workgroup of up to 16 wavefronts per CU
+// (see PickShape). Lane l takes the 16-byte chunks c = l + 64 i (i < CPL) of
+// each row, so every load instruction of a wavefront reads 1 KiB of one row,
+// coalesced. A chunk holds 32 nibbles k = 32c .. 32c+31, all in one
 // quantization block (block_size >= 32).
 //
-// Activations. A is staged once per workgroup in LDS (8 float4 per chunk, the
-// float4 index XOR-swizzled by (c & 7) so that the lanes of a half-wave spread
-// over the banks), with the per-chunk sums asum = sum_j a_j. All staging loads
-// are issued before the first LDS store (one memory round trip). The R rows
-// of a batch share each chunk's LDS read.
+// Order of work, chosen so that neither HBM nor the arithmetic waits on the
+// other:
+//  1. the workgroup issues its staging loads: A, and each wavefront the scale
+//     and zero point of every (row, block) of its rows;
+//  2. every wavefront issues the non-temporal buffer loads of all its rows'
+//     weights at once (row offsets are wave-uniform SGPRs);
+//  3. the staged values go to LDS as they return (loads complete in issue
+//     order, so this never waits behind the weights): A as swizzled float4
+//     chunks with the per-chunk sums asum = sum_j a_j, and the pairs
+//     (scale * 2^24, zp * 2^-24), so the inner loop does no small global
+//     loads;
+//  4. one barrier, then each wavefront computes its rows as their weights
+//     arrive and reduces them across lanes.
+// When the grid is one workgroup per CU, more than half of the LDS is
+// requested so that the dispatcher places exactly one on each CU.
 //
 // Arithmetic. v_fma_mix_f32 multiplies an fp32 activation by an fp16 operand
-// taken straight from one half of a register. Masking a packed word with
-// 0x000F000F leaves two nibbles q in the two halves, i.e. the fp16 subnormals
-// q * 2^-24, exact. So per chunk the lane forms
-//   dot  = sum_j a_j * q_j * 2^-24          (products exact, fp32 sums)
-//   y   += scale * (dot * 2^24 - zp * asum)
-// at seven bit operations per eight nibbles plus one FMA per nibble, with no
-// per-nibble conversion or zero-point subtraction. This relies on fp16
-// subnormal inputs being kept (the gfx950 HIP default FP16 denormal mode);
-// the parity tests would see every product vanish otherwise.
+// taken straight from one half of a register. A packed word w holds nibbles
+// 0..7 (k order); masking w and w >> 8 with 0x000F000F and 0x00F000F0 leaves
+// two nibbles per mask in the two halves as the exact fp16 subnormals
+// q * 2^-24 (bits 0-3 of a half) or q * 2^-20 (bits 4-7). The LDS copy of A
+// holds a_j / 16 at odd j (exact), so every product is a_j q_j 2^-24 and per
+// chunk
+//   d  = sum_j a_j q_j 2^-24
+//   y += (scale 2^24) * (d - (zp 2^-24) * asum)
+// costs five bit operations per eight nibbles plus one FMA per nibble, with
+// no per-nibble conversion or zero-point subtraction; products are exact.
+// This relies on fp16 subnormal inputs being kept (the gfx950 HIP default
+// FP16 denormal mode); the parity tests would see every product vanish
+// otherwise.
 //
 // Reduction per row: 4 DPP steps give every lane its 16-lane row sum, 4
-// readlanes add the rows in a fixed order; lane r stores row r of the batch.
+// readlanes add the rows in a fixed order; lane r stores row r of the wave.
 #include "mnb_kernels.h"
+
+#include <algorithm>
 
 namespace mnb {
 namespace m1 {
+
+constexpr int kMaxWaves = 16;             // 1024 threads per workgroup
+constexpr size_t kLdsLimit = 150 * 1024;  // of the 160 KiB per CU
+constexpr size_t kOnePerCu = 81 * 1024;   // more than half: one workgroup per CU
+constexpr uint32_t kNonTemporal = 2;      // buffer-load cache policy: NT
+constexpr int kAPasses = 4;               // A float4 per thread staged ahead of the weights
+constexpr int kPPasses = 2;               // (scale, zp) work items per thread ahead of the weights
 
 // acc += a * f16(lo half of h), accumulator tied to the destination.
 __device__ __forceinline__ void MixLo(float &acc, float a, uint32_t h) {
   __asm__("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(a), "v"(h));
 }
-
 // acc += a * f16(hi half of h)
 __device__ __forceinline__ void MixHi(float &acc, float a, uint32_t h) {
   __asm__("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
           : "+v"(acc)
           : "v"(a), "v"(h));
 }
+// a * f16(lo half of h), a fresh accumulator
+__device__ __forceinline__ float MixLo0(float a, uint32_t h) {
+  float r;
+  __asm__("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h));
+  return r;
+}
+// a * f16(hi half of h), a fresh accumulator
+__device__ __forceinline__ float MixHi0(float a, uint32_t h) {
+  float r;
+  __asm__("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h));
+  return r;
+}
 
-// d0/d1 += sum_j a[j] * q_j * 2^-24 over the 32 nibbles of one chunk, k order.
-__device__ __forceinline__ void DotChunk(const float *a, const uint4 &w4, float &d0, float &d1) {
+// sum_j a'[j] * f16-subnormal masks of one chunk = sum_j a_j q_j 2^-24, where
+// a' holds a_j / 16 at odd j (k order inside the chunk).
+__device__ __forceinline__ float DotChunk(const float *a, const uint4 &w4) {
   const uint32_t words[4] = {w4.x, w4.y, w4.z, w4.w};
+  float lo = 0.f, hi = 0.f;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const uint32_t w = words[t];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t h = (w >> (4 * i)) & 0x000F000Fu;  // nibbles i (lo half) and i+4 (hi half)
-      MixLo(d0, a[8 * t + i], h);
-      MixHi(d1, a[8 * t + i + 4], h);
+    const uint32_t w8 = w >> 8;
+    const uint32_t h0 = w & 0x000F000Fu;   // nibbles 0 | 4, as q * 2^-24
+    const uint32_t h1 = w & 0x00F000F0u;   // nibbles 1 | 5, as q * 2^-20
+    const uint32_t h2 = w8 & 0x000F000Fu;  // nibbles 2 | 6, as q * 2^-24
+    const uint32_t h3 = w8 & 0x00F000F0u;  // nibbles 3 | 7, as q * 2^-20
+    if (t == 0) {
+      lo = MixLo0(a[0], h0);
+      hi = MixHi0(a[4], h0);
+    } else {
+      MixLo(lo, a[8 * t + 0], h0);
+      MixHi(hi, a[8 * t + 4], h0);
     }
+    MixLo(lo, a[8 * t + 1], h1);
+    MixHi(hi, a[8 * t + 5], h1);
+    MixLo(lo, a[8 * t + 2], h2);
+    MixHi(hi, a[8 * t + 6], h2);
+    MixLo(lo, a[8 * t + 3], h3);
+    MixHi(hi, a[8 * t + 7], h3);
   }
+  return lo + hi;
 }
 
 template <int CTRL>
@@ -85,198 +131,337 @@ __device__ __forceinline__ float WaveTotal(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
-// Copies A[0 .. 32*nchunks) into LDS as swizzled float4 chunks and writes the
-// per-chunk sums. A 256-thread workgroup moves 256 float4 per pass; CPL * 2
-// passes cover nchunks <= 64 * CPL chunks. Loads are all issued before the
-// first store, so staging costs one memory round trip.
-template <int CPL>
-__device__ __forceinline__ void StageA(const float *__restrict__ A, float4 *lds4,
-                                       float *asum_lds, int nchunks) {
-  constexpr int kPasses = CPL * 2;  // 64*CPL chunks * 8 float4 / 256 threads
-  const float4 *src = reinterpret_cast<const float4 *>(A);
-  const int total = nchunks * 8;
-  float4 t[kPasses];
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int f = threadIdx.x + 256 * p;
-    t[p] = f < total ? src[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int f = threadIdx.x + 256 * p;
-    const int c = f >> 3, v = f & 7;
-    if (f < total) lds4[c * 8 + (v ^ (c & 7))] = t[p];
-    float s = (t[p].x + t[p].y) + (t[p].z + t[p].w);
-    s = DppAdd<0xB1>(s);   // quad_perm [1,0,3,2]
-    s = DppAdd<0x4E>(s);   // quad_perm [2,3,0,1]
-    s = DppAdd<0x141>(s);  // row_half_mirror: every lane holds its 8-lane sum
-    if (v == 0 && f < total) asum_lds[c] = s;
-  }
-  __syncthreads();
+// LDS layout of one workgroup: A as nchunks * 8 swizzled float4 plus one
+// spare float4, the chunk sums plus one spare float, then per wavefront its
+// R * nb pairs (scale, zp), row-major, plus 4 spare pairs. Staging lanes with
+// nothing to store write to the spares, so the staging code has no branches
+// (a branch between a load and its use lets the compiler sink the load below
+// the weight loads). A wavefront writes and reads only its own pairs: LDS
+// operations of one wavefront execute in order, so the pairs need no
+// workgroup barrier and the barrier waits only for A.
+__host__ __device__ inline size_t AsumOffsetF4(int nchunks) { return static_cast<size_t>(nchunks) * 8 + 1; }
+__host__ __device__ inline size_t PairsOffsetF2(int nchunks) {
+  return (AsumOffsetF4(nchunks) * 16 + (static_cast<size_t>(nchunks) + 1) * 4 + 7) / 8;
+}
+inline size_t LdsBytes(int nchunks, int wave_rows, int64_t nb) {
+  return (PairsOffsetF2(nchunks) + static_cast<size_t>(wave_rows) * nb + 4) * 8;
 }
 
-// R rows x CPL chunks of weights with their scales and zero-point bytes.
-template <int CPL, int R, bool FULL, bool HAS_ZP>
-struct Batch {
-  uint4 w[R][CPL];
-  float s[R][CPL];
-  uint32_t z[R][CPL];
-};
+// q = j / nb and r = j % nb for 0 <= j < 2^16 through the fp32 reciprocal
+// (error below one, corrected once).
+__device__ __forceinline__ int DivNb(int j, int nb, float rnb, int &r) {
+  int q = static_cast<int>(static_cast<float>(j) * rnb);
+  r = j - q * nb;
+  if (r >= nb) { ++q; r -= nb; }
+  if (r < 0) { --q; r += nb; }
+  return q;
+}
 
-struct Rsrc {
-  __amdgpu_buffer_rsrc_t b, s, z;
-};
+// One work item of a wavefront's (scale, zp) staging: PW consecutive pairs of
+// one of its rows (PW = 4 needs nb % 4 == 0: one 16-byte scale load, one
+// 2-byte zero-point load). Pair j = PW * item of the wavefront, row-major
+// [wave row][block]; rows past the band re-read the band's last row.
+template <int PW, bool HAS_ZP>
+struct PairItem {
+  float s[PW];
+  uint32_t z;
+  int j, shift;
 
-// Buffer loads: the row offset is wave-uniform (SGPR), the lane offset is a
-// per-lane constant, so no per-row vector address arithmetic is needed.
-template <int CPL, int R, bool FULL, bool HAS_ZP>
-__device__ __forceinline__ void LoadBatch(Batch<CPL, R, FULL, HAS_ZP> &bt, const Rsrc &rs,
-                                          int row0, int N, int lane, int nchunks, int nb,
-                                          int chunk_shift, int row_bytes, int zp_row_bytes) {
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = __builtin_amdgcn_readfirstlane(min(row0 + r, N - 1));
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = lane + 64 * i;
-      if (FULL || c < nchunks) {
-        const int blk = c >> chunk_shift;
-        bt.w[r][i] =
-            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs.b, c * 16, row * row_bytes, 0));
-        bt.s[r][i] = __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(rs.s, blk * 4, row * nb * 4, 0));
-        if (HAS_ZP)
-          bt.z[r][i] = __builtin_amdgcn_raw_buffer_load_b8(rs.z, blk >> 1, row * zp_row_bytes, 0);
+  // Loads are unconditional (item clamped to the last one) so that no branch
+  // forces the compiler to wait for them early; Store skips clamped items.
+  __device__ __forceinline__ void Load(int item, int nitems, int nb, float rnb, int wrow0,
+                                       int last_row, int zp_row_bytes,
+                                       __amdgpu_buffer_rsrc_t rsc, __amdgpu_buffer_rsrc_t rz) {
+    j = item < nitems ? item * PW : -1;
+    const int jl = min(item, nitems - 1) * PW;
+    int blk;
+    const int row = min(wrow0 + DivNb(jl, nb, rnb, blk), last_row);
+    if (PW == 4) {
+      const float4 v = __builtin_bit_cast(
+          float4, __builtin_amdgcn_raw_buffer_load_b128(rsc, (row * nb + blk) * 4, 0, 0));
+      s[0] = v.x;
+      s[1 % PW] = v.y;
+      s[2 % PW] = v.z;
+      s[3 % PW] = v.w;
+    } else {
+      s[0] = __builtin_bit_cast(float,
+                                __builtin_amdgcn_raw_buffer_load_b32(rsc, (row * nb + blk) * 4, 0, 0));
+    }
+    z = 0x8888u;
+    shift = 0;
+    if (HAS_ZP) {
+      const int off = row * zp_row_bytes + (blk >> 1);
+      if (PW == 4) {
+        z = __builtin_amdgcn_raw_buffer_load_b16(rz, off, 0, 0);
+      } else {
+        z = __builtin_amdgcn_raw_buffer_load_b8(rz, off, 0, 0);
+        shift = (blk & 1) * 4;
       }
     }
   }
+
+  // spare: index of the 4 spare pairs
+  __device__ __forceinline__ void Store(float2 *pairs, int spare) const {
+    const int base = j >= 0 ? j : spare;
+#pragma unroll
+    for (int u = 0; u < PW; ++u) {
+      const uint32_t zp = (z >> (shift + 4 * u)) & 0xFu;
+      pairs[base + u] = make_float2(s[u] * 16777216.f, static_cast<float>(zp) * 5.9604644775390625e-8f);
+    }
+  }
+};
+
+// A float4 f of the chunk layout: stored swizzled, odd k divided by 16, the
+// 8-lane DPP sum of the original values gives the chunk sum. total is a
+// multiple of 8, so the 8 lanes of a chunk are all valid or all clamped;
+// clamped lanes write to the spare slots.
+__device__ __forceinline__ void StoreA(float4 *lds4, float *asum_lds, int nchunks, int f, int total,
+                                       float4 t) {
+  const int c = f >> 3, v = f & 7;
+  const bool valid = f < total;
+  float sum = (t.x + t.y) + (t.z + t.w);
+  sum = DppAdd<0xB1>(sum);   // quad_perm [1,0,3,2]
+  sum = DppAdd<0x4E>(sum);   // quad_perm [2,3,0,1]
+  sum = DppAdd<0x141>(sum);  // row_half_mirror: every lane holds its 8-lane sum
+  t.y *= 0.0625f;
+  t.w *= 0.0625f;
+  lds4[valid ? c * 8 + (v ^ (c & 7)) : nchunks * 8] = t;
+  asum_lds[valid && v == 0 ? c : nchunks] = sum;
 }
 
-template <int CPL, int R, bool FULL, bool HAS_ZP>
-__global__ __launch_bounds__(256) void GemvM1Kernel(const float *__restrict__ A,
-                                                    const uint8_t *__restrict__ B,
-                                                    const float *__restrict__ S,
-                                                    const uint8_t *__restrict__ Z,
-                                                    float *__restrict__ Y, int K, int N, int nb,
-                                                    int chunk_shift, int row_bytes,
-                                                    int zp_row_bytes) {
+template <int CPL, int R, bool FULL, bool HAS_ZP, int PW>
+__global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A,
+                                                     const uint8_t *__restrict__ B,
+                                                     const float *__restrict__ S,
+                                                     const uint8_t *__restrict__ Z,
+                                                     float *__restrict__ Y, int K, int N, int nb,
+                                                     int chunk_shift, int row_bytes,
+                                                     int zp_row_bytes, int G) {
   extern __shared__ float4 lds4[];
   const int nchunks = K >> 5;
-  const int lane = threadIdx.x & 63;
-  const int TW = gridDim.x * (blockDim.x >> 6);
-  const int nbatches = (N + R - 1) / R;
-  int bi = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int tid = threadIdx.x, nthreads = blockDim.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
+  const int row0 = blockIdx.x * G;    // first row of the band
+  const int rows = min(G, N - row0);  // rows in the band
+  const int wr0 = wave * R;           // first band row of this wavefront
 
-  Rsrc rs;
-  rs.b = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(B), 0, 0x7FFFFFFF, 0x00020000);
-  rs.s = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(S), 0, 0x7FFFFFFF, 0x00020000);
-  rs.z = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(HAS_ZP ? Z : B), 0, 0x7FFFFFFF,
-                                           0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(B), 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(S), 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(HAS_ZP ? Z : B), 0, 0x7FFFFFFF, 0x00020000);
 
-  // 1. the first batch goes in flight before anything else
-  Batch<CPL, R, FULL, HAS_ZP> cur;
-  if (bi < nbatches)
-    LoadBatch(cur, rs, bi * R, N, lane, nchunks, nb, chunk_shift, row_bytes, zp_row_bytes);
+  float *asum_lds = reinterpret_cast<float *>(lds4 + AsumOffsetF4(nchunks));
+  float2 *pair_lds = reinterpret_cast<float2 *>(lds4) + PairsOffsetF2(nchunks);
+  float2 *wpairs = pair_lds + wr0 * nb;  // this wavefront's pairs
+  const int spare = blockDim.x / 64 * R * nb;
+  const float4 *src = reinterpret_cast<const float4 *>(A);
+  const int total = nchunks * 8;      // float4 of A
+  const int nitems = R * nb / PW;     // (scale, zp) work items of this wavefront
+  const int last_row = row0 + rows - 1;
+  const float rnb = 1.0f / static_cast<float>(nb);
 
-  // 2. stage A once per workgroup: all global loads first (one round trip),
-  //    then swizzled LDS stores; the 8 float4 of a chunk sit in 8 consecutive
-  //    lanes, so the chunk sum is an 8-lane DPP reduction.
-  float *asum_lds = reinterpret_cast<float *>(lds4 + nchunks * 8);
-  StageA<CPL>(A, lds4, asum_lds, nchunks);
-  float asum[CPL];
+  // 1. the first staging loads (A, scales, zero points) go out first: loads
+  //    complete in issue order, so staging never waits behind the weights.
+  // All loads below are unconditional with clamped addresses: a branch
+  // around a load makes the compiler wait for it at the join.
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, 0x7FFFFFFF, 0x00020000);
+  float4 ta[kAPasses];
+#pragma unroll
+  for (int p = 0; p < kAPasses; ++p)
+    ta[p] = __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(ra, min(nthreads * p + tid, total - 1) * 16, 0, 0));
+  PairItem<PW, HAS_ZP> pi[kPPasses];
+#pragma unroll
+  for (int q = 0; q < kPPasses; ++q)
+    pi[q].Load(64 * q + lane, nitems, nb, rnb, row0 + wr0, last_row, zp_row_bytes, rsc, rz);
+
+  // Keep the issue order: the scheduler must not sink the staging loads below
+  // the weight loads (completion is in issue order).
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. then all weights of this wavefront's rows (rows past the band re-read
+  //    the band's last row; their results are not stored)
+  uint4 w[R][CPL];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = __builtin_amdgcn_readfirstlane(row0 + min(wr0 + r, rows - 1));
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = FULL ? lane + 64 * i : min(lane + 64 * i, nchunks - 1);
+      w[r][i] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, c * 16, row * row_bytes, kNonTemporal));
+    }
+  }
+
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. LDS stores of A; further passes (long K) load and store behind the
+  //    weights.
+#pragma unroll
+  for (int p = 0; p < kAPasses; ++p) StoreA(lds4, asum_lds, nchunks, nthreads * p + tid, total, ta[p]);
+  for (int f0 = nthreads * kAPasses; f0 < total; f0 += nthreads) {
+    const int f = f0 + tid;
+    StoreA(lds4, asum_lds, nchunks, f, total, src[min(f, total - 1)]);
+  }
+  __syncthreads();
+
+  // The wavefront's own pairs: stored after the barrier, which therefore
+  // never waits for the (cold) scales.
+#pragma unroll
+  for (int q = 0; q < kPPasses; ++q) pi[q].Store(wpairs, spare - wr0 * nb);
+  for (int i0 = 64 * kPPasses; i0 < nitems; i0 += 64) {
+    PairItem<PW, HAS_ZP> it;
+    it.Load(i0 + lane, nitems, nb, rnb, row0 + wr0, last_row, zp_row_bytes, rsc, rz);
+    it.Store(wpairs, spare - wr0 * nb);
+  }
+
+  // 4. dot products of this wavefront's rows. LDS addresses are a per-lane
+  //    base plus compile-time offsets: chunk c = lane + 64 i sits 8192 i bytes
+  //    after chunk lane, and its swizzle (c & 7) == (lane & 7).
+  const float4 *ab = lds4 + lane * 8;
+  const int sw = lane & 7;
+  const float2 *pr = wpairs;
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = lane + 64 * i;
-    asum[i] = (FULL || c < nchunks) ? asum_lds[c] : 0.f;
-  }
-
-  // 3. batches bi, bi + TW, ...: prefetch the next batch, compute this one
-  for (; bi < nbatches; bi += TW) {
-    Batch<CPL, R, FULL, HAS_ZP> nxt;
-    const int bn = bi + TW;
-    if (bn < nbatches)
-      LoadBatch(nxt, rs, bn * R, N, lane, nchunks, nb, chunk_shift, row_bytes, zp_row_bytes);
-
-    float acc[R];
+    if (FULL || c < nchunks) {
+      float a[32];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+      for (int v = 0; v < 8; ++v) {
+        const float4 t = ab[512 * i + (v ^ sw)];
+        a[4 * v] = t.x;
+        a[4 * v + 1] = t.y;
+        a[4 * v + 2] = t.z;
+        a[4 * v + 3] = t.w;
+      }
+      const float asum = asum_lds[c];
+      const int blk = c >> chunk_shift;
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = lane + 64 * i;
-      if (FULL || c < nchunks) {
-        float a[32];
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const float4 t = lds4[c * 8 + (v ^ (c & 7))];
-          a[4 * v] = t.x;
-          a[4 * v + 1] = t.y;
-          a[4 * v + 2] = t.z;
-          a[4 * v + 3] = t.w;
-        }
-        const int blk = c >> chunk_shift;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          float d0 = 0.f, d1 = 0.f;
-          DotChunk(a, cur.w[r][i], d0, d1);
-          const float zf =
-              HAS_ZP ? static_cast<float>((cur.z[r][i] >> ((blk & 1) * 4)) & 0xFu) : 8.f;
-          acc[r] = fmaf(cur.s[r][i], fmaf(d0 + d1, 16777216.f, -zf * asum[i]), acc[r]);
+      for (int r = 0; r < R; ++r) {
+        if (wr0 + r < rows) {  // wave-uniform
+          const float d = DotChunk(a, w[r][i]);
+          const float2 sz = pr[r * nb + blk];
+          acc[r] = fmaf(sz.x, fmaf(-sz.y, asum, d), acc[r]);
         }
       }
     }
-    float mine = 0.f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float t = WaveTotal(acc[r]);
-      mine = lane == r ? t : mine;
-    }
-    const int n = bi * R + lane;
-    if (lane < R && n < N) Y[n] = mine;
-    cur = nxt;
   }
+
+  // 5. one total per row; lane r stores row r
+  float mine = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float t = WaveTotal(acc[r]);
+    mine = lane == r ? t : mine;
+  }
+  if (lane < R && wr0 + lane < rows) Y[row0 + wr0 + lane] = mine;
 }
 
-template <int CPL, int R, bool FULL, bool HAS_ZP>
-hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s, int wgs) {
+struct Shape {
+  int G, R, waves, grid;
+  size_t lds;
+};
+
+// Band rows per workgroup G and rows per wavefront R (a power of two), from
+// measured sweeps on MI355X:
+//  - short rows (CPL <= 2): workgroups of at most 4 wavefronts x 4 rows, k
+//    workgroups per CU with k = ceil(rows per CU / 16), so that every CU gets
+//    the same number of rows and several independent workgroups (one
+//    workgroup's staging and barrier overlap another's arithmetic);
+//  - long rows: one workgroup of up to 16 wavefronts per CU owning the CU's
+//    whole band (A, up to 64 KiB, is staged once per CU).
+// Both keep the LDS within kLdsLimit, shrinking G (more rounds) if needed.
+inline int RMax(int cpl) { return cpl <= 2 ? 8 : (cpl <= 4 ? 4 : 2); }
+
+inline Shape PickShape(const WeightView &w, int cpl, int G, int R) {
   const int nchunks = static_cast<int>(w.K / 32);
-  const size_t lds = static_cast<size_t>(nchunks) * (8 * sizeof(float4) + sizeof(float));
-  // Equalise batches per wavefront over the persistent grid.
-  const int64_t nbatches = (w.N + R - 1) / R;
-  const int64_t max_waves = static_cast<int64_t>(wgs) * 4;
-  const int64_t per_wave = (nbatches + max_waves - 1) / max_waves;
-  const int64_t waves = (nbatches + per_wave - 1) / per_wave;
-  const int64_t blocks = (waves + 3) / 4;
-  hipLaunchKernelGGL((GemvM1Kernel<CPL, R, FULL, HAS_ZP>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(256), lds, s, A, w.B, w.scales, w.zp, Y, static_cast<int>(w.K),
-                     static_cast<int>(w.N), static_cast<int>(w.nb), w.log2_bs - 5,
-                     static_cast<int>(w.row_bytes), static_cast<int>(w.zp_row_bytes));
+  const int rows_per_cu = static_cast<int>((w.N + w.num_cus - 1) / w.num_cus);
+  Shape sh{};
+  if (G <= 0) {
+    if (cpl <= 2) {
+      const int k = (rows_per_cu + 15) / 16;
+      G = (rows_per_cu + k - 1) / k;
+      if (R <= 0) R = G > 8 ? 4 : (G > 4 ? 2 : 1);
+    } else {
+      G = std::min(rows_per_cu, kMaxWaves * RMax(cpl));
+    }
+    while (G > 1 && LdsBytes(nchunks, G + kMaxWaves, w.nb) > kLdsLimit) G = (G + 1) / 2;
+  }
+  if (R <= 0) {
+    const int need = (G + kMaxWaves - 1) / kMaxWaves;
+    R = 1;
+    while (R < need) R *= 2;
+  }
+  sh.G = G;
+  sh.R = R;
+  sh.waves = (G + R - 1) / R;
+  sh.grid = static_cast<int>((w.N + G - 1) / G);
+  sh.lds = LdsBytes(nchunks, sh.waves * R, w.nb);
+  if (sh.grid <= w.num_cus) sh.lds = std::max(sh.lds, kOnePerCu);
+  return sh;
+}
+
+template <int CPL, int R, bool HAS_ZP>
+hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s, const Shape &sh) {
+  const bool full = (w.K / 32) == 64 * CPL;
+  const bool quads = (w.nb % 4) == 0;
+  const dim3 grid(static_cast<unsigned>(sh.grid)), block(static_cast<unsigned>(sh.waves * 64));
+  const int K = static_cast<int>(w.K), N = static_cast<int>(w.N), nb = static_cast<int>(w.nb);
+  const int cs = w.log2_bs - 5, rb = static_cast<int>(w.row_bytes);
+  const int zb = static_cast<int>(w.zp_row_bytes);
+#define MNB_M1_LAUNCH(FULLV, PWV)                                                                  \
+  hipLaunchKernelGGL((GemvM1Kernel<CPL, R, FULLV, HAS_ZP, PWV>), grid, block, sh.lds, s, A, w.B,  \
+                     w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G)
+  if (full) {
+    if (quads) MNB_M1_LAUNCH(true, 4);
+    else MNB_M1_LAUNCH(true, 1);
+  } else {
+    if (quads) MNB_M1_LAUNCH(false, 4);
+    else MNB_M1_LAUNCH(false, 1);
+  }
+#undef MNB_M1_LAUNCH
   return hipGetLastError();
 }
 
 template <int CPL, bool HAS_ZP>
-hipError_t LaunchF(const WeightView &w, const float *A, float *Y, hipStream_t s, int wgs, int R) {
-  const bool full = (w.K / 32) == 64 * CPL;
-  if (R >= 4)
-    return full ? LaunchT<CPL, 4, true, HAS_ZP>(w, A, Y, s, wgs)
-                : LaunchT<CPL, 4, false, HAS_ZP>(w, A, Y, s, wgs);
-  if (R == 2)
-    return full ? LaunchT<CPL, 2, true, HAS_ZP>(w, A, Y, s, wgs)
-                : LaunchT<CPL, 2, false, HAS_ZP>(w, A, Y, s, wgs);
-  return full ? LaunchT<CPL, 1, true, HAS_ZP>(w, A, Y, s, wgs)
-              : LaunchT<CPL, 1, false, HAS_ZP>(w, A, Y, s, wgs);
+hipError_t LaunchC(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R) {
+  const Shape sh = PickShape(w, CPL, G, R);
+  // Rows per wavefront are capped so that R * CPL weight chunks stay within
+  // 16 VGPR quads (no spills under the 1024-thread launch bound).
+  constexpr int kRMax = CPL <= 2 ? 8 : (CPL <= 4 ? 4 : 2);
+  if (sh.waves < 1 || sh.waves > kMaxWaves || sh.lds > 160 * 1024 || sh.R > kRMax)
+    return hipErrorInvalidValue;
+  switch (sh.R) {
+  case 1: return LaunchT<CPL, 1, HAS_ZP>(w, A, Y, s, sh);
+  case 2: return LaunchT<CPL, 2, HAS_ZP>(w, A, Y, s, sh);
+  case 4:
+    if constexpr (kRMax >= 4) return LaunchT<CPL, 4, HAS_ZP>(w, A, Y, s, sh);
+    return hipErrorInvalidValue;
+  case 8:
+    if constexpr (kRMax >= 8) return LaunchT<CPL, 8, HAS_ZP>(w, A, Y, s, sh);
+    return hipErrorInvalidValue;
+  default: return hipErrorInvalidValue;
+  }
 }
 
 template <bool HAS_ZP>
-hipError_t LaunchZ(const WeightView &w, const float *A, float *Y, hipStream_t s, int wgs, int R) {
+hipError_t LaunchZ(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R) {
   switch ((w.K / 32 + 63) / 64) {
-  case 1: return LaunchF<1, HAS_ZP>(w, A, Y, s, wgs, R);
-  case 2: return LaunchF<2, HAS_ZP>(w, A, Y, s, wgs, R);
-  case 3: return LaunchF<3, HAS_ZP>(w, A, Y, s, wgs, R);
-  case 4: return LaunchF<4, HAS_ZP>(w, A, Y, s, wgs, R);
-  case 5: return LaunchF<5, HAS_ZP>(w, A, Y, s, wgs, R);
-  case 6: return LaunchF<6, HAS_ZP>(w, A, Y, s, wgs, R);
-  case 7: return LaunchF<7, HAS_ZP>(w, A, Y, s, wgs, R);
-  default: return LaunchF<8, HAS_ZP>(w, A, Y, s, wgs, R);
+  case 1: return LaunchC<1, HAS_ZP>(w, A, Y, s, G, R);
+  case 2: return LaunchC<2, HAS_ZP>(w, A, Y, s, G, R);
+  case 3: return LaunchC<3, HAS_ZP>(w, A, Y, s, G, R);
+  case 4: return LaunchC<4, HAS_ZP>(w, A, Y, s, G, R);
+  case 5: return LaunchC<5, HAS_ZP>(w, A, Y, s, G, R);
+  case 6: return LaunchC<6, HAS_ZP>(w, A, Y, s, G, R);
+  case 7: return LaunchC<7, HAS_ZP>(w, A, Y, s, G, R);
+  default: return LaunchC<8, HAS_ZP>(w, A, Y, s, G, R);
   }
 }
 
@@ -284,17 +469,21 @@ hipError_t LaunchZ(const WeightView &w, const float *A, float *Y, hipStream_t s,
 
 bool GemvM1Supports(const WeightView &w) {
   // Buffer offsets are 32-bit: every byte of B, scales and zero points must
-  // be addressable below 2^31.
+  // be addressable below 2^31. K <= 16384 keeps a row within 8 chunks per
+  // lane (the largest CPL instantiated) and A within 64 KiB of LDS; the
+  // 16-byte scale loads need 16-byte aligned scales, the 2-byte zero-point
+  // loads 2-byte aligned zero points.
   return (w.K % 32) == 0 && w.K <= 16384 && w.block_size >= 32 && (w.row_bytes % 16) == 0 &&
          (reinterpret_cast<uintptr_t>(w.B) % 16) == 0 &&
+         (reinterpret_cast<uintptr_t>(w.scales) % 16) == 0 &&
+         (reinterpret_cast<uintptr_t>(w.zp) % 2) == 0 &&
          w.row_bytes * w.N < (int64_t{1} << 31) && w.nb * 4 * w.N < (int64_t{1} << 31);
 }
 
 hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
-                        int workgroups, int rows_per_batch) {
-  if (workgroups < 1) workgroups = 1;
-  return w.zp ? m1::LaunchZ<true>(w, A, Y, s, workgroups, rows_per_batch)
-              : m1::LaunchZ<false>(w, A, Y, s, workgroups, rows_per_batch);
+                        int band_rows, int rows_per_wave) {
+  return w.zp ? m1::LaunchZ<true>(w, A, Y, s, band_rows, rows_per_wave)
+              : m1::LaunchZ<false>(w, A, Y, s, band_rows, rows_per_wave);
 }
 
 } // namespace mnb

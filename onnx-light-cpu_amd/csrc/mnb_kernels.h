@@ -27,10 +27,11 @@ struct WeightView {
 hipError_t LaunchGemv(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s);
 bool GemvSupports(const WeightView &w, int64_t M);
 
-// Decode GEMV for M == 1 (fp16-subnormal mixed FMA), persistent grid of at
-// most `workgroups` workgroups of 256 threads.
+// Decode GEMV for M == 1 (fp16-subnormal mixed FMA): one workgroup per band
+// of `band_rows` weight rows, `rows_per_wave` (1, 2, 4 or 8) rows per
+// wavefront; 0 picks both from the shape and the device's CU count.
 hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
-                        int workgroups, int rows_per_batch);
+                        int band_rows, int rows_per_wave);
 bool GemvM1Supports(const WeightView &w);
 
 // Prefill GEMM on fp16 MFMA, any M, K % 64 == 0, block_size >= 32. `work`
