@@ -284,9 +284,12 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (path) {
   case 1:
-    e = (M == 1 && mnb::GemvM1Supports(plan->view))
-            ? mnb::LaunchGemvM1(plan->view, dA, dY, s, 0, 0)
-            : mnb::LaunchGemv(plan->view, M, dA, dY, s);
+    if (M == 1 && mnb::GemvM1Supports(plan->view))
+      e = mnb::LaunchGemvM1(plan->view, dA, dY, s, 0, 0);
+    else if (mnb::GemvSmallMSupports(plan->view, M))
+      e = mnb::LaunchGemvSmallM(plan->view, M, dA, dY, s);
+    else
+      e = mnb::LaunchGemv(plan->view, M, dA, dY, s);
     break;
   case 2: e = mnb::LaunchGemm(plan->view, M, dA, dY, dWorkspace, s); break;
   default: e = mnb::LaunchGeneric(plan->view, M, dA, dY, s); break;

@@ -45,42 +45,20 @@
 //
 // Reduction per row: 4 DPP steps give every lane its 16-lane row sum, 4
 // readlanes add the rows in a fixed order; lane r stores row r of the wave.
-#include "mnb_kernels.h"
+#include "mnb_decode_common.h"
 
 #include <algorithm>
 
 namespace mnb {
 namespace m1 {
 
+using namespace dec;
+
 constexpr int kMaxWaves = 16;             // 1024 threads per workgroup
 constexpr size_t kLdsLimit = 150 * 1024;  // of the 160 KiB per CU
 constexpr size_t kOnePerCu = 81 * 1024;   // more than half: one workgroup per CU
-constexpr uint32_t kNonTemporal = 2;      // buffer-load cache policy: NT
 constexpr int kAPasses = 4;               // A float4 per thread staged ahead of the weights
 constexpr int kPPasses = 2;               // (scale, zp) work items per thread ahead of the weights
-
-// acc += a * f16(lo half of h), accumulator tied to the destination.
-__device__ __forceinline__ void MixLo(float &acc, float a, uint32_t h) {
-  __asm__("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(a), "v"(h));
-}
-// acc += a * f16(hi half of h)
-__device__ __forceinline__ void MixHi(float &acc, float a, uint32_t h) {
-  __asm__("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
-          : "+v"(acc)
-          : "v"(a), "v"(h));
-}
-// a * f16(lo half of h), a fresh accumulator
-__device__ __forceinline__ float MixLo0(float a, uint32_t h) {
-  float r;
-  __asm__("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h));
-  return r;
-}
-// a * f16(hi half of h), a fresh accumulator
-__device__ __forceinline__ float MixHi0(float a, uint32_t h) {
-  float r;
-  __asm__("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h));
-  return r;
-}
 
 // sum_j a'[j] * f16-subnormal masks of one chunk = sum_j a_j q_j 2^-24, where
 // a' holds a_j / 16 at odd j (k order inside the chunk).
@@ -112,25 +90,6 @@ __device__ __forceinline__ float DotChunk(const float *a, const uint4 &w4) {
   return lo + hi;
 }
 
-template <int CTRL>
-__device__ __forceinline__ float DppAdd(float v) {
-  const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false);
-  return v + __int_as_float(moved);
-}
-
-// Sum over the 64 lanes; the result is wave-uniform.
-__device__ __forceinline__ float WaveTotal(float v) {
-  v = DppAdd<0xB1>(v);   // quad_perm [1,0,3,2]
-  v = DppAdd<0x4E>(v);   // quad_perm [2,3,0,1]
-  v = DppAdd<0x141>(v);  // row_half_mirror
-  v = DppAdd<0x140>(v);  // row_mirror: every lane holds its 16-lane row sum
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 47));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-  return (r0 + r1) + (r2 + r3);
-}
-
 // LDS layout of one workgroup: A as nchunks * 8 swizzled float4 plus one
 // spare float4, the chunk sums plus one spare float, then per wavefront its
 // R * nb pairs (scale, zp), row-major, plus 4 spare pairs. Staging lanes with
@@ -146,70 +105,6 @@ __host__ __device__ inline size_t PairsOffsetF2(int nchunks) {
 inline size_t LdsBytes(int nchunks, int wave_rows, int64_t nb) {
   return (PairsOffsetF2(nchunks) + static_cast<size_t>(wave_rows) * nb + 4) * 8;
 }
-
-// q = j / nb and r = j % nb for 0 <= j < 2^16 through the fp32 reciprocal
-// (error below one, corrected once).
-__device__ __forceinline__ int DivNb(int j, int nb, float rnb, int &r) {
-  int q = static_cast<int>(static_cast<float>(j) * rnb);
-  r = j - q * nb;
-  if (r >= nb) { ++q; r -= nb; }
-  if (r < 0) { --q; r += nb; }
-  return q;
-}
-
-// One work item of a wavefront's (scale, zp) staging: PW consecutive pairs of
-// one of its rows (PW = 4 needs nb % 4 == 0: one 16-byte scale load, one
-// 2-byte zero-point load). Pair j = PW * item of the wavefront, row-major
-// [wave row][block]; rows past the band re-read the band's last row.
-template <int PW, bool HAS_ZP>
-struct PairItem {
-  float s[PW];
-  uint32_t z;
-  int j, shift;
-
-  // Loads are unconditional (item clamped to the last one) so that no branch
-  // forces the compiler to wait for them early; Store skips clamped items.
-  __device__ __forceinline__ void Load(int item, int nitems, int nb, float rnb, int wrow0,
-                                       int last_row, int zp_row_bytes,
-                                       __amdgpu_buffer_rsrc_t rsc, __amdgpu_buffer_rsrc_t rz) {
-    j = item < nitems ? item * PW : -1;
-    const int jl = min(item, nitems - 1) * PW;
-    int blk;
-    const int row = min(wrow0 + DivNb(jl, nb, rnb, blk), last_row);
-    if (PW == 4) {
-      const float4 v = __builtin_bit_cast(
-          float4, __builtin_amdgcn_raw_buffer_load_b128(rsc, (row * nb + blk) * 4, 0, 0));
-      s[0] = v.x;
-      s[1 % PW] = v.y;
-      s[2 % PW] = v.z;
-      s[3 % PW] = v.w;
-    } else {
-      s[0] = __builtin_bit_cast(float,
-                                __builtin_amdgcn_raw_buffer_load_b32(rsc, (row * nb + blk) * 4, 0, 0));
-    }
-    z = 0x8888u;
-    shift = 0;
-    if (HAS_ZP) {
-      const int off = row * zp_row_bytes + (blk >> 1);
-      if (PW == 4) {
-        z = __builtin_amdgcn_raw_buffer_load_b16(rz, off, 0, 0);
-      } else {
-        z = __builtin_amdgcn_raw_buffer_load_b8(rz, off, 0, 0);
-        shift = (blk & 1) * 4;
-      }
-    }
-  }
-
-  // spare: index of the 4 spare pairs
-  __device__ __forceinline__ void Store(float2 *pairs, int spare) const {
-    const int base = j >= 0 ? j : spare;
-#pragma unroll
-    for (int u = 0; u < PW; ++u) {
-      const uint32_t zp = (z >> (shift + 4 * u)) & 0xFu;
-      pairs[base + u] = make_float2(s[u] * 16777216.f, static_cast<float>(zp) * 5.9604644775390625e-8f);
-    }
-  }
-};
 
 // A float4 f of the chunk layout: stored swizzled, odd k divided by 16, the
 // 8-lane DPP sum of the original values gives the chunk sum. total is a

@@ -8,6 +8,24 @@
 
 namespace mnb {
 
+// Global -> LDS copy of 16 bytes per lane: lane L's 16 bytes at gsrc land at
+// LDS byte lds_base + 16 L (global_load_lds_dwordx4). Issued through inline
+// asm on purpose: the compiler cannot tell which LDS bytes such a copy writes,
+// so for the builtin it orders every later LDS access behind all outstanding
+// vector-memory loads (an s_waitcnt vmcnt(0) before each LDS read or write),
+// which serialises the prefetch pipeline. Hidden from it, the copy still
+// counts in the hardware vmcnt, so the compiler's own waits for register
+// loads stay correct (loads complete in issue order; at worst they also wait
+// for an older copy); callers wait for the copy themselves (s_waitcnt vmcnt
+// counting the loads issued after it, then a barrier) before reading its
+// destination. One wait state separates the M0 write from the copy.
+__device__ __forceinline__ void CopyToLds16(const void *gsrc, uint32_t lds_base) {
+  __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                   :
+                   : "s"(lds_base), "v"(gsrc)
+                   : "memory", "m0");
+}
+
 // Everything a kernel needs to address one plan's constants.
 struct WeightView {
   const uint8_t *B;       // [N, nb, bs/2] packed nibbles, low nibble first
@@ -26,6 +44,16 @@ struct WeightView {
 // Decode GEMV, M in [1, 16], K % 32 == 0, block_size >= 32.
 hipError_t LaunchGemv(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s);
 bool GemvSupports(const WeightView &w, int64_t M);
+
+// Decode GEMV for 2 <= M <= 16 (fp32 FMA on fp16-subnormal decoded nibbles),
+// in groups of at most 4 tokens, one launch per group.
+hipError_t LaunchGemvSmallM(const WeightView &w, int64_t M, const float *A, float *Y,
+                            hipStream_t s);
+bool GemvSmallMSupports(const WeightView &w, int64_t M);
+// Same with an explicit shape (tuning): tokens per group (<= 8), wavefronts
+// per workgroup (4 or 8), rows per wavefront (1, 2 or 4); 0 = default.
+hipError_t LaunchGemvSmallMShape(const WeightView &w, int64_t M, const float *A, float *Y,
+                                 hipStream_t s, int max_tokens, int waves, int rows_per_wave);
 
 // Decode GEMV for M == 1 (fp16-subnormal mixed FMA): one workgroup per band
 // of `band_rows` weight rows, `rows_per_wave` (1, 2, 4 or 8) rows per
