@@ -52,7 +52,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline sampling budget (0 disables)")
     ap.add_argument("--only", default="",
-                    help="comma list of legs: decode,gemm,sweep,cpu,copy (default: all but copy)")
+                    help="comma list of legs: decode,gemm,sweep,c5,cpu,copy (default: all but copy)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step directly instead of replaying a HIP graph "
                          "(for counter collection, which serialises dispatches)")
@@ -182,6 +182,45 @@ def gemm_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
     return res
 
 
+def c5_leg(torch, pkg, dev, M, steps, warmup, stream):
+    """BASELINE config c5: 32 Llama-3-8B-shaped layers (QKV, O, gate+up, down;
+    bs = 128, zero points; 3.74 GB of 4-bit weights) run back to back, one
+    mnb_run per projection, at M tokens. Inputs are independent random
+    activations (no inter-layer math), so the leg measures the 128 projections
+    alone."""
+    c = pkg.workloads.CONFIGS["c5"]
+    ops, sets = [], []
+    for layer in range(c.layers):
+        for j, p in enumerate(c.projections):
+            s = make_device_weights(torch, p, 1, pkg.workloads.weight_seed(c.index, layer, j), dev)
+            sets.append(s)
+            ops.append((p, pkg.MatMulNBits(p.K, p.N, 4, p.block_size).prepare_device(*s[0])))
+    g = torch.Generator(device=dev)
+    g.manual_seed(29)
+    acts = {K: (torch.randn((M, K), device=dev, generator=g) * 1.0).contiguous()
+            for K in sorted({p.K for p in c.projections})}
+    outs = {N: torch.empty((M, N), device=dev) for N in sorted({p.N for p in c.projections})}
+
+    def launches():
+        for p, op in ops:
+            op(acts[p.K], out=outs[p.N], stream=torch.cuda.current_stream())
+
+    ms, wall = time_graph(torch, launches, steps, warmup, stream)
+    nbytes = sum(p.algorithmic_bytes(M) for p, _ in ops)
+    flops = sum(p.flops(M) for p, _ in ops)
+    res = {"M": M, "layers": c.layers, "launches_per_step": len(ops), "ms_per_step": ms,
+           "us_per_launch": ms * 1e3 / len(ops), "bytes_per_step": nbytes,
+           "flops_per_step": flops, "GBps": nbytes / (ms * 1e-3) / 1e9,
+           "TFLOPs": flops / (ms * 1e-3) / 1e12, "wall_ms_per_step": wall * 1e3 / steps}
+    res["frac_hbm"] = res["GBps"] / HBM_PEAK_GBS
+    res["frac_fp16_peak"] = res["TFLOPs"] / FP16_PEAK_TFLOPS
+    for _, op in ops:
+        op.release()
+    del ops, sets
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_leg(pkg, budget_s):
     """Fused int4 GEMV of the C oracle on the c2 M=1 workload, all host threads."""
     import __graft_entry__
@@ -233,7 +272,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(device=dev)
-    legs = set(args.only.split(",")) if args.only else {"decode", "gemm", "sweep", "cpu"}
+    legs = set(args.only.split(",")) if args.only else {"decode", "gemm", "sweep", "c5", "cpu"}
     W = pkg.workloads
 
     t_start = time.perf_counter()
@@ -260,6 +299,13 @@ def main():
                 sweep.append({k: r[k] for k in ("config", "M", "us_per_launch", "GBps", "path")})
                 print(f"# decode {cname} M={M}: {r['us_per_launch']:.2f} us, {r['GBps']:.0f} GB/s",
                       file=sys.stderr, flush=True)
+    c5 = []
+    if "c5" in legs:
+        for M in (1, 512):
+            r = c5_leg(torch, pkg, dev, M, max(3, args.steps // 4), 2, stream)
+            c5.append(r)
+            print(f"# c5 32 layers M={M}: {r['ms_per_step']:.3f} ms/step, {r['GBps']:.0f} GB/s, "
+                  f"{r['TFLOPs']:.1f} TFLOP/s", file=sys.stderr, flush=True)
     copy = None
     if "copy" in legs:
         copy = copy_leg(torch, dev, args.steps, args.warmup, stream)
@@ -295,6 +341,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill_gemm": gemm,
         "decode_sweep": sweep,
+        "c5_layer_stack": c5,
         "copy_calibration": copy,
         "timing": "eager launches" if EAGER else "HIP graph replay",
         "bench_wall_s": time.perf_counter() - t_start,

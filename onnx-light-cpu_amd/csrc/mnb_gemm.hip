@@ -256,39 +256,38 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
   // Iteration kt: after the wait and barrier, A tile kt (stage kt % 3) and B
   // buffer kt % 2 are complete and visible, and every read of stage
   // (kt+2) % 3 and of buffer (kt+1) % 2 from iteration kt-1 is retired. Then
-  // A and B of tile kt+2 are issued, tile kt is multiplied, and B tile kt+1
-  // (loaded one iteration earlier) is dequantized into the other buffer.
+  // B tile kt+1 (loaded one iteration earlier) is dequantized into the other
+  // buffer, A and B of tile kt+2 are issued, and tile kt is multiplied.
+  // The dequantized stores come before the new loads on purpose: the compiler
+  // orders an LDS write behind every outstanding global->LDS copy (it cannot
+  // tell which LDS bytes a copy writes), so a store issued after the copies
+  // of tile kt+2 would wait for them; before them it waits only for the
+  // loads of tile kt+1, which it needs anyway.
   // Unrolled by two so the B register sets are static.
-  // Vector memory operations issued per k-tile and thread: 8 direct A copies
-  // and the B loads. Waiting until at most one k-tile's worth is outstanding
-  // completes tile kt and leaves tile kt+1 in flight.
+  // Vector memory operations issued per k-tile and thread: the direct A
+  // copies and the B loads; at most one k-tile's worth is outstanding at the
+  // barrier.
   constexpr int kOpsPerTile = kAUnits / 256 + 2 + (HAS_ZP ? 1 : 0);
   for (int kt = 0; kt < ktiles; kt += 2) {
     // even step: rb1 holds tile kt+1, rb0 is free
-    if (kt + 1 < ktiles)
-      WaitVm<kOpsPerTile>();
-    else
-      WaitVm<0>();
+    WaitVm<kOpsPerTile>();
     __syncthreads();
+    if (kt + 1 < ktiles) store_b(rb1, 1);
     if (kt + 2 < ktiles) {
       issue_a(kt + 2, (kt + 2) % kAStages);
       load_b(rb0, kt + 2);
     }
     mma_tile(kt % kAStages, 0);
     if (kt + 1 >= ktiles) break;
-    store_b(rb1, 1);
     // odd step: rb0 holds tile kt+2, rb1 is free
-    if (kt + 2 < ktiles)
-      WaitVm<kOpsPerTile>();
-    else
-      WaitVm<0>();
+    WaitVm<kOpsPerTile>();
     __syncthreads();
+    if (kt + 2 < ktiles) store_b(rb0, 0);
     if (kt + 3 < ktiles) {
       issue_a(kt + 3, (kt + 3) % kAStages);
       load_b(rb1, kt + 3);
     }
     mma_tile((kt + 1) % kAStages, 1);
-    if (kt + 2 < ktiles) store_b(rb0, 0);
   }
 
   // Output: lane holds column (lane & 15), rows 4*(lane >> 4) + v of each 16 x 16 tile.

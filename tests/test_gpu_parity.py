@@ -237,3 +237,32 @@ def test_gemm_workspace_contract(pkg, cuda):
     torch.cuda.synchronize()
     assert torch.equal(Y.cpu(), ref)
     op.release()
+
+
+@pytest.mark.parametrize("proj", [0, 1, 2, 3])
+@pytest.mark.parametrize("M", [1, 512])
+def test_c5_layer_projections(pkg, orc, cuda, proj, M):
+    """BASELINE config c5: each projection of a Llama-3-8B-shaped layer (QKV,
+    O, gate+up, down; bs = 128, zero points) at M = 1 (decode GEMV, full
+    output) and M = 512 (prefill GEMM, 32 sampled rows plus the first and
+    last)."""
+    c = pkg.workloads.CONFIGS["c5"]
+    p = c.projections[proj]
+    B, S, Z = pkg.workloads.make_weights(p, pkg.workloads.weight_seed(c.index, 0, proj))
+    A = pkg.workloads.make_activations(M, p.K, p.a_sigma,
+                                       pkg.workloads.activation_seed(c.index, M))
+    Y, path = _run(pkg, cuda, p.K, p.N, p.block_size, B, S, Z, A)
+    if M == 1:
+        assert path == pkg.PATH_GEMV
+        err = orc.normwise_max_error(Y, orc.matmul_nbits_f64(A, B, S, Z, p.K, p.N, p.block_size))
+        print(f"c5 {p.name} M=1: normwise error {err:.3e}")
+        assert err <= GEMV_TOL
+    else:
+        assert path == pkg.PATH_GEMM
+        rows = np.random.default_rng(proj).choice(M, size=32, replace=False)
+        rows = np.sort(np.concatenate([rows, [0, M - 1]]))
+        y64 = orc.matmul_nbits_f64(A[rows], B, S, Z, p.K, p.N, p.block_size)
+        err = orc.l2_rel_error(Y[rows], y64)
+        print(f"c5 {p.name} M=512: L2 relative error on {rows.size} rows {err:.3e}")
+        assert err <= GEMM_TOL
+        assert np.isfinite(Y).all()
