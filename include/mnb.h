@@ -83,7 +83,9 @@ int mnb_plan_destroy(mnb_plan *plan);
 
 /* Device workspace (16-byte aligned) that mnb_run and mnb_run_path need for M
  * rows, whichever path serves them (0 when none). Only the prefill GEMM uses
- * it: A rounded to fp16 in its tile layout, ceil(M/128)*128*K*2 bytes. */
+ * it: A rounded to fp16 in its tile layout, ceil(M/128)*128*K*2 bytes, then,
+ * when the GEMM splits K into S > 1 parts, (S - 1)*M*N*4 bytes of fp32
+ * partial sums (S <= 16, chosen from the shape). */
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
 
 /* Y = MatMulNBits(A, plan) for M rows; dA and dY are device pointers on the

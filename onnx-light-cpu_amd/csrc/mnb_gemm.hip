@@ -35,6 +35,9 @@
 //    all their N tiles, so each XCD's L2 holds one slab of A.
 #include "mnb_kernels.h"
 
+#include <algorithm>
+#include <utility>
+
 namespace mnb {
 namespace {
 
@@ -42,14 +45,17 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;
+constexpr int kMaxBM = 128;  // largest tile height; the workspace pads M to it
 constexpr int kBN = 128;
 constexpr int kBK = 64;
 constexpr int kUnits = kBK / 8;             // 16-byte units per LDS row
-constexpr int kAUnits = kBM * kUnits;       // units per A tile (16 KiB)
 constexpr int kBUnits = kBN * kUnits;       // units per B tile (16 KiB)
 constexpr int kAStages = 3;
-constexpr size_t kLdsBytes = (kAStages * kAUnits + 2 * kBUnits) * 16;  // 80 KiB
+// Output tiles are BM x 128 with BM in {32, 64, 128}; A tiles BM x 64 fp16.
+template <int BM>
+constexpr int AUnits() { return BM * kUnits; }  // units per A tile
+template <int BM>
+constexpr size_t LdsBytes() { return (kAStages * AUnits<BM>() + 2 * kBUnits) * 16; }  // <= 80 KiB
 
 __device__ __forceinline__ int Swz(int row, int unit) {
   return row * kUnits + (unit ^ ((row >> 1) & 7));
@@ -82,6 +88,7 @@ __device__ __forceinline__ uint4 DequantWord(uint32_t w, uint32_t neg_offset, ui
 // One thread per 16-byte LDS unit of the converted A: 8 consecutive fp32 of a
 // row -> 8 fp16 in [0,4,1,5,2,6,3,7] order, written where GemmKernel's direct
 // copy expects it. Rows >= M are written as zeros.
+template <int BM>
 __global__ __launch_bounds__(256) void ConvertAKernel(const float *__restrict__ A,
                                                       uint4 *__restrict__ Ah, int M, int K,
                                                       int64_t total_units) {
@@ -98,10 +105,10 @@ __global__ __launch_bounds__(256) void ConvertAKernel(const float *__restrict__ 
                      PackHalf2(x.w, y.w));
   }
   const int ktiles = K / kBK;
-  const int64_t mt = row / kBM;
-  const int r = static_cast<int>(row - mt * kBM);
+  const int64_t mt = row / BM;
+  const int r = static_cast<int>(row - mt * BM);
   const int kt = ku / kUnits, u = ku % kUnits;
-  Ah[(mt * ktiles + kt) * kAUnits + Swz(r, u)] = out;
+  Ah[(mt * ktiles + kt) * AUnits<BM>() + Swz(r, u)] = out;
 }
 
 // s_waitcnt vmcnt(N) with the other counters left free (gfx9 encoding: vmcnt
@@ -119,15 +126,17 @@ struct BRegs {
   uint32_t z;
 };
 
-template <bool HAS_ZP>
+template <int BM, bool HAS_ZP>
 __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ Ah,
                                                      const uint8_t *__restrict__ B,
                                                      const float *__restrict__ S,
                                                      const uint8_t *__restrict__ Z,
                                                      float *__restrict__ Y, int M, int K, int N,
                                                      int nb, int log2_bs, int row_bytes,
-                                                     int zp_row_bytes) {
+                                                     int zp_row_bytes, int kt_per_split,
+                                                     float *__restrict__ partials) {
   extern __shared__ uint4 lds[];
+  constexpr int kAUnits = AUnits<BM>();
   uint4 *Astage = lds;                        // [kAStages][kAUnits]
   uint4 *Bbuf = lds + kAStages * kAUnits;     // [2][kBUnits]
 
@@ -137,13 +146,15 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
   const int wm = wave >> 1;
   const int wn = wave & 1;
 
-  // XCD-aware tile order.
-  const int tiles_m = (M + kBM - 1) / kBM;
+  // Workgroup b computes output tile b % tiles over the k-tiles of split
+  // b / tiles. XCD-aware tile order.
+  const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + kBN - 1) / kBN;
+  const int split = static_cast<int>(blockIdx.x) / (tiles_m * tiles_n);
   int tm, tn;
   {
-    const int b = blockIdx.x;
-    if (tiles_m % 8 == 0 && gridDim.x == static_cast<unsigned>(tiles_m * tiles_n)) {
+    const int b = static_cast<int>(blockIdx.x) - split * tiles_m * tiles_n;
+    if (tiles_m % 8 == 0) {
       const int xcd = b & 7, local = b >> 3;
       const int band = tiles_m / 8;
       tm = xcd * band + local / tiles_n;
@@ -153,9 +164,11 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
       tn = b % tiles_n;
     }
   }
-  const int m0 = tm * kBM;
+  const int m0 = tm * BM;
   const int n0 = tn * kBN;
-  const int ktiles = K / kBK;
+  // This split's k-tiles: kt0 .. kt0 + ktiles - 1 (the host leaves no split empty).
+  const int kt0 = split * kt_per_split;
+  const int ktiles = min(kt_per_split, K / kBK - kt0);
 
   // B resources based at this tile's first weight row; rows past N read as
   // zero and their outputs are never stored.
@@ -171,7 +184,7 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
 
   // A: converted tile (tm, kt) is kAUnits contiguous units; instruction i of
   // wavefront w copies units i*256 + w*64 + lane to the same LDS offsets.
-  const uint4 *a_tiles = Ah + static_cast<size_t>(tm) * ktiles * kAUnits;
+  const uint4 *a_tiles = Ah + (static_cast<size_t>(tm) * (K / kBK) + kt0) * kAUnits;
   auto issue_a = [&](int kt, int stage) {
     const uint4 *src = a_tiles + static_cast<size_t>(kt) * kAUnits;
     uint4 *dst = Astage + stage * kAUnits;
@@ -190,7 +203,7 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
   const int b_row = tid >> 1;
   const int b_half = tid & 1;
   auto load_b = [&](BRegs &r, int kt) {
-    const int kk = kt * kBK + 32 * b_half;
+    const int kk = (kt0 + kt) * kBK + 32 * b_half;
     r.b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                         rb_rsrc, b_row * row_bytes + (kk >> 1), 0, 0));
     const int blk = kk >> log2_bs;
@@ -214,7 +227,7 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
       Bbuf[buf * kBUnits + Swz(b_row, 4 * b_half + u)] = DequantWord(words[u], neg, sc);
   };
 
-  constexpr int kMI = kBM / 32;  // 16-row MFMA tiles per wavefront along M
+  constexpr int kMI = BM / 32;  // 16-row MFMA tiles per wavefront along M
   floatx4 acc[kMI][4];
 #pragma unroll
   for (int i = 0; i < kMI; ++i)
@@ -234,7 +247,7 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
 #pragma unroll
       for (int i = 0; i < kMI; ++i) {
         const half8 af =
-            __builtin_bit_cast(half8, as[Swz(wm * (kBM / 2) + i * 16 + (lane & 15), unit)]);
+            __builtin_bit_cast(half8, as[Swz(wm * (BM / 2) + i * 16 + (lane & 15), unit)]);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
@@ -290,7 +303,10 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
     mma_tile((kt + 1) % kAStages, 1);
   }
 
-  // Output: lane holds column (lane & 15), rows 4*(lane >> 4) + v of each 16 x 16 tile.
+  // Output: split 0 writes Y, split s > 0 of a split-K launch its partial sum
+  // at partials + (s - 1) * M * N. Lane holds column (lane & 15), rows
+  // 4*(lane >> 4) + v of each 16 x 16 tile.
+  if (split > 0) Y = partials + static_cast<size_t>(split - 1) * M * N;
 #pragma unroll
   for (int i = 0; i < kMI; ++i) {
 #pragma unroll
@@ -298,33 +314,152 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
       const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int gm = m0 + wm * (kBM / 2) + i * 16 + 4 * (lane >> 4) + v;
+        const int gm = m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + v;
         if (gm < M && gn < N) Y[static_cast<size_t>(gm) * N + gn] = acc[i][j][v];
       }
     }
   }
 }
 
-template <bool HAS_ZP>
-hipError_t LaunchT(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, hipStream_t s) {
-  const int tiles = static_cast<int>(((M + kBM - 1) / kBM) * ((w.N + kBN - 1) / kBN));
-  hipLaunchKernelGGL((GemmKernel<HAS_ZP>), dim3(tiles), dim3(256), kLdsBytes, s, Ah, w.B,
-                     w.scales, w.zp, Y, static_cast<int>(M), static_cast<int>(w.K),
-                     static_cast<int>(w.N), static_cast<int>(w.nb), w.log2_bs,
-                     static_cast<int>(w.row_bytes), static_cast<int>(w.zp_row_bytes));
+// Split-K epilogue: Y += partials[0] + ... + partials[PARTS - 1], summed in
+// that order for every element, so results do not depend on scheduling.
+// PARTS is a template argument so that every load is in flight before the
+// first add (one HBM round trip per thread, not PARTS of them).
+template <bool VEC, int PARTS>
+__global__ __launch_bounds__(256) void SplitReduceKernel(float *__restrict__ Y,
+                                                         const float *__restrict__ P,
+                                                         int64_t mn) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * (VEC ? 4 : 1);
+  if (i >= mn) return;
+  if constexpr (VEC) {
+    f32x4 v[PARTS];
+#pragma unroll
+    for (int p = 0; p < PARTS; ++p)
+      v[p] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(P + p * mn + i));
+    f32x4 y = *reinterpret_cast<const f32x4 *>(Y + i);
+#pragma unroll
+    for (int p = 0; p < PARTS; ++p) y += v[p];
+    *reinterpret_cast<f32x4 *>(Y + i) = y;
+  } else {
+    float v[PARTS];
+#pragma unroll
+    for (int p = 0; p < PARTS; ++p) v[p] = __builtin_nontemporal_load(P + p * mn + i);
+    float y = Y[i];
+#pragma unroll
+    for (int p = 0; p < PARTS; ++p) y += v[p];
+    Y[i] = y;
+  }
+}
+
+template <int PARTS>
+hipError_t LaunchReduce(float *Y, const float *P, int64_t mn, hipStream_t s) {
+  if (mn % 4 == 0 && reinterpret_cast<uintptr_t>(Y) % 16 == 0) {
+    hipLaunchKernelGGL((SplitReduceKernel<true, PARTS>),
+                       dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s, Y, P,
+                       mn);
+  } else {
+    hipLaunchKernelGGL((SplitReduceKernel<false, PARTS>),
+                       dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, Y, P, mn);
+  }
   return hipGetLastError();
+}
+
+template <int... Ps>
+hipError_t DispatchReduce(int parts, float *Y, const float *P, int64_t mn, hipStream_t s,
+                          std::integer_sequence<int, Ps...>) {
+  hipError_t e = hipErrorInvalidValue;
+  ((parts == Ps + 1 ? (e = LaunchReduce<Ps + 1>(Y, P, mn, s), true) : false) || ...);
+  return e;
+}
+
+constexpr int kMaxSplits = 16;
+
+struct Shape {
+  int bm;      // tile height: 32, 64 or 128
+  int splits;  // K splits, each a contiguous run of kt_per_split k-tiles
+  int kt_per_split;
+};
+
+// Normalises a requested split count: no split is left without k-tiles.
+inline Shape MakeShape(const WeightView &w, int bm, int splits) {
+  const int ktiles = static_cast<int>(w.K / kBK);
+  splits = std::max(1, std::min({splits, ktiles, kMaxSplits}));
+  const int per = (ktiles + splits - 1) / splits;
+  return Shape{bm, (ktiles + per - 1) / per, per};
+}
+
+inline size_t AImageBytes(const WeightView &w, int64_t M) {
+  const int64_t mpad = (M + kMaxBM - 1) / kMaxBM * kMaxBM;  // covers every tile height
+  return static_cast<size_t>(mpad) * static_cast<size_t>(w.K) * 2;
+}
+
+inline size_t PartialBytes(const WeightView &w, int64_t M, const Shape &sh) {
+  return static_cast<size_t>(sh.splits - 1) * static_cast<size_t>(M) * w.N * 4;
+}
+
+template <int BM, bool HAS_ZP>
+hipError_t LaunchT(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, float *partials,
+                   const Shape &sh, hipStream_t s) {
+  const int tiles = static_cast<int>(((M + BM - 1) / BM) * ((w.N + kBN - 1) / kBN));
+  hipLaunchKernelGGL((GemmKernel<BM, HAS_ZP>), dim3(tiles * sh.splits), dim3(256), LdsBytes<BM>(),
+                     s, Ah, w.B, w.scales, w.zp, Y, static_cast<int>(M), static_cast<int>(w.K),
+                     static_cast<int>(w.N), static_cast<int>(w.nb), w.log2_bs,
+                     static_cast<int>(w.row_bytes), static_cast<int>(w.zp_row_bytes),
+                     sh.kt_per_split, partials);
+  return hipGetLastError();
+}
+
+template <int BM>
+hipError_t LaunchBM(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                    const Shape &sh, hipStream_t s) {
+  uint4 *Ah = static_cast<uint4 *>(work);
+  float *partials = reinterpret_cast<float *>(static_cast<char *>(work) + AImageBytes(w, M));
+  const int64_t units = (M + BM - 1) / BM * BM * (w.K / 8);
+  hipLaunchKernelGGL(ConvertAKernel<BM>, dim3(static_cast<unsigned>((units + 255) / 256)),
+                     dim3(256), 0, s, A, Ah, static_cast<int>(M), static_cast<int>(w.K), units);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = w.zp != nullptr ? LaunchT<BM, true>(w, M, Ah, Y, partials, sh, s)
+                      : LaunchT<BM, false>(w, M, Ah, Y, partials, sh, s);
+  if (e != hipSuccess || sh.splits == 1) return e;
+  return DispatchReduce(sh.splits - 1, Y, partials, M * w.N, s,
+                        std::make_integer_sequence<int, kMaxSplits - 1>{});
+}
+
+// Tile height and K splits, from sweeps on MI355X of every tile height
+// against 1..16 splits (c2..c5 shapes, M = 2..2048):
+// - tile height: 32 for M <= 32, 64 for M <= 64, else 128 (taller tiles
+//   amortise the B dequantization over more rows and won at every M >= 128,
+//   once split-K supplies the workgroups);
+// - splits: as many as keep the whole launch within one wave of two
+//   workgroups per CU (a partial second wave costs a full k-loop), and no
+//   fewer than 8 k-tiles per split (the prologue and the reduction are not
+//   free).
+inline Shape PickShape(const WeightView &w, int64_t M) {
+  const int bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+  const int64_t tiles = (M + bm - 1) / bm * ((w.N + kBN - 1) / kBN);
+  const int64_t slots = 2 * static_cast<int64_t>(w.num_cus);
+  const int ktiles = static_cast<int>(w.K / kBK);
+  int64_t splits = std::max<int64_t>(1, slots / tiles);
+  splits = std::min<int64_t>({splits, kMaxSplits, std::max(1, ktiles / 8)});
+  return MakeShape(w, bm, static_cast<int>(splits));
 }
 
 } // namespace
 
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M) {
-  const int64_t mpad = (M + kBM - 1) / kBM * kBM;
-  return static_cast<size_t>(mpad) * static_cast<size_t>(w.K) * 2;
+  return AImageBytes(w, M) + PartialBytes(w, M, PickShape(w, M));
+}
+
+size_t GemmShapeWorkspaceBytes(const WeightView &w, int64_t M, int splits) {
+  return AImageBytes(w, M) + PartialBytes(w, M, MakeShape(w, 32, splits));
 }
 
 bool GemmSupports(const WeightView &w, int64_t M) {
-  // Buffer offsets are 32-bit within one tile of 128 weight rows.
-  const int64_t tiles = ((M + kBM - 1) / kBM) * ((w.N + kBN - 1) / kBN);
+  // Buffer offsets are 32-bit within one tile of 128 weight rows; up to 16
+  // splits of the BM = 32 tiling must fit one grid.
+  const int64_t tiles = ((M + 31) / 32) * ((w.N + kBN - 1) / kBN) * 16;
   return M >= 1 && (w.K % kBK) == 0 && w.block_size >= 32 && tiles < (int64_t{1} << 31) &&
          int64_t{kBN} * w.row_bytes < (int64_t{1} << 31) &&
          int64_t{kBN} * w.nb * 4 < (int64_t{1} << 31) && (w.row_bytes % 16) == 0 &&
@@ -332,15 +467,21 @@ bool GemmSupports(const WeightView &w, int64_t M) {
          w.N <= (int64_t{1} << 30) && w.K <= (int64_t{1} << 24);
 }
 
+hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                           hipStream_t s, int bm, int splits) {
+  Shape sh = PickShape(w, M);
+  if (bm > 0) sh = MakeShape(w, bm, splits > 0 ? splits : 1);
+  switch (sh.bm) {
+  case 32: return LaunchBM<32>(w, M, A, Y, work, sh, s);
+  case 64: return LaunchBM<64>(w, M, A, Y, work, sh, s);
+  case 128: return LaunchBM<128>(w, M, A, Y, work, sh, s);
+  default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                       hipStream_t s) {
-  uint4 *Ah = static_cast<uint4 *>(work);
-  const int64_t units = (M + kBM - 1) / kBM * kBM * (w.K / 8);
-  hipLaunchKernelGGL(ConvertAKernel, dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256),
-                     0, s, A, Ah, static_cast<int>(M), static_cast<int>(w.K), units);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return w.zp != nullptr ? LaunchT<true>(w, M, Ah, Y, s) : LaunchT<false>(w, M, Ah, Y, s);
+  return LaunchGemmShape(w, M, A, Y, work, s, 0, 0);
 }
 
 } // namespace mnb

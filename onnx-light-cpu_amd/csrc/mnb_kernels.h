@@ -63,11 +63,18 @@ hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream
 bool GemvM1Supports(const WeightView &w);
 
 // Prefill GEMM on fp16 MFMA, any M, K % 64 == 0, block_size >= 32. `work`
-// holds GemmWorkspaceBytes(w, M) bytes of device memory (A rounded to fp16).
+// holds GemmWorkspaceBytes(w, M) bytes of device memory: A rounded to fp16,
+// then the partial sums of a split-K launch.
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                       hipStream_t s);
 bool GemmSupports(const WeightView &w, int64_t M);
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M);
+// Same with an explicit tile height (32, 64 or 128; 0 picks both) and split
+// count (1..16), for tuning; `work` then holds
+// GemmShapeWorkspaceBytes(w, M, splits) bytes.
+hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                           hipStream_t s, int bm, int splits);
+size_t GemmShapeWorkspaceBytes(const WeightView &w, int64_t M, int splits);
 
 // Generic fallback: any K, any block_size, any M. Slow; for odd shapes and
 // cross-checks.

@@ -94,6 +94,38 @@ def test_small_shapes_auto_path(pkg, orc, cuda, K, N, bs, zp, M):
         assert orc.normwise_max_error(Y, y64) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("K,N,bs,zp,M,y_offset", [
+    (2368, 200, 64, True, 20, 0),     # tile height 32, 37 k-tiles in 4 uneven splits
+    (2368, 200, 64, True, 20, 1),     # same, Y 4 bytes past a 16-byte boundary (scalar sums)
+    (4096, 129, 128, False, 33, 0),   # tile height 64, 8 splits, M*N odd, ragged N
+    (8192, 64, 32, True, 100, 0),     # tile height 128, 16 splits of 8 k-tiles
+    (1024, 1000, 128, True, 65, 0),   # tile height 128, 2 splits, 8 N tiles
+    (4096, 4096, 128, True, 256, 0),  # 64 tiles, 8 splits
+])
+def test_gemm_split_k(pkg, orc, cuda, K, N, bs, zp, M, y_offset):
+    """Split-K GEMM: partial sums of every split reach Y exactly once, in
+    order, for each tile height and for uneven and 16-way splits."""
+    import torch
+    p, B, S, Z = _case(pkg, K, N, bs, zp, seed=K + N + M)
+    A = pkg.workloads.make_activations(M, K, 1.0, seed=M + 5)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    assert op.select_path(M) == pkg.PATH_GEMM
+    print(f"case split-K K={K} N={N} bs={bs} zp={zp} M={M} y_offset={y_offset} "
+          f"workspace={op.workspace_bytes(M)}", flush=True)
+    buf = torch.full((M * N + 4,), float("nan"), device=cuda)
+    out = buf[y_offset:y_offset + M * N]
+    op(torch.from_numpy(A).to(cuda), out=out)
+    torch.cuda.synchronize()
+    Y = out.reshape(M, N).cpu().numpy()
+    assert np.isfinite(Y).all()
+    assert torch.isnan(buf[:y_offset]).all() and torch.isnan(buf[y_offset + M * N:]).all()
+    rows = np.unique(np.linspace(0, M - 1, 24).astype(int))
+    err = orc.l2_rel_error(Y[rows], orc.matmul_nbits_f64(A[rows], B, S, Z, K, N, bs))
+    print(f"  L2 relative error {err:.3e}")
+    assert err <= GEMM_TOL
+    op.release()
+
+
 @pytest.mark.parametrize("K,N,bs,zp", [(100, 37, 32, True), (33, 5, 16, False),
                                        (1000, 64, 128, True), (4095, 19, 64, False)])
 @pytest.mark.parametrize("M", [1, 5, 20])
@@ -205,16 +237,19 @@ def test_prepare_device_borrows(pkg, orc, cuda):
 
 
 def test_gemm_workspace_contract(pkg, cuda):
-    """mnb_workspace_bytes is ceil(M/128)*128*K*2 for the GEMM; path 2 refuses
-    a missing, short or misaligned workspace with MNB_ERR_WORKSPACE before any
-    launch, and a reused larger workspace gives the same bits."""
+    """mnb_workspace_bytes is ceil(M/128)*128*K*2 (A in fp16) plus (S-1)*M*N*4
+    for a GEMM that splits K into S <= 16 parts; path 2 refuses a missing,
+    short or misaligned workspace with MNB_ERR_WORKSPACE before any launch, and
+    a reused larger workspace with stale contents gives the same bits."""
     import ctypes
     import torch
     K, N, bs = 512, 256, 64
     p, B, S, Z = _case(pkg, K, N, bs, True, seed=31)
     op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
     for M in (1, 16, 17, 128, 129, 300):
-        assert op.workspace_bytes(M) == -(-M // 128) * 128 * K * 2
+        a_image = -(-M // 128) * 128 * K * 2
+        extra = op.workspace_bytes(M) - a_image
+        assert extra >= 0 and extra % (M * N * 4) == 0 and extra // (M * N * 4) < 16, (M, extra)
     assert op.workspace_bytes(0) == 0
     M = 200
     print(f"case workspace K={K} N={N} bs={bs} M={M} path=2", flush=True)
