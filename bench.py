@@ -10,8 +10,11 @@ their event-timed duration (GB/s), inputs resident in HBM.
 
 Also reported on the same line: the prefill GEMM (configs[3], M=2048
 K=N=4096 bs=128 symmetric) in TFLOP/s against the fp16 dense MFMA peak, the
-other decode shapes, and the CPU baseline: the C oracle's fused int4 GEMV
-(``kind: port``) timed on this host's cores over the same c2 inputs.
+other decode shapes, the c5 32-layer stack, and the CPU baseline on this
+host's cores over the same c2 inputs: the C oracle's fused int4 GEMV
+(``kind: port``, the value) at T threads and at 1, and the reference's own
+MatMulPlan<float> (built from its sources into oracle/_ref) over the weights
+dequantized to fp32, at T threads and at 1.
 
 Algorithmic bytes per launch = N*nb*bs/2 (packed B) + 4*N*nb (scales) +
 N*ceil(nb/2) (zero points) + 4*M*K (A) + 4*M*N (Y); FLOPs = 2*M*N*K.
@@ -24,6 +27,7 @@ import os
 import pathlib
 import platform
 import statistics
+import subprocess
 import sys
 import time
 
@@ -49,8 +53,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="CPU baseline sampling budget (0 disables)")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="CPU baseline sampling budget over its four modes (0 disables)")
     ap.add_argument("--only", default="",
                     help="comma list of legs: decode,gemm,sweep,c5,cpu,copy (default: all but copy)")
     ap.add_argument("--eager", action="store_true",
@@ -221,40 +225,95 @@ def c5_leg(torch, pkg, dev, M, steps, warmup, stream):
     return res
 
 
+def _cpu_topology():
+    """lscpu's sockets x cores x threads-per-core, or None where lscpu is absent."""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    f = {}
+    for line in out.splitlines():
+        k, _, v = line.partition(":")
+        f[k.strip()] = v.strip()
+    return {"sockets": f.get("Socket(s)"), "cores_per_socket": f.get("Core(s) per socket"),
+            "threads_per_core": f.get("Thread(s) per core"), "model": f.get("Model name")}
+
+
+def _time_calls(fn, budget_s, max_calls=100000):
+    """Median and IQR of fn() over about budget_s seconds, after 3 warmup calls, >= 7 samples."""
+    for _ in range(3):
+        fn()
+    samples = []
+    t_end = time.perf_counter() + budget_s
+    while len(samples) < 7 or (time.perf_counter() < t_end and len(samples) < max_calls):
+        t0 = time.perf_counter()
+        fn()
+        samples.append(time.perf_counter() - t0)
+    med = statistics.median(samples)
+    q = statistics.quantiles(samples, n=4)
+    return med, q[2] - q[0], len(samples)
+
+
 def cpu_leg(pkg, budget_s):
-    """Fused int4 GEMV of the C oracle on the c2 M=1 workload, all host threads."""
+    """CPU baselines on the c2 M=1 workload, host cores of this machine.
+
+    Four modes, about budget_s / 4 seconds each:
+    - fused: the C oracle's fused unpack-scale-FMA fp32 GEMV over the packed
+      4-bit weights, N-partitioned like the reference's ExecuteRanges
+      (onnx_light_cpu/impl/execution.h:72-184), at T threads and at 1;
+    - reference: the reference's own MatMulPlan<float> (compiled from its
+      sources into oracle/_ref) over W dequantized to fp32 [N, K] once
+      beforehand, i.e. the dequantize-then-fp32-MatMul order of the reference
+      engine with the dequantization folded away, at T threads and at 1.
+    Every rate is the workload's algorithmic bytes (4-bit weights, scales, zero
+    points, A, Y) over the median call time, the unit of the GPU figure.
+    """
+    import numpy as np
     import __graft_entry__
     orc = __graft_entry__.load_oracle()
     c = pkg.workloads.CONFIGS["c2"]
     p = c.projections[0]
     B, S, Z = pkg.workloads.make_weights(p, pkg.workloads.weight_seed(c.index))
     A = pkg.workloads.make_activations(1, p.K, p.a_sigma, pkg.workloads.activation_seed(c.index, 1))
-    threads = orc.default_threads()
     try:
-        threads = min(threads, len(os.sched_getaffinity(0)))
+        avail = len(os.sched_getaffinity(0))
     except AttributeError:
-        pass
-    samples = []
-    for _ in range(3):
-        orc.matmul_nbits_fused_f32(A, B, S, Z, p.K, p.N, p.block_size, threads)
-    t_end = time.perf_counter() + budget_s
-    while len(samples) < 7 or time.perf_counter() < t_end:
-        t0 = time.perf_counter()
-        orc.matmul_nbits_fused_f32(A, B, S, Z, p.K, p.N, p.block_size, threads)
-        samples.append(time.perf_counter() - t0)
-        if len(samples) >= 2000:
-            break
-    med = statistics.median(samples)
-    q = statistics.quantiles(samples, n=4) if len(samples) >= 4 else [med, med, med]
+        avail = os.cpu_count() or 1
+    T = max(1, min(orc.default_threads(), avail))
     nbytes = p.algorithmic_bytes(1)
-    return {
-        "value": nbytes / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": (f"c2 M=1 K=4096 N=14336 bs=128 zp, full matrix, {len(samples)} calls "
-                   f"(median {med * 1e3:.2f} ms, IQR {(q[2] - q[0]) * 1e3:.2f} ms) of the C "
-                   f"oracle's fused int4 GEMV; onnx-light CpuExecutor: not available "
-                   f"(onnx-light absent); equivalent participants = {threads}"),
-        "host": platform.processor() or platform.machine(), "nproc": os.cpu_count(),
-    }
+    per = budget_s / 4.0
+    modes = []
+
+    def add(name, threads, fn):
+        med, iqr, n = _time_calls(fn, per)
+        modes.append({"mode": name, "threads": threads, "GBps": nbytes / med / 1e9,
+                      "median_ms": med * 1e3, "iqr_ms": iqr * 1e3, "calls": n})
+        print(f"# cpu {name} threads={threads}: {med * 1e3:.2f} ms/call, "
+              f"{nbytes / med / 1e9:.2f} GB/s ({n} calls)", file=sys.stderr, flush=True)
+
+    for t in (T, 1):
+        add("fused int4 GEMV (C oracle)", t,
+            lambda t=t: orc.matmul_nbits_fused_f32(A, B, S, Z, p.K, p.N, p.block_size, t))
+    if orc.ref_available():
+        # [K, N]: the orientation an ONNX MatMul's B input has after the
+        # dequantization is folded into a constant.
+        W = np.ascontiguousarray(orc.dequantize(B, S, Z, p.K, p.N, p.block_size).T,
+                                 dtype=np.float32)
+        for t in (T, 1):
+            add("reference MatMulPlan<float> on dequantized W [K,N] (oracle/_ref)", t,
+                lambda t=t: orc.ref_matmul_f32(A, W, t, trans_b=False))
+        del W
+    head = modes[0]
+    sample = (f"c2 M=1 K=4096 N=14336 bs=128 zp, full matrix per call; value = fused int4 GEMV "
+              f"of the C oracle on {T} threads, {head['calls']} calls (median "
+              f"{head['median_ms']:.2f} ms, IQR {head['iqr_ms']:.2f} ms); 1-thread and "
+              f"reference-MatMul figures under modes (the reference plan picks kSkinnyM at "
+              f"M=1, whose column-panel split gave no parallel speedup on this host); "
+              f"onnx-light CpuExecutor: not available "
+              f"(onnx-light absent); equivalent participants = {T}")
+    return {"value": head["GBps"], "unit": "GB/s", "cores": T, "kind": "port", "sample": sample,
+            "modes": modes, "host": platform.processor() or platform.machine(),
+            "nproc": os.cpu_count(), "affinity": avail, "topology": _cpu_topology()}
 
 
 def main():

@@ -159,14 +159,16 @@ def execution_block_count(total, cost, threads):
 
 # ---- reference build wrappers (oracle/_ref) ----
 
-def ref_matmul_f32(A, W, threads=1):
-    """Reference MatMulPlan<float>: Y = A @ W^T with W [N, K] passed as trans_b."""
+def ref_matmul_f32(A, W, threads=1, trans_b=True):
+    """Reference MatMulPlan<float>: Y = A @ W^T with W [N, K] passed as trans_b,
+    or (trans_b=False) Y = A @ W with W [K, N], the orientation of an ONNX
+    MatMul's B input."""
     A = np.ascontiguousarray(A, dtype=np.float32)
     W = np.ascontiguousarray(W, dtype=np.float32)
     M, K = A.shape
-    N = W.shape[0]
+    N = W.shape[0] if trans_b else W.shape[1]
     Y = np.empty((M, N), np.float32)
-    algo = ref().olcref_matmul_f32(M, N, K, _ptr(A), _ptr(W), 1, _ptr(Y), threads)
+    algo = ref().olcref_matmul_f32(M, N, K, _ptr(A), _ptr(W), int(trans_b), _ptr(Y), threads)
     return Y, algo
 
 

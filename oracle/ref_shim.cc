@@ -44,21 +44,25 @@ void olcref_int4_matmul(const uint8_t *a, int a_signed, const uint8_t *b, int b_
 // Y[M,N] = A[M,K] * B where B is [K,N] (trans_b = 0) or [N,K] (trans_b = 1).
 // threads > 1 injects an executor view, as the onnx-light session would.
 // Returns the GemmAlgorithm the plan selected.
-int olcref_matmul_f32(int64_t M, int64_t N, int64_t K, const float *A, const float *B,
-                      int trans_b, float *Y, int threads) {
+// The plan is built inside the executor scope, as in a session: GemmPlan fixes
+// its useful thread count when it is constructed (gemm_plan.cc:200-215).
+static int PlanAndRun(int64_t M, int64_t N, int64_t K, const float *A, const float *B,
+                      int trans_b, float *Y) {
   onnx_light_cpu::MatMulPlan<float> plan(static_cast<size_t>(M), static_cast<size_t>(N),
                                          static_cast<size_t>(K), false, trans_b != 0);
-  if (threads > 1) {
-    onnx_light_cpu::ExecutionExecutorView view;
-    view.context = nullptr;
-    view.effective_threads = threads;
-    view.run_blocks = &RunBlocksOnThreads;
-    onnx_light_cpu::ExecutionExecutorScope scope(&view);
-    plan.Execute(A, B, Y);
-  } else {
-    plan.Execute(A, B, Y);
-  }
+  plan.Execute(A, B, Y);
   return static_cast<int>(plan.gemm_plan().algorithm());
+}
+
+int olcref_matmul_f32(int64_t M, int64_t N, int64_t K, const float *A, const float *B,
+                      int trans_b, float *Y, int threads) {
+  if (threads <= 1) return PlanAndRun(M, N, K, A, B, trans_b, Y);
+  onnx_light_cpu::ExecutionExecutorView view;
+  view.context = nullptr;
+  view.effective_threads = threads;
+  view.run_blocks = &RunBlocksOnThreads;
+  onnx_light_cpu::ExecutionExecutorScope scope(&view);
+  return PlanAndRun(M, N, K, A, B, trans_b, Y);
 }
 
 uint16_t olcref_f32_to_f16_bits(float value) {
