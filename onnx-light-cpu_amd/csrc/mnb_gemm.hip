@@ -12,19 +12,22 @@
 //    A bytes it streams.
 //
 // 2. GemmKernel: one workgroup (256 threads, 4 wavefronts as 2 x 2) owns a
-//    128 x 128 output tile; each wavefront a 64 x 64 sub-tile = 4 x 4
-//    v_mfma_f32_16x16x32_f16 tiles. K advances in k-tiles of 64. 80 KiB of LDS
-//    per workgroup lets two workgroups share a CU, so one hides the other's
-//    barrier and dequantization stalls.
-//    - A tiles (16 KiB) go global -> LDS directly (global_load_lds_dwordx4,
-//      no registers) through a 3-stage ring, two k-tiles ahead.
-//    - B tiles: each thread loads 32 nibbles of one weight row two k-tiles
-//      ahead into registers. A masked word (w >> 4i) & 0x000F000F | 0x64006400
-//      holds two fp16 values 1024 + q exactly; one packed add of -(1024 + zp)
-//      makes q - zp exact and one packed multiply by the block's fp16 scale
-//      gives the weight; the dequantized tile goes to a double-buffered LDS
-//      tile while the current k-tile is multiplied.
-//    - One barrier per k-tile.
+//    BM x 128 output tile (BM = 128, 64 or 32, by M); each wavefront a
+//    BM/2 x 64 sub-tile of v_mfma_f32_16x16x32_f16 tiles. K advances in
+//    k-tiles of 64, optionally split over several workgroups (split-K; the
+//    partial sums are added in split order by SplitReduceKernel). 80 KiB of
+//    LDS per workgroup (BM = 128) lets two workgroups share a CU, so one
+//    hides the other's barrier and dequantization stalls.
+//    - A tiles go global -> LDS directly (global_load_lds_dwordx4 through
+//      inline asm, no registers) into a 3-stage ring, two k-tiles ahead.
+//    - B tiles: each thread loads 32 nibbles of one weight row into
+//      registers four k-tiles ahead, dequantizes them one k-tile ahead into a
+//      double-buffered LDS tile (DequantWord: masks and fp16 exponent
+//      constants give 1024 + q and 64 + q exactly, a packed add of the
+//      matching -(1024 + zp) or -(64 + zp) makes q - zp exact, one packed
+//      multiply by the block's fp16 scale rounds the weight once).
+//    - One barrier per k-tile; the loop is written so that the compiler's
+//      own waits never drain the prefetch (see the pipeline comment below).
 //    Inside every group of 8 k the LDS order is [0,4,1,5,2,6,3,7] for both A
 //    and B (the order the masked words produce); the contraction is unchanged.
 //    LDS rows are 64 fp16 = 8 units of 16 B; unit u of row r is stored at
@@ -36,6 +39,7 @@
 #include "mnb_kernels.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <utility>
 
 namespace mnb {
@@ -76,13 +80,47 @@ __device__ __forceinline__ uint32_t PkMulF16(uint32_t a, uint32_t b) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// One packed word of 8 nibbles (k order) -> 8 fp16 weights in [0,4,1,5,2,6,3,7] order.
-__device__ __forceinline__ uint4 DequantWord(uint32_t w, uint32_t neg_offset, uint32_t scale2) {
-  uint32_t t[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    t[i] = PkMulF16(PkAddF16(((w >> (4 * i)) & 0x000F000Fu) | 0x64006400u, neg_offset), scale2);
-  return make_uint4(t[0], t[1], t[2], t[3]);
+// Per-thread constants of the dequantization, held in VGPRs (an empty asm
+// hides their values from the compiler): VOP3 instructions on gfx9 take no
+// literal, so with the masks as literals (w & m) | c costs two instructions
+// instead of one v_and_or_b32.
+struct DequantConsts {
+  uint32_t lo, hi, e1024, e64;  // 0x000F000F, 0x00F000F0, fp16 pairs 1024.0, 64.0
+};
+__device__ __forceinline__ DequantConsts MakeDequantConsts() {
+  DequantConsts c{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u};
+  __asm__ volatile("" : "+v"(c.lo), "+v"(c.hi), "+v"(c.e1024), "+v"(c.e64));
+  return c;
+}
+
+// Per (row, k-tile) operands of DequantWord: -(1024 + zp) and -(64 + zp)
+// (exact in fp16) and the block scale in fp16.
+struct DequantRow {
+  uint32_t neg_lo, neg_hi, s;
+};
+__device__ __forceinline__ DequantRow MakeDequantRow(float s, uint32_t zp) {
+  const float z = static_cast<float>(zp);
+  return DequantRow{PackHalf2(-(1024.f + z), -(1024.f + z)), PackHalf2(-(64.f + z), -(64.f + z)),
+                    PackHalf2(s, s)};
+}
+
+// One packed word of 8 nibbles (k order) -> 8 fp16 weights in [0,4,1,5,2,6,3,7]
+// order, with no per-nibble shift: in fp16, 1024.0 (0x6400) has an ulp of 1
+// and 64.0 (0x5400) an ulp of 1/16, so (w & 0x000F000F) | 0x6400.. is the
+// pair 1024 + q of nibbles 0 | 4 and (w & 0x00F000F0) | 0x5400.. the pair
+// 64 + q of nibbles 1 | 5, both exact; the same of w >> 8 gives nibbles
+// 2 | 6 and 3 | 7. Adding -(1024 + zp) or -(64 + zp) leaves q - zp exactly,
+// and one multiply by the fp16 scale rounds the weight once. Per word: one
+// shift, four v_and_or_b32, four packed adds and four packed multiplies.
+__device__ __forceinline__ uint4 DequantWord(uint32_t w, const DequantRow &r,
+                                             const DequantConsts &c) {
+  const uint32_t w8 = w >> 8;
+  const uint32_t h0 = (w & c.lo) | c.e1024;   // nibbles 0 | 4: 1024 + q
+  const uint32_t h1 = (w & c.hi) | c.e64;     // nibbles 1 | 5: 64 + q
+  const uint32_t h2 = (w8 & c.lo) | c.e1024;  // nibbles 2 | 6
+  const uint32_t h3 = (w8 & c.hi) | c.e64;    // nibbles 3 | 7
+  return make_uint4(PkMulF16(PkAddF16(h0, r.neg_lo), r.s), PkMulF16(PkAddF16(h1, r.neg_hi), r.s),
+                    PkMulF16(PkAddF16(h2, r.neg_lo), r.s), PkMulF16(PkAddF16(h3, r.neg_hi), r.s));
 }
 
 // One thread per 16-byte LDS unit of the converted A: 8 consecutive fp32 of a
@@ -119,11 +157,15 @@ __device__ __forceinline__ void WaitVm() {
 }
 
 // One k-tile of B for this thread: 32 nibbles of one weight row (one
-// quantization block, block_size >= 32), its scale and zero point.
+// quantization block, block_size >= 32), its scale, and the byte holding its
+// zero point with the nibble's shift. The nibble is extracted only when the
+// tile is dequantized: extracting it at load time would make the compiler wait
+// for the load right after issuing it.
 struct BRegs {
   uint4 b;
   float s;
   uint32_t z;
+  uint32_t zshift;
 };
 
 template <int BM, bool HAS_ZP>
@@ -185,46 +227,54 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
   // A: converted tile (tm, kt) is kAUnits contiguous units; instruction i of
   // wavefront w copies units i*256 + w*64 + lane to the same LDS offsets.
   const uint4 *a_tiles = Ah + (static_cast<size_t>(tm) * (K / kBK) + kt0) * kAUnits;
+  // The copies go through CopyToLds16: with the builtin, the compiler waits
+  // for every outstanding load (s_waitcnt vmcnt(0)) before the next LDS read,
+  // which would stall each k-tile's MFMAs on the loads of tile kt + 2. The
+  // WaitVm + barrier at the top of each iteration covers the copies.
+  const uint32_t lds_a = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(Astage)) +
+                         __builtin_amdgcn_readfirstlane(wave) * 64 * 16;  // uniform
+  const uint4 *a_src = a_tiles + wave * 64 + lane;
   auto issue_a = [&](int kt, int stage) {
-    const uint4 *src = a_tiles + static_cast<size_t>(kt) * kAUnits;
-    uint4 *dst = Astage + stage * kAUnits;
+    const uint4 *src = a_src + static_cast<size_t>(kt) * kAUnits;
 #pragma unroll
-    for (int i = 0; i < kAUnits / 256; ++i) {
-      const int c = i * 256 + wave * 64;  // wave-uniform; the lane offset is implicit
-      __builtin_amdgcn_global_load_lds(
-          static_cast<const void *>(src + c + lane),
-          reinterpret_cast<__attribute__((address_space(3))) void *>(
-              static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst + c))),
-          16, 0, 0);
-    }
+    for (int i = 0; i < kAUnits / 256; ++i)
+      CopyToLds16(src + i * 256, lds_a + (stage * kAUnits + i * 256) * 16);
   };
 
   // B: thread t -> weight row t >> 1, 32 nibbles at k offset 32 * (t & 1).
+  // Buffer offsets are a per-thread constant (voffset) plus the k-tile's
+  // uniform part (soffset), so the loads cost no address arithmetic. The
+  // block of the thread's 32 nibbles is blk_u + blk_l: blk_u = (k-tile start)
+  // >> log2_bs, plus the thread's half when blocks are 32 wide (then blk_u is
+  // even, so the zero-point byte is blk_u >> 1 and the nibble blk_l).
   const int b_row = tid >> 1;
   const int b_half = tid & 1;
+  const int blk_l = log2_bs == 5 ? b_half : 0;
+  const int vo_b = b_row * row_bytes + 16 * b_half;
+  const int vo_s = (b_row * nb + blk_l) * 4;
+  const int vo_z = b_row * zp_row_bytes;
   auto load_b = [&](BRegs &r, int kt) {
-    const int kk = (kt0 + kt) * kBK + 32 * b_half;
-    r.b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                        rb_rsrc, b_row * row_bytes + (kk >> 1), 0, 0));
-    const int blk = kk >> log2_bs;
-    r.s = __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(rs_rsrc, (b_row * nb + blk) * 4, 0, 0));
+    const int kg = kt0 + kt;
+    const int blk_u = (kg * kBK) >> log2_bs;
+    r.b = __builtin_bit_cast(uint4,
+                             __builtin_amdgcn_raw_buffer_load_b128(rb_rsrc, vo_b, kg * 32, 0));
+    r.s = __builtin_bit_cast(float,
+                             __builtin_amdgcn_raw_buffer_load_b32(rs_rsrc, vo_s, blk_u * 4, 0));
     if (HAS_ZP) {
-      const uint32_t zb =
-          __builtin_amdgcn_raw_buffer_load_b8(rz_rsrc, b_row * zp_row_bytes + (blk >> 1), 0, 0);
-      r.z = (zb >> ((blk & 1) * 4)) & 0xFu;
+      r.z = __builtin_amdgcn_raw_buffer_load_b8(rz_rsrc, vo_z, blk_u >> 1, 0);
+      r.zshift = ((blk_u & 1) + blk_l) * 4;
     } else {
       r.z = 8u;
+      r.zshift = 0;
     }
   };
+  const DequantConsts dq = MakeDequantConsts();
   auto store_b = [&](const BRegs &r, int buf) {
     const uint32_t words[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-    const float zf = static_cast<float>(r.z);
-    const uint32_t neg = PackHalf2(-(1024.f + zf), -(1024.f + zf));
-    const uint32_t sc = PackHalf2(r.s, r.s);
+    const DequantRow dr = MakeDequantRow(r.s, (r.z >> r.zshift) & 0xFu);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      Bbuf[buf * kBUnits + Swz(b_row, 4 * b_half + u)] = DequantWord(words[u], neg, sc);
+      Bbuf[buf * kBUnits + Swz(b_row, 4 * b_half + u)] = DequantWord(words[u], dr, dq);
   };
 
   constexpr int kMI = BM / 32;  // 16-row MFMA tiles per wavefront along M
@@ -255,53 +305,69 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
     }
   };
 
-  // Prologue: A tiles 0 and 1 in flight to stages 0 and 1, B tiles 0 and 1 in
-  // registers; B tile 0 dequantized into buffer 0.
-  BRegs rb0, rb1;
+  // Pipeline: A tile t is copied to LDS stage t % 3 two k-tiles ahead; the B
+  // registers of tile t are loaded kPD k-tiles ahead (HBM latency under load
+  // is several k-tiles long) and dequantized into LDS buffer t % 2 one k-tile
+  // ahead. Iteration t:
+  //  1. wait until A tile t (and with it B tile t+1) has landed, then a
+  //     barrier: A tile t and B buffer t % 2 are complete and visible, and
+  //     every read of stage (t+2) % 3 and buffer (t+1) % 2 from iteration
+  //     t-1 is retired;
+  //  2. dequantize B tile t+1 into buffer (t+1) % 2;
+  //  3. copy A tile t+2, load the B registers of tile t+kPD into the set that
+  //     held tile t;
+  //  4. multiply tile t.
+  // Every copy, load and store is issued unconditionally, with the k-tile
+  // index clamped to the last one (the tail re-reads the last tile into
+  // buffers nobody reads again): a branch around a load makes the compiler
+  // wait for all outstanding loads where the paths join. So per iteration the
+  // vector memory operations are exactly [kAOps A copies, kBOps B loads], and
+  // after A tile t come B tile t+2, A tile t+1 and B tile t+3.
+  constexpr int kPD = 4;
+  constexpr int kAOps = kAUnits / 256;
+  constexpr int kBOps = HAS_ZP ? 3 : 2;
+  const int klast = ktiles - 1;
+  BRegs rb[kPD];
   issue_a(0, 0);
-  load_b(rb0, 0);
-  if (ktiles > 1) {
-    issue_a(1, 1);
-    load_b(rb1, 1);
-  }
-  store_b(rb0, 0);
+  load_b(rb[0], 0);
+  load_b(rb[1], min(1, klast));
+  issue_a(min(1, klast), 1);
+#pragma unroll
+  for (int p = 2; p < kPD; ++p) load_b(rb[p], min(p, klast));
+  store_b(rb[0], 0);
 
-  // Iteration kt: after the wait and barrier, A tile kt (stage kt % 3) and B
-  // buffer kt % 2 are complete and visible, and every read of stage
-  // (kt+2) % 3 and of buffer (kt+1) % 2 from iteration kt-1 is retired. Then
-  // B tile kt+1 (loaded one iteration earlier) is dequantized into the other
-  // buffer, A and B of tile kt+2 are issued, and tile kt is multiplied.
-  // The dequantized stores come before the new loads on purpose: the compiler
-  // orders an LDS write behind every outstanding global->LDS copy (it cannot
-  // tell which LDS bytes a copy writes), so a store issued after the copies
-  // of tile kt+2 would wait for them; before them it waits only for the
-  // loads of tile kt+1, which it needs anyway.
-  // Unrolled by two so the B register sets are static.
-  // Vector memory operations issued per k-tile and thread: the direct A
-  // copies and the B loads; at most one k-tile's worth is outstanding at the
-  // barrier.
-  constexpr int kOpsPerTile = kAUnits / 256 + 2 + (HAS_ZP ? 1 : 0);
-  for (int kt = 0; kt < ktiles; kt += 2) {
-    // even step: rb1 holds tile kt+1, rb0 is free
-    WaitVm<kOpsPerTile>();
+  // One iteration; u = t % kPD is a compile-time constant so the register
+  // sets are static.
+  auto step = [&](int t, auto uc) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+    // Nothing crosses the wait and barrier at the top of an iteration:
+    // hoisted above them, the tile's dequantization would make the compiler
+    // wait for its B registers with a count that ignores the A copies (it
+    // cannot see them), i.e. for the copies just issued.
+    __builtin_amdgcn_sched_barrier(0);
+    WaitVm<2 * kBOps + kAOps>();
     __syncthreads();
-    if (kt + 1 < ktiles) store_b(rb1, 1);
-    if (kt + 2 < ktiles) {
-      issue_a(kt + 2, (kt + 2) % kAStages);
-      load_b(rb0, kt + 2);
-    }
-    mma_tile(kt % kAStages, 0);
-    if (kt + 1 >= ktiles) break;
-    // odd step: rb0 holds tile kt+2, rb1 is free
-    WaitVm<kOpsPerTile>();
-    __syncthreads();
-    if (kt + 2 < ktiles) store_b(rb0, 0);
-    if (kt + 3 < ktiles) {
-      issue_a(kt + 3, (kt + 3) % kAStages);
-      load_b(rb1, kt + 3);
-    }
-    mma_tile((kt + 1) % kAStages, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    store_b(rb[(u + 1) % kPD], (t + 1) & 1);
+    issue_a(min(t + 2, klast), (t + 2) % kAStages);
+    load_b(rb[u], min(t + kPD, klast));
+    mma_tile(t % kAStages, t & 1);
+  };
+  // Whole groups of kPD iterations, then the remainder: a loop body with an
+  // exit in the middle would merge different sets of outstanding loads at the
+  // back edge, and the compiler would wait for all of them there.
+  int kt = 0;
+  for (; kt + kPD <= ktiles; kt += kPD) {
+    step(kt, std::integral_constant<int, 0>{});
+    step(kt + 1, std::integral_constant<int, 1>{});
+    step(kt + 2, std::integral_constant<int, 2>{});
+    step(kt + 3, std::integral_constant<int, 3>{});
   }
+  if (kt < ktiles) step(kt, std::integral_constant<int, 0>{});
+  if (kt + 1 < ktiles) step(kt + 1, std::integral_constant<int, 1>{});
+  if (kt + 2 < ktiles) step(kt + 2, std::integral_constant<int, 2>{});
+  // No copy into this workgroup's LDS may land after it exits.
+  WaitVm<0>();
 
   // Output: split 0 writes Y, split s > 0 of a split-K launch its partial sum
   // at partials + (s - 1) * M * N. Lane holds column (lane & 15), rows
@@ -369,7 +435,7 @@ template <int... Ps>
 hipError_t DispatchReduce(int parts, float *Y, const float *P, int64_t mn, hipStream_t s,
                           std::integer_sequence<int, Ps...>) {
   hipError_t e = hipErrorInvalidValue;
-  ((parts == Ps + 1 ? (e = LaunchReduce<Ps + 1>(Y, P, mn, s), true) : false) || ...);
+  (void)((parts == Ps + 1 ? (e = LaunchReduce<Ps + 1>(Y, P, mn, s), true) : false) || ...);
   return e;
 }
 
