@@ -265,35 +265,53 @@ struct Shape {
 };
 
 // Band rows per workgroup G and rows per wavefront R (a power of two), from
-// measured sweeps on MI355X:
+// measured sweeps on MI355X (c1, c2, c3 and the c5 projections):
 //  - short rows (CPL <= 2): workgroups of at most 4 wavefronts x 4 rows, k
 //    workgroups per CU with k = ceil(rows per CU / 16), so that every CU gets
 //    the same number of rows and several independent workgroups (one
-//    workgroup's staging and barrier overlap another's arithmetic);
+//    workgroup's staging and barrier overlap another's arithmetic); when
+//    that gives 3 wavefronts per workgroup, k + 1 (qkv: 12 x 4 6.4 us,
+//    8 x 2 5.2 us). Interleaved medians put c2's 14 x 4 within 2 % of the
+//    best of 8 x 2 and 16 x 4, whose order changes from box to box;
 //  - long rows: one workgroup of up to 16 wavefronts per CU owning the CU's
 //    whole band (A, up to 64 KiB, is staged once per CU).
 // Both keep the LDS within kLdsLimit, shrinking G (more rounds) if needed.
 inline int RMax(int cpl) { return cpl <= 2 ? 8 : (cpl <= 4 ? 4 : 2); }
 
+inline int RowsPerWave(int G) {
+  const int need = (G + kMaxWaves - 1) / kMaxWaves;
+  int R = 1;
+  while (R < need) R *= 2;
+  return R;
+}
+
 inline Shape PickShape(const WeightView &w, int cpl, int G, int R) {
   const int nchunks = static_cast<int>(w.K / 32);
-  const int rows_per_cu = static_cast<int>((w.N + w.num_cus - 1) / w.num_cus);
+  const int64_t cus = w.num_cus;
+  const int rows_per_cu = static_cast<int>((w.N + cus - 1) / cus);
   Shape sh{};
   if (G <= 0) {
     if (cpl <= 2) {
-      const int k = (rows_per_cu + 15) / 16;
+      auto rows_per_wave = [](int g) { return g > 8 ? 4 : (g > 4 ? 2 : 1); };
+      int k = (rows_per_cu + 15) / 16;
       G = (rows_per_cu + k - 1) / k;
-      if (R <= 0) R = G > 8 ? 4 : (G > 4 ? 2 : 1);
+      const int r0 = R > 0 ? R : rows_per_wave(G);
+      if ((G + r0 - 1) / r0 == 3) {
+        ++k;
+        G = (rows_per_cu + k - 1) / k;
+      }
+      if (R <= 0) R = rows_per_wave(G);
     } else {
       G = std::min(rows_per_cu, kMaxWaves * RMax(cpl));
     }
-    while (G > 1 && LdsBytes(nchunks, G + kMaxWaves, w.nb) > kLdsLimit) G = (G + 1) / 2;
+    // Pair space is allocated for waves * R rows.
+    auto lds_for = [&](int g) {
+      const int r = R > 0 ? R : RowsPerWave(g);
+      return LdsBytes(nchunks, (g + r - 1) / r * r, w.nb);
+    };
+    while (G > 1 && lds_for(G) > kLdsLimit) G = (G + 1) / 2;
   }
-  if (R <= 0) {
-    const int need = (G + kMaxWaves - 1) / kMaxWaves;
-    R = 1;
-    while (R < need) R *= 2;
-  }
+  if (R <= 0) R = RowsPerWave(G);
   sh.G = G;
   sh.R = R;
   sh.waves = (G + R - 1) / R;
