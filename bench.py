@@ -322,7 +322,8 @@ def main():
     EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
-              "supported (the decode GEMV would shard column-parallel over N, see DESIGN.md)",
+              "supported (the decode GEMV would shard column-parallel over N, one shard "
+              "of weight rows per GPU)",
               file=sys.stderr)
         sys.exit(2)
     import torch
