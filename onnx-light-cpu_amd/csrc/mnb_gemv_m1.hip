@@ -16,8 +16,13 @@
 // other:
 //  1. the workgroup issues its staging loads: A, and each wavefront the scale
 //     and zero point of every (row, block) of its rows;
-//  2. every wavefront issues the non-temporal buffer loads of all its rows'
-//     weights at once (row offsets are wave-uniform SGPRs);
+//  2. every wavefront issues the first few non-temporal buffer loads of its
+//     rows' weights (row offsets are wave-uniform SGPRs); the rest are issued
+//     one by one behind the dot products of step 4, a fixed number ahead, so
+//     that a wavefront stalled at issue (the memory pipeline full) still has
+//     arrived data to compute on: with every load issued up front, waves
+//     spent up to 5 us of a 7.6 us launch issuing, and the last ones did all
+//     their arithmetic after HBM had gone idle (per-wave timestamps);
 //  3. the staged values go to LDS as they return (loads complete in issue
 //     order, so this never waits behind the weights): A as swizzled float4
 //     chunks with the per-chunk sums asum = sum_j a_j, and the pairs
@@ -59,6 +64,11 @@ constexpr size_t kLdsLimit = 150 * 1024;  // of the 160 KiB per CU
 constexpr size_t kOnePerCu = 81 * 1024;   // more than half: one workgroup per CU
 constexpr int kAPasses = 4;               // A float4 per thread staged ahead of the weights
 constexpr int kPPasses = 2;               // (scale, zp) work items per thread ahead of the weights
+// Weight loads kept in flight per wavefront behind the dot products: 4, or 2
+// when a wavefront owns one long row (interleaved medians on MI355X, window
+// 2/4/6/all: c2 8.09/7.99/8.33/8.40 us, c3 9.82/10.22/11.40/11.85 us).
+template <int R>
+constexpr int M1Window() { return R == 1 ? 2 : 4; }
 
 // sum_j a'[j] * f16-subnormal masks of one chunk = sum_j a_j q_j 2^-24, where
 // a' holds a_j / 16 at odd j (k order inside the chunk).
@@ -178,19 +188,25 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
   // the weight loads (completion is in issue order).
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. then all weights of this wavefront's rows (rows past the band re-read
-  //    the band's last row; their results are not stored)
+  // 2. then the first kWin weight loads of this wavefront (rows past the band
+  //    re-read the band's last row; their results are not stored). Load j is
+  //    chunk i = j / R of row r = j % R, the order the dot products consume
+  //    them; the rest are issued one by one behind the dot products (step 4).
+  constexpr int kLoads = R * CPL;
+  constexpr int kWin = M1Window<R>() < kLoads ? M1Window<R>() : kLoads;
   uint4 w[R][CPL];
+  int row_off[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = __builtin_amdgcn_readfirstlane(row0 + min(wr0 + r, rows - 1));
+  for (int r = 0; r < R; ++r)
+    row_off[r] = __builtin_amdgcn_readfirstlane(row0 + min(wr0 + r, rows - 1)) * row_bytes;
+  auto issue = [&](int j) __attribute__((always_inline)) {
+    const int i = j / R, r = j % R;
+    const int c = FULL ? lane + 64 * i : min(lane + 64 * i, nchunks - 1);
+    w[r][i] = __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, c * 16, row_off[r], kNonTemporal));
+  };
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = FULL ? lane + 64 * i : min(lane + 64 * i, nchunks - 1);
-      w[r][i] = __builtin_bit_cast(
-          uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, c * 16, row * row_bytes, kNonTemporal));
-    }
-  }
+  for (int j = 0; j < kWin; ++j) issue(j);
 
   __builtin_amdgcn_sched_barrier(0);
 
@@ -245,7 +261,17 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
           const float2 sz = pr[r * nb + blk];
           acc[r] = fmaf(sz.x, fmaf(-sz.y, asum, d), acc[r]);
         }
+        // The load kWin places later in the order, issued here, behind this
+        // dot product: a wavefront whose loads cannot issue (the memory
+        // pipeline is full) is then still doing arithmetic on data that has
+        // arrived, instead of stalling in front of all of it.
+        if (i * R + r + kWin < kLoads) issue(i * R + r + kWin);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (i * R + r + kWin < kLoads) issue(i * R + r + kWin);
     }
   }
 
