@@ -82,18 +82,24 @@ int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float 
 int mnb_plan_destroy(mnb_plan *plan);
 
 /* Device workspace (16-byte aligned) that mnb_run and mnb_run_path need for M
- * rows, whichever path serves them (0 when none). Only the prefill GEMM uses
- * it: A rounded to fp16 in its tile layout, ceil(M/128)*128*K*2 bytes, then,
- * when the GEMM splits K into S > 1 parts, (S - 1)*M*N*4 bytes of fp32
- * partial sums (S <= 16, chosen from the shape). */
+ * rows, whichever path serves them (0 when none): the larger of
+ *  - the prefill GEMM's: A rounded to fp16 in its tile layout,
+ *    ceil(M/128)*128*K*2 bytes, then, when the GEMM splits K into S > 1
+ *    parts, (S - 1)*M*N*4 bytes of fp32 partial sums (S <= 16, chosen from
+ *    the shape);
+ *  - for 5 <= M <= 16, the MFMA decode kernel's: (K/512 - 1)*M*N*4 bytes of
+ *    fp32 partial sums of its 512-k ranges.
+ * Without it (NULL or smaller) the decode path runs its fp32-FMA kernels. */
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
 
 /* Y = MatMulNBits(A, plan) for M rows; dA and dY are device pointers on the
  * plan's device. M == 0 is a no-op. Replaces the operator's compute call,
  * MatMulKernel::operator() -> MatMulPlan<float>::Execute
  * (onnx_light_cpu/kernels/math/matmul_kernel.cc:117-134, gemm_plan.cc:539-570).
- * M <= 16: fp32-FMA decode GEMV; M > 16: fp16-MFMA prefill GEMM with A
- * rounded to fp16 (round to nearest even, half_conversion.h:42-78) and fp32
+ * M <= 4: fp32-FMA decode GEMV; 5 <= M <= 16: decode GEMV on fp16 MFMA with
+ * exact products (A split into three fp16 terms after a power-of-two
+ * scaling) and fp32 sums; M > 16: fp16-MFMA prefill GEMM with A rounded to
+ * fp16 (round to nearest even, half_conversion.h:42-78) and fp32
  * accumulation. The launch is asynchronous on `stream`. */
 int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
             size_t workspace_bytes, void *stream);

@@ -217,7 +217,7 @@ class MatMulNBits:
     def workspace(self, M: int, device, path: int = PATH_AUTO):
         """Device workspace for M rows, kept and grown across calls (not during capture)."""
         import torch
-        need = self.workspace_bytes(M) if path in (PATH_AUTO, PATH_GEMM) else 0
+        need = self.workspace_bytes(M) if path != PATH_GENERIC else 0
         if need == 0:
             return None
         if self._work is None or self._work.numel() < need or self._work.device != device:

@@ -9,6 +9,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -231,12 +232,30 @@ int mnb_plan_destroy(mnb_plan *plan) {
   return MNB_OK;
 }
 
+// Rows from which the decode path multiplies on MFMA (when the caller passes
+// the workspace): below it the fp32-FMA kernels are faster, their cost
+// growing with M while the MFMA kernel's barely does.
+constexpr int64_t kMfmaDecodeMinRows = 5;
+
+static bool UsesMfmaDecode(const mnb_plan *plan, int64_t M) {
+  return M >= kMfmaDecodeMinRows && M <= 16 && mnb::GemvMfmaSupports(plan->view, M);
+}
+
+static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
+  return need == 0 ||
+         (work != nullptr && bytes >= need && (reinterpret_cast<uintptr_t>(work) % 16) == 0);
+}
+
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
   if (plan == nullptr || bytes == nullptr) return MNB_ERR_NULL_POINTER;
   if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
-  // Only the prefill GEMM uses a workspace (A rounded to fp16, tile layout);
-  // the size covers every path mnb_run_path may be asked to take for M rows.
-  *bytes = (M > 0 && mnb::GemmSupports(plan->view, M)) ? mnb::GemmWorkspaceBytes(plan->view, M) : 0;
+  // The size covers every path mnb_run_path may be asked to take for M rows:
+  // the prefill GEMM (A rounded to fp16, tile layout, split-K partial sums)
+  // and the MFMA decode kernel (split-K partial sums).
+  size_t need = 0;
+  if (M > 0 && mnb::GemmSupports(plan->view, M)) need = mnb::GemmWorkspaceBytes(plan->view, M);
+  if (UsesMfmaDecode(plan, M)) need = std::max(need, mnb::GemvMfmaWorkspaceBytes(plan->view, M));
+  *bytes = need;
   return MNB_OK;
 }
 
@@ -286,6 +305,9 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
   case 1:
     if (M == 1 && mnb::GemvM1Supports(plan->view))
       e = mnb::LaunchGemvM1(plan->view, dA, dY, s, 0, 0);
+    else if (UsesMfmaDecode(plan, M) && HasWorkspace(dWorkspace, workspace_bytes,
+                                                      mnb::GemvMfmaWorkspaceBytes(plan->view, M)))
+      e = mnb::LaunchGemvMfma(plan->view, M, dA, dY, dWorkspace, s);
     else if (mnb::GemvSmallMSupports(plan->view, M))
       e = mnb::LaunchGemvSmallM(plan->view, M, dA, dY, s);
     else

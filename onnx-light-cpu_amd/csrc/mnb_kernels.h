@@ -68,6 +68,19 @@ hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream
                         int band_rows, int rows_per_wave);
 bool GemvM1Supports(const WeightView &w);
 
+// Decode GEMV for 2 <= M <= 16 on fp16 MFMA with exact products (each
+// activation split into three fp16 terms after a power-of-two scaling); K a
+// multiple of 512 (at most 32768), power-of-two block_size >= 32. `work`
+// holds GemvMfmaWorkspaceBytes(w, M) bytes: the partial sums of K ranges 1..
+hipError_t LaunchGemvMfma(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                          hipStream_t s);
+bool GemvMfmaSupports(const WeightView &w, int64_t M);
+size_t GemvMfmaWorkspaceBytes(const WeightView &w, int64_t M);
+// Same with an explicit shape (tuning): 16-row blocks per item (1 or 2) and
+// workgroups per CU; 0 picks.
+hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, float *Y,
+                               void *work, hipStream_t s, int rows_per_wave, int wgs_per_cu);
+
 // Prefill GEMM on fp16 MFMA, any M, K % 64 == 0, block_size >= 32. `work`
 // holds GemmWorkspaceBytes(w, M) bytes of device memory: A rounded to fp16,
 // then the partial sums of a split-K launch.
