@@ -403,24 +403,44 @@ __global__ __launch_bounds__(64 * kWaves) void GemvMfmaKernel(
   }
 }
 
-// Y += P[0] + P[1] + ... + P[parts - 1], added in that order; loads issued
-// eight at a time.
+// Y += P[0] + P[1] + ... + P[parts - 1], added in that order. VEC: four
+// consecutive outputs per thread (Y, P 16-byte aligned, M N % 4 == 0); the
+// parts' loads are issued sixteen at a time.
+template <bool VEC>
 __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
                                                          const float *__restrict__ P, int64_t mn,
                                                          int parts) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= mn) return;
-  float y = Y[i];
-  int p = 0;
-  for (; p + 8 <= parts; p += 8) {
-    float v[8];
+  constexpr int kBatch = 16;
+  if constexpr (VEC) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= mn) return;
+    floatx4 y = *reinterpret_cast<const floatx4 *>(Y + i);
+    for (int p = 0; p < parts; p += kBatch) {
+      floatx4 v[kBatch];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) v[q] = __builtin_nontemporal_load(P + (p + q) * mn + i);
+      for (int q = 0; q < kBatch; ++q)
+        if (p + q < parts)
+          v[q] = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(P + (p + q) * mn + i));
 #pragma unroll
-    for (int q = 0; q < 8; ++q) y += v[q];
+      for (int q = 0; q < kBatch; ++q)
+        if (p + q < parts) y += v[q];
+    }
+    *reinterpret_cast<floatx4 *>(Y + i) = y;
+  } else {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= mn) return;
+    float y = Y[i];
+    for (int p = 0; p < parts; p += kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q)
+        if (p + q < parts) v[q] = __builtin_nontemporal_load(P + (p + q) * mn + i);
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q)
+        if (p + q < parts) y += v[q];
+    }
+    Y[i] = y;
   }
-  for (; p < parts; ++p) y += __builtin_nontemporal_load(P + p * mn + i);
-  Y[i] = y;
 }
 
 struct Shape {
@@ -506,8 +526,15 @@ hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, f
   }
   if (e != hipSuccess || sh.splits == 1) return e;
   const int64_t mn = M * w.N;
-  hipLaunchKernelGGL(mf::SumPartialsKernel, dim3(static_cast<unsigned>((mn + 255) / 256)),
-                     dim3(256), 0, s, Y, P, mn, sh.splits - 1);
+  const bool vec = (mn % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0 &&
+                   (reinterpret_cast<uintptr_t>(P) % 16) == 0;
+  if (vec)
+    hipLaunchKernelGGL(mf::SumPartialsKernel<true>,
+                       dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s, Y, P,
+                       mn, sh.splits - 1);
+  else
+    hipLaunchKernelGGL(mf::SumPartialsKernel<false>, dim3(static_cast<unsigned>((mn + 255) / 256)),
+                       dim3(256), 0, s, Y, P, mn, sh.splits - 1);
   return hipGetLastError();
 }
 
