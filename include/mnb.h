@@ -110,6 +110,14 @@ int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *d
 int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
                  size_t workspace_bytes, void *stream, int path);
 
+/* Same as mnb_run_path, plus MatMulNBits' optional input 5: dBias, fp32 [N]
+ * in device memory (NULL = absent), added to every row of Y:
+ * Y = A * W^T + bias. Replaces the bias input the reference's operator
+ * wrappers read as an optional input (integer_matmul_kernel.cc:375-376,
+ * GetInput returning null when absent). */
+int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dBias, float *dY,
+               void *dWorkspace, size_t workspace_bytes, void *stream, int path);
+
 /* Which path mnb_run takes for M rows (1, 2 or 3 as in mnb_run_path). */
 int mnb_select_path(const mnb_plan *plan, int64_t M, int *path);
 
@@ -123,6 +131,29 @@ const char *mnb_last_error(void);
  * (packed B + fp32 scales + packed zero points): the algorithmic weight
  * bytes of one launch. */
 int mnb_weight_bytes(const mnb_desc *desc, size_t *bytes);
+
+/* QDQ front-end: repacks a constant weight-only DequantizeLinear feeding
+ * MatMul(A, W) -- W[K, N] = DequantizeLinear(x, x_scale, x_zero_point) with
+ * blocked quantization along axis 0 (K), the roadmap's qwen3-int4-qdq export
+ * contract (docs/next_steps/2026/2026_08_qwen3_inference.rst:96-101, 262) --
+ * into MatMulNBits inputs on the host, without forming any float weight:
+ *   x            INT4 (is_signed = 1) or UINT4 [K, N], ONNX packing: element
+ *                i of the row-major flattening is nibble i & 1 of byte i / 2,
+ *                low nibble first, signed nibbles two's complement
+ *                (onnx_light_cpu/impl/math/gemm/vnni/integer_gemm_vnni.h:42-47,
+ *                ReadPacked4Bit integer_gemm_vnni.cc:60-65)
+ *   x_scale      fp32 [ceil(K / block_size), N]
+ *   x_zero_point same type and packing as x, [ceil(K / block_size), N], or
+ *                NULL (ONNX default 0)
+ * Outputs (caller-allocated, host memory): B [N, nb, block_size/2] (padding
+ * nibbles past K are 0), scales [N, nb], zero_points [N, ceil(nb/2)], and
+ * *has_zero_points: 0 when every zero point is the MatMulNBits default 8
+ * (INT4 without x_zero_point; zero_points is then left untouched), else 1.
+ * A signed nibble x maps to x + 8 and its zero point z to z + 8, so
+ * (x - z) is unchanged. block_size must be a power of two >= 16. */
+int mnb_qdq_repack(int64_t K, int64_t N, int32_t block_size, int32_t is_signed,
+                   const uint8_t *x, const float *x_scale, const uint8_t *x_zero_point,
+                   uint8_t *B, float *scales, uint8_t *zero_points, int32_t *has_zero_points);
 
 /* Library version string. */
 const char *mnb_version(void);

@@ -61,6 +61,10 @@ def library():
         L.mnb_workspace_bytes.argtypes = [vp, i64, ctypes.POINTER(sz)]
         L.mnb_run.argtypes = [vp, i64, vp, vp, vp, sz, vp]
         L.mnb_run_path.argtypes = [vp, i64, vp, vp, vp, sz, vp, ctypes.c_int]
+        L.mnb_run_ex.argtypes = [vp, i64, vp, vp, vp, vp, sz, vp, ctypes.c_int]
+        i32 = ctypes.c_int32
+        L.mnb_qdq_repack.argtypes = [i64, i64, i32, i32, vp, vp, vp, vp, vp, vp,
+                                     ctypes.POINTER(i32)]
         L.mnb_select_path.argtypes = [vp, i64, ctypes.POINTER(ctypes.c_int)]
         L.mnb_status_str.argtypes = [ctypes.c_int]
         L.mnb_status_str.restype = ctypes.c_char_p
@@ -69,7 +73,7 @@ def library():
         L.mnb_version.restype = ctypes.c_char_p
         for name in ("mnb_plan_create", "mnb_plan_create_device", "mnb_plan_destroy",
                      "mnb_workspace_bytes", "mnb_run", "mnb_run_path", "mnb_select_path",
-                     "mnb_weight_bytes"):
+                     "mnb_weight_bytes", "mnb_run_ex", "mnb_qdq_repack"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib
@@ -113,7 +117,7 @@ class MatMulNBits:
 
     Mirrors the operator contract of ONNX Runtime's com.microsoft::MatMulNBits
     (attributes K, N, bits, block_size, accuracy_level; inputs A, B, scales,
-    zero_points). ``g_idx`` and ``bias`` inputs are rejected.
+    zero_points, bias). The ``g_idx`` input is rejected.
     """
 
     domain = "com.microsoft"
@@ -185,7 +189,16 @@ class MatMulNBits:
         _check(library().mnb_select_path(self._plan, M, ctypes.byref(p)), "select_path")
         return p.value
 
-    def __call__(self, A, out=None, path: int = PATH_AUTO, stream=None):
+    @classmethod
+    def from_qdq(cls, x, x_scale, x_zero_point=None, *, K: int, N: int, signed: bool,
+                 block_size: int = 0, axis=None, accuracy_level: int = 0):
+        """The MatMulNBits node for MatMul(A, DequantizeLinear(x, x_scale,
+        x_zero_point)) with constant weights (see qdq_to_matmul_nbits), prepared."""
+        attrs, B, S, Z = qdq_to_matmul_nbits(x, x_scale, x_zero_point, K=K, N=N, signed=signed,
+                                             block_size=block_size, axis=axis)
+        return cls(K, N, 4, attrs["block_size"], accuracy_level).prepare(B, S, Z)
+
+    def __call__(self, A, out=None, path: int = PATH_AUTO, stream=None, bias=None):
         """Y[..., M, N] = A[..., M, K] * W^T on A's device (a torch CUDA tensor)."""
         import torch
         if not self._plan:
@@ -202,10 +215,12 @@ class MatMulNBits:
         if not out.is_contiguous() or out.numel() != M * self.desc.N:
             raise ValueError(f"{KERNEL_PREFIX}: out must be contiguous [..., M, N]")
         s = stream if stream is not None else torch.cuda.current_stream(A.device)
+        if bias is not None and (bias.numel() != self.desc.N or not bias.is_contiguous()):
+            raise ValueError(f"{KERNEL_PREFIX}: bias must be a contiguous [N] tensor")
         work = self.workspace(M, A.device, path)
-        _check(library().mnb_run_path(self._plan, M, _dev_ptr(A2), _dev_ptr(out),
-                                      _dev_ptr(work), 0 if work is None else work.numel(),
-                                      ctypes.c_void_p(s.cuda_stream), path),
+        _check(library().mnb_run_ex(self._plan, M, _dev_ptr(A2), _dev_ptr(bias), _dev_ptr(out),
+                                    _dev_ptr(work), 0 if work is None else work.numel(),
+                                    ctypes.c_void_p(s.cuda_stream), path),
                "run")
         return out
 
@@ -239,6 +254,39 @@ def weight_bytes(K, N, block_size, has_zero_points, bits=4) -> int:
 _host = None
 
 
+def qdq_to_matmul_nbits(x, x_scale, x_zero_point=None, *, K: int, N: int, signed: bool,
+                        block_size: int = 0, axis=None):
+    """Constant DequantizeLinear -> MatMul weight as MatMulNBits inputs.
+
+    x: uint8 array, the ONNX packing of an INT4 (signed) or UINT4 [K, N] tensor
+    (low nibble first); x_scale: float32 [ceil(K/block_size), N] (blocked along
+    K, axis 0), [N] (per column, axis 1) or one value; x_zero_point: packed
+    like x with x_scale's shape, or None. Runs the C++ recognizer
+    (host/qdq_matmul.cc) over the C ABI's mnb_qdq_repack. Returns
+    (attributes, B, scales, zero_points or None).
+    """
+    import numpy as np
+    H = host_library()
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    sc = np.ascontiguousarray(x_scale, dtype=np.float32)
+    zp = None if x_zero_point is None else np.ascontiguousarray(x_zero_point, dtype=np.uint8)
+    bs_out = block_size if block_size > 0 else K
+    nb = -(-K // bs_out)
+    B = np.empty((N, nb, bs_out // 2), np.uint8)
+    S = np.empty((N, nb), np.float32)
+    Z = np.empty((N, (nb + 1) // 2), np.uint8)
+    dims = (ctypes.c_int64 * max(1, sc.ndim))(*sc.shape)
+    out_bs = ctypes.c_int64()
+    has_zp = ctypes.c_int()
+    _host_check(H.olc_amd_dequantize_linear_to_matmul_nbits(
+        22 if signed else 21, K, N, _host_ptr(x), _host_ptr(sc), sc.ndim, dims, _host_ptr(zp),
+        0 if axis is None else 1, 0 if axis is None else axis, block_size,
+        ctypes.byref(out_bs), _host_ptr(B), B.size, _host_ptr(S), S.size, _host_ptr(Z), Z.size,
+        ctypes.byref(has_zp)))
+    attrs = {"K": K, "N": N, "bits": 4, "block_size": out_bs.value}
+    return attrs, B, S, (Z if has_zp.value else None)
+
+
 def host_library():
     """Loads libolc_amd.so, the C++ registration boundary and operator adapter."""
     global _host
@@ -263,6 +311,11 @@ def host_library():
                                        ctypes.POINTER(vp), i32p, i32p, i32p, i64p, vp,
                                        ctypes.c_int64, vp]
         H.olc_amd_run_node.restype = ctypes.c_int
+        H.olc_amd_dequantize_linear_to_matmul_nbits.argtypes = [
+            ctypes.c_int, ctypes.c_int64, ctypes.c_int64, vp, vp, ctypes.c_int, i64p, vp,
+            ctypes.c_int, ctypes.c_int64, ctypes.c_int64, i64p, vp, ctypes.c_size_t, vp,
+            ctypes.c_size_t, vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int)]
+        H.olc_amd_dequantize_linear_to_matmul_nbits.restype = ctypes.c_int
         _host = H
     return _host
 

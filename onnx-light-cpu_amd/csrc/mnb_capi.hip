@@ -128,6 +128,24 @@ int CheckInputs(const mnb_desc *desc, const void *B, const void *scales, const v
 
 } // namespace
 
+// Y[m][n] += bias[n]: MatMulNBits' optional bias input, an epilogue over the
+// finished Y on the same stream (every path's kernels have completed their
+// writes of Y when it starts).
+__global__ __launch_bounds__(256) void AddBiasKernel(float *__restrict__ Y,
+                                                     const float *__restrict__ bias, int64_t mn,
+                                                     int64_t N) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < mn) Y[i] += bias[i % N];
+}
+
+static hipError_t LaunchAddBias(float *Y, const float *bias, int64_t M, int64_t N,
+                                hipStream_t s) {
+  const int64_t mn = M * N;
+  hipLaunchKernelGGL(AddBiasKernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0,
+                     s, Y, bias, mn, N);
+  return hipGetLastError();
+}
+
 extern "C" {
 
 const char *mnb_version(void) { return "mnb-gfx950 0.1.0"; }
@@ -274,8 +292,8 @@ int mnb_select_path(const mnb_plan *plan, int64_t M, int *path) {
   return MNB_OK;
 }
 
-int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
-                 size_t workspace_bytes, void *stream, int path) {
+int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dBias, float *dY,
+               void *dWorkspace, size_t workspace_bytes, void *stream, int path) {
   if (plan == nullptr) return MNB_ERR_NULL_POINTER;
   if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
   if (M == 0) return MNB_OK;
@@ -316,6 +334,7 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
   case 2: e = mnb::LaunchGemm(plan->view, M, dA, dY, dWorkspace, s); break;
   default: e = mnb::LaunchGeneric(plan->view, M, dA, dY, s); break;
   }
+  if (e == hipSuccess && dBias != nullptr) e = LaunchAddBias(dY, dBias, M, plan->view.N, s);
   if (e != hipSuccess) {
     SetLastError("kernel launch", e);
     return MNB_ERR_HIP;
@@ -323,9 +342,14 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
   return MNB_OK;
 }
 
+int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
+                 size_t workspace_bytes, void *stream, int path) {
+  return mnb_run_ex(plan, M, dA, nullptr, dY, dWorkspace, workspace_bytes, stream, path);
+}
+
 int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
             size_t workspace_bytes, void *stream) {
-  return mnb_run_path(plan, M, dA, dY, dWorkspace, workspace_bytes, stream, 0);
+  return mnb_run_ex(plan, M, dA, nullptr, dY, dWorkspace, workspace_bytes, stream, 0);
 }
 
 } // extern "C"

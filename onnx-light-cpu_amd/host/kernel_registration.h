@@ -32,7 +32,7 @@ enum class Device : int32_t { kUndefined = 0, kCPU = 1, kGPU = 2 };
 
 // TensorProto::DataType values used by this operator.
 enum class DataType : int32_t { kUndefined = 0, kFloat = 1, kUint8 = 2, kInt32 = 6,
-                                kFloat16 = 10 };
+                                kFloat16 = 10, kUint4 = 21, kInt4 = 22 };
 
 // A borrowed tensor: pointer, element type, shape and the memory it lives in.
 struct TensorView {

@@ -99,7 +99,7 @@ void MatMulNBitsKernel::EnsurePlan(const TensorView &b, const TensorView &scales
 
 void MatMulNBitsKernel::operator()(const TensorView &a, const TensorView &b,
                                    const TensorView &scales, const TensorView *zero_points,
-                                   TensorView &y, void *stream) {
+                                   TensorView &y, void *stream, const TensorView *bias) {
   const int64_t K = desc_.K, N = desc_.N, bs = desc_.block_size;
   const int64_t nb = (K + bs - 1) / bs;
   if (a.type != DataType::kFloat) Fail("input A must be float");
@@ -118,12 +118,16 @@ void MatMulNBitsKernel::operator()(const TensorView &a, const TensorView &b,
   if (zero_points && zero_points->numel() != N * ((nb + 1) / 2))
     Fail("zero_points must have N*ceil(n_blocks/2) = " + std::to_string(N * ((nb + 1) / 2)) +
          " bytes");
+  if (bias && bias->type != DataType::kFloat) Fail("input bias must be float");
+  if (bias && bias->numel() != N) Fail("bias must have N=" + std::to_string(N) + " elements");
+  if (bias && bias->device != Device::kGPU) Fail("bias must be in device memory");
   EnsurePlan(b, scales, zero_points);
   const int64_t M = a.numel() / K;
   void *work = Workspace(M);
-  CheckStatus(mnb_run(plan_, M, static_cast<const float *>(a.data), static_cast<float *>(y.data),
-                      work, work_bytes_, stream),
-              "mnb_run");
+  CheckStatus(mnb_run_ex(plan_, M, static_cast<const float *>(a.data),
+                         bias ? static_cast<const float *>(bias->data) : nullptr,
+                         static_cast<float *>(y.data), work, work_bytes_, stream, 0),
+              "mnb_run_ex");
 }
 
 void MatMulNBitsKernel::Run(RuntimeContext &rt) {
@@ -136,12 +140,12 @@ void MatMulNBitsKernel::Run(RuntimeContext &rt) {
   const TensorView *zp = rt.GetInput(3);
   if (!a || !b || !scales) Fail("inputs A, B and scales are required");
   if (rt.GetInput(4)) Fail("input g_idx is not supported");
-  if (rt.GetInput(5)) Fail("input bias is not supported");
+  const TensorView *bias = rt.GetInput(5);
   std::vector<int64_t> shape = a->shape;
   if (shape.empty()) Fail("A must have rank >= 1");
   shape.back() = desc_.N;
   TensorView &y = rt.MakeOutputTensor(0, DataType::kFloat, shape);
-  (*this)(*a, *b, *scales, zp, y, rt.stream);
+  (*this)(*a, *b, *scales, zp, y, rt.stream, bias);
 }
 
 void RegisterMatMulNBitsKernel() {

@@ -26,11 +26,13 @@ public:
 
   void Run(RuntimeContext &rt) override;
 
-  // Y = A * W^T for device tensors. B/scales/zero_points are the node's
-  // constant initializers: the device plan is prepared on first use and
-  // reused while the same buffers are passed.
+  // Y = A * W^T (+ bias) for device tensors. B/scales/zero_points are the
+  // node's constant initializers: the device plan is prepared on first use
+  // and reused while the same buffers are passed. bias (input 5) is fp32 [N]
+  // in device memory, or null.
   void operator()(const TensorView &a, const TensorView &b, const TensorView &scales,
-                  const TensorView *zero_points, TensorView &y, void *stream);
+                  const TensorView *zero_points, TensorView &y, void *stream,
+                  const TensorView *bias = nullptr);
 
   const mnb_desc &desc() const { return desc_; }
 

@@ -4,6 +4,7 @@
 // table the way onnx-light's RunNode would. Exceptions never cross this
 // boundary: failures return -1 and leave a message for olc_amd_last_error().
 #include "kernel_registration.h"
+#include "qdq_matmul.h"
 #include "register_kernels.h"
 
 #include <algorithm>
@@ -155,6 +156,46 @@ int olc_amd_run_node(const char *domain, const char *op_type, int device, int n_
     rt.outputs.push_back(y);
     std::unique_ptr<KernelBase> kernel = fn(attrs, rt);
     kernel->Run(rt);
+  });
+}
+
+// DequantizeLinearToMatMulNBits for the Python mirror: x is INT4 (x_type 22)
+// or UINT4 (21) [K, N], x_scale fp32 with scale_rank dims, x_zero_point of
+// x's type or NULL; axis_set = 0 means the ONNX default axis. Outputs go to
+// caller buffers of the given capacities (elements); *out_block_size and
+// *has_zero_points describe the MatMulNBits node.
+int olc_amd_dequantize_linear_to_matmul_nbits(
+    int x_type, int64_t K, int64_t N, const uint8_t *x, const float *x_scale, int scale_rank,
+    const int64_t *scale_dims, const uint8_t *x_zero_point, int axis_set, int64_t axis,
+    int64_t block_size, int64_t *out_block_size, uint8_t *B, size_t B_cap, float *scales,
+    size_t scales_cap, uint8_t *zero_points, size_t zero_points_cap, int *has_zero_points) {
+  return Guard([&] {
+    DequantizeLinearWeight w;
+    w.x.data = const_cast<uint8_t *>(x);
+    w.x.type = static_cast<DataType>(x_type);
+    w.x.shape = {K, N};
+    w.x.device = Device::kCPU;
+    w.x_scale.data = const_cast<float *>(x_scale);
+    w.x_scale.type = DataType::kFloat;
+    w.x_scale.shape.assign(scale_dims, scale_dims + scale_rank);
+    w.x_scale.device = Device::kCPU;
+    if (x_zero_point != nullptr) {
+      TensorView z = w.x_scale;
+      z.data = const_cast<uint8_t *>(x_zero_point);
+      z.type = w.x.type;
+      w.x_zero_point = z;
+    }
+    if (axis_set) w.attrs.ints["axis"] = axis;
+    if (block_size > 0) w.attrs.ints["block_size"] = block_size;
+    MatMulNBitsWeights m = DequantizeLinearToMatMulNBits(w);
+    if (m.B.size() > B_cap || m.scales.size() > scales_cap ||
+        m.zero_points.size() > zero_points_cap)
+      throw std::invalid_argument("olc_amd_dequantize_linear_to_matmul_nbits: buffer too small");
+    std::copy(m.B.begin(), m.B.end(), B);
+    std::copy(m.scales.begin(), m.scales.end(), scales);
+    std::copy(m.zero_points.begin(), m.zero_points.end(), zero_points);
+    *out_block_size = *m.attrs.GetInt("block_size");
+    *has_zero_points = m.zero_points.empty() ? 0 : 1;
   });
 }
 

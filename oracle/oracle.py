@@ -139,6 +139,46 @@ def dequantize(B, scales, zp, K, N, bs):
     return W
 
 
+def dequantize_linear_4bit(x_packed, K, N, signed, scale, zp=None, block_size=0, axis=None):
+    """ONNX DequantizeLinear of a constant 4-bit MatMul weight: W [K, N] float32.
+
+    Restates the ONNX operator (opset 21 blocked quantization): element (k, n)
+    of x is element k*N + n of the row-major flattening, nibble (i & 1) of
+    byte i // 2, low nibble first, signed nibbles two's complement -- the
+    packing the reference's ReadPacked4Bit reads
+    (onnx_light_cpu/impl/math/gemm/vnni/integer_gemm_vnni.h:42-47, .cc:60-65).
+    y = (x - zero_point) * scale, with the scale (and zero point) of element
+    (k, n) at [k // block_size, n] when block_size > 0 (axis 0), at [n] for
+    per-axis scales along axis 1, or the single value of a per-tensor scale;
+    an absent zero point is 0. Plain numpy, one element at a time in effect.
+    """
+    xb = np.asarray(x_packed, np.uint8).ravel()
+    idx = np.arange(K * N)
+    q = ((xb[idx >> 1] >> ((idx & 1) * 4)) & 0xF).astype(np.int64)
+    if signed:
+        q = np.where(q >= 8, q - 16, q)
+    q = q.reshape(K, N)
+    sc = np.asarray(scale, np.float32)
+    if zp is not None:
+        zb = np.asarray(zp, np.uint8).ravel()
+        zi = np.arange(sc.size)
+        z = ((zb[zi >> 1] >> ((zi & 1) * 4)) & 0xF).astype(np.int64)
+        if signed:
+            z = np.where(z >= 8, z - 16, z)
+        z = z.reshape(sc.shape)
+    else:
+        z = np.zeros(sc.shape, np.int64)
+    if block_size > 0:
+        rows = np.arange(K) // block_size
+        s_full, z_full = sc[rows, :], z[rows, :]
+    elif sc.size == N and sc.ndim == 1:
+        s_full, z_full = np.broadcast_to(sc, (K, N)), np.broadcast_to(z, (K, N))
+    else:
+        s_full = np.full((K, N), sc.ravel()[0], np.float32)
+        z_full = np.full((K, N), z.ravel()[0], np.int64)
+    return ((q - z_full).astype(np.float32) * s_full).astype(np.float32)
+
+
 def f32_to_f16_bits(x):
     x = np.ascontiguousarray(x, dtype=np.float32).ravel()
     out = np.empty(x.size, np.uint16)

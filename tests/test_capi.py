@@ -18,8 +18,8 @@ def test_library_exports_every_header_function(pkg):
     names = pkg.header_functions()
     assert names == sorted([
         "mnb_plan_create", "mnb_plan_create_device", "mnb_plan_destroy", "mnb_workspace_bytes",
-        "mnb_run", "mnb_run_path", "mnb_select_path", "mnb_status_str", "mnb_last_error",
-        "mnb_weight_bytes", "mnb_version"])
+        "mnb_run", "mnb_run_path", "mnb_run_ex", "mnb_select_path", "mnb_status_str",
+        "mnb_last_error", "mnb_weight_bytes", "mnb_version", "mnb_qdq_repack"])
     for name in names:
         assert hasattr(L, name), name
 
@@ -93,6 +93,7 @@ def test_run_and_queries_reject_null_plan(pkg):
     p = ctypes.c_int()
     assert L.mnb_run(None, 1, None, None, None, 0, None) == NULLP
     assert L.mnb_run_path(None, 1, None, None, None, 0, None, 1) == NULLP
+    assert L.mnb_run_ex(None, 1, None, None, None, None, 0, None, 1) == NULLP
     assert L.mnb_workspace_bytes(None, 1, ctypes.byref(x)) == NULLP
     assert L.mnb_select_path(None, 1, ctypes.byref(p)) == NULLP
     assert L.mnb_plan_destroy(None) == MNB_OK

@@ -41,7 +41,7 @@ def _run(pkg, attrs, inputs, out=None):
 ATTRS = {"K": 64, "N": 8, "bits": 4, "block_size": 32}
 
 
-def _inputs(pkg, a_type=1, b_type=2, s_type=1, zp=None, g_idx=False, bias=False, n_b=8 * 32):
+def _inputs(pkg, a_type=1, b_type=2, s_type=1, zp=None, g_idx=False, bias=None, n_b=8 * 32):
     # device pointers are never dereferenced: every case fails validation first
     dev = pkg.DEVICE_GPU
     ins = [(0x1000, a_type, dev, [1, 64]), (0x2000, b_type, dev, [n_b]),
@@ -51,7 +51,7 @@ def _inputs(pkg, a_type=1, b_type=2, s_type=1, zp=None, g_idx=False, bias=False,
     if g_idx or bias:
         ins.append((0x5000, 6, dev, [64]) if g_idx else (None, 6, dev, [0]))
     if bias:
-        ins.append((0x6000, 1, dev, [8]))
+        ins.append(bias)
     return ins
 
 
@@ -73,7 +73,9 @@ def test_adapter_attribute_errors(pkg, attrs, msg):
     ({"s_type": 10}, "input scales must be float"),
     ({"n_b": 7}, "B must have"),
     ({"g_idx": True}, "input g_idx is not supported"),
-    ({"bias": True}, "input bias is not supported"),
+    ({"bias": (0x6000, 6, 2, [8])}, "input bias must be float"),
+    ({"bias": (0x6000, 1, 2, [7])}, "bias must have N=8 elements"),
+    ({"bias": (0x6000, 1, 1, [8])}, "bias must be in device memory"),
     ({"zp": (0x4000, 1, 2, [8])}, "zero_points must be uint8"),
     ({"zp": (0x4000, 2, 2, [3])}, "zero_points must have"),
 ])
