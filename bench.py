@@ -40,12 +40,12 @@ METRIC = "MatMulNBits 4-bit: M=1 achieved HBM GB/s; M=2048 TFLOP/s; % roofline"
 ROTATION_BYTES = 1 << 30
 
 # HBM bytes per launch of the headline kernel (GemvM1Kernel on c2 M=1), from
-# two rocprofv3 --pmc passes over `bench.py --only decode,gemm,copy --eager
-# --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15525.7 KiB and WRITE_SIZE
-# 80.0 KiB per dispatch, each scaled by what the same counter reads for the
-# copy leg's 512 MiB device copy (FETCH_SIZE 262156.7 KiB -> x1.99990,
+# two rocprofv3 --pmc passes over `bench.py --only decode,gemm,sweep,copy
+# --eager --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15524.7 KiB and
+# WRITE_SIZE 80.0 KiB per dispatch, each scaled by what the same counter reads
+# for the copy leg's 512 MiB device copy (FETCH_SIZE 262157.1 KiB -> x1.99990,
 # WRITE_SIZE 524288.0 KiB -> x1.00000). Re-measure when the kernel changes.
-GEMV_M1_C2_TRAFFIC_BYTES = round((15525.7 * (524288.0 / 262156.7) + 80.0) * 1024)
+GEMV_M1_C2_TRAFFIC_BYTES = round((15524.7 * (524288.0 / 262157.1) + 80.0) * 1024)
 
 
 def parse_args():
@@ -132,6 +132,18 @@ def copy_leg(torch, dev, steps, warmup, stream):
             "GBps": 2 * n / (ms * 1e-3) / 1e9, "wall_s": wall}
 
 
+def decode_kernel(M):
+    """Kernel mnb_run's decode path launches for M rows when the plan's shape
+    qualifies (K a multiple of 512, block_size >= 32, a workspace given; true
+    for c1..c3): fp32-FMA kernels for M <= 4, the exact-product MFMA kernel and
+    its ordered partial-sum pass for 5 <= M <= 16."""
+    if M == 1:
+        return "GemvM1Kernel"
+    if M <= 4:
+        return "GemvSmallMKernel"
+    return "GemvMfmaKernel + SumPartialsKernel"
+
+
 def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
     """One decode shape over >= 1 GiB of rotated weight copies."""
     rot = max(2, -(-ROTATION_BYTES // p.weight_bytes()))
@@ -156,7 +168,8 @@ def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
     torch.cuda.empty_cache()
     return {
         "K": p.K, "N": p.N, "M": M, "block_size": p.block_size,
-        "zero_points": p.has_zero_points, "path": path, "rotation_copies": rot,
+        "zero_points": p.has_zero_points, "path": path, "kernel": decode_kernel(M),
+        "rotation_copies": rot,
         "us_per_launch": per_launch_us, "bytes_per_launch": nbytes,
         "GBps": nbytes / (per_launch_us * 1e-6) / 1e9, "ms_per_step": ms, "wall_s": wall,
         "wall_ms_per_step": wall * 1e3 / steps,
@@ -356,7 +369,8 @@ def main():
             for M in Ms:
                 r = decode_leg(torch, pkg, dev, p, M, max(3, args.steps // 4), 2, 17 + M, stream)
                 r["config"] = cname
-                sweep.append({k: r[k] for k in ("config", "M", "us_per_launch", "GBps", "path")})
+                sweep.append({k: r[k] for k in ("config", "M", "us_per_launch", "GBps", "path",
+                                                 "kernel")})
                 print(f"# decode {cname} M={M}: {r['us_per_launch']:.2f} us, {r['GBps']:.0f} GB/s",
                       file=sys.stderr, flush=True)
     c5 = []
