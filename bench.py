@@ -56,7 +56,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline sampling budget over its four modes (0 disables)")
     ap.add_argument("--only", default="",
-                    help="comma list of legs: decode,gemm,sweep,c5,cpu,copy (default: all but copy)")
+                    help="comma list of legs: decode,gemm,sweep,c5,gate_up,cpu,copy "
+                         "(default: all but copy)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step directly instead of replaying a HIP graph "
                          "(for counter collection, which serialises dispatches)")
@@ -197,6 +198,62 @@ def gemm_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
            "wall_ms_per_step": wall * 1e3 / steps}
     op.release()
     return res
+
+
+def gate_up_leg(torch, pkg, dev, Ms, steps, warmup, stream):
+    """Measured fusion: the c5 gate+up projection (K=4096, two 14336-row
+    weights, bs=128, zero points) as one gate/up plan writing
+    silu(gate) * up, against the unfused graph -- one MatMulNBits over the
+    concatenated [Wg; Wu] rows, then silu(g) * u as torch elementwise ops --
+    and against that MatMulNBits alone. Decode shapes rotate 4 weight copies
+    (0.47 GB per variant), prefill shapes use one."""
+    import numpy as np
+    import torch.nn.functional as F
+    W = pkg.workloads
+    K, I, bs = 4096, 14336, 128
+    p = W.Projection("gate_up", K, I, bs, True, 1.0, 0.005, 0.02)
+    copies = 4 if min(Ms) <= 16 else 1
+    fused, plain = [], []
+    for c in range(copies):
+        Bg, Sg, Zg = W.make_weights(p, 1000 + 2 * c)
+        Bu, Su, Zu = W.make_weights(p, 1001 + 2 * c)
+        fused.append(pkg.GateUpSiLU(K, I, 4, bs).prepare(Bg, Sg, Zg, Bu, Su, Zu))
+        cat = [np.concatenate([x.reshape(I, -1), y.reshape(I, -1)])
+               for x, y in ((Bg, Bu), (Sg, Su), (Zg, Zu))]
+        plain.append(pkg.MatMulNBits(K, 2 * I, 4, bs).prepare(*cat))
+    out = []
+    for M in Ms:
+        n = copies if M <= 16 else 1
+        g = torch.Generator(device=dev)
+        g.manual_seed(29 + M)
+        A = torch.randn((M, K), device=dev, generator=g)
+        H = torch.empty(M, I, device=dev)
+        Y = torch.empty(M, 2 * I, device=dev)
+
+        def run_fused():
+            for op in fused[:n]:
+                op(A, out=H, stream=torch.cuda.current_stream())
+
+        def run_plain():
+            for op in plain[:n]:
+                op(A, out=Y, stream=torch.cuda.current_stream())
+
+        def run_unfused():
+            for op in plain[:n]:
+                op(A, out=Y, stream=torch.cuda.current_stream())
+                torch.mul(F.silu(Y[:, :I]), Y[:, I:], out=H)
+
+        r = {"M": M, "weight_copies": n}
+        for name, fn in (("fused_us", run_fused), ("unfused_us", run_unfused),
+                         ("matmul_only_us", run_plain)):
+            ms, _ = time_graph(torch, fn, steps, warmup, stream)
+            r[name] = ms * 1e3 / n
+        r["gain"] = r["unfused_us"] / r["fused_us"]
+        out.append(r)
+    for op in fused + plain:
+        op.release()
+    torch.cuda.empty_cache()
+    return out
 
 
 def c5_leg(torch, pkg, dev, M, steps, warmup, stream):
@@ -345,7 +402,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(device=dev)
-    legs = set(args.only.split(",")) if args.only else {"decode", "gemm", "sweep", "c5", "cpu"}
+    legs = (set(args.only.split(",")) if args.only
+            else {"decode", "gemm", "sweep", "c5", "gate_up", "cpu"})
     W = pkg.workloads
 
     t_start = time.perf_counter()
@@ -380,6 +438,14 @@ def main():
             c5.append(r)
             print(f"# c5 32 layers M={M}: {r['ms_per_step']:.3f} ms/step, {r['GBps']:.0f} GB/s, "
                   f"{r['TFLOPs']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    gate_up = []
+    if "gate_up" in legs:
+        gate_up = gate_up_leg(torch, pkg, dev, (1, 16, 512, 2048), max(3, args.steps // 4), 2,
+                              stream)
+        for r in gate_up:
+            print(f"# gate/up + SiLU M={r['M']}: fused {r['fused_us']:.1f} us, unfused "
+                  f"{r['unfused_us']:.1f} us ({r['gain']:.2f}x), matmul alone "
+                  f"{r['matmul_only_us']:.1f} us", file=sys.stderr, flush=True)
     copy = None
     if "copy" in legs:
         copy = copy_leg(torch, dev, args.steps, args.warmup, stream)
@@ -416,6 +482,7 @@ def main():
         "prefill_gemm": gemm,
         "decode_sweep": sweep,
         "c5_layer_stack": c5,
+        "gate_up_fusion": gate_up,
         "copy_calibration": copy,
         "timing": "eager launches" if EAGER else "HIP graph replay",
         "bench_wall_s": time.perf_counter() - t_start,

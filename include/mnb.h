@@ -78,6 +78,24 @@ int mnb_plan_create(const mnb_desc *desc, const uint8_t *B, const float *scales,
 int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float *dScales,
                            const uint8_t *dZeroPoints, mnb_plan **out_plan);
 
+/* Gated-MLP front half as one plan: H[M, N] = silu(A * Wg^T) (*) (A * Wu^T),
+ * silu(x) = x * sigmoid(x), for a gate weight (Bg, Sg, Zg) and an up weight
+ * (Bu, Su, Zu) that share desc (K, N = intermediate size, block_size,
+ * zero-point presence; host pointers, MatMulNBits layout each). The graph
+ * fusion the roadmap lists as "gate projection, SiLU, and gate/up
+ * multiplication" over two MatMulNBits nodes, a Sigmoid and two Muls
+ * (docs/next_steps/2026/2026_08_qwen3_inference.rst:371-377); the unfused
+ * graph stays the correctness reference. The plan re-lays the rows once, at
+ * creation (row 2n = gate row n, row 2n + 1 = up row n), so each pair meets
+ * in one wavefront. mnb_run / mnb_run_path / mnb_run_ex on it write H
+ * (M x N floats); bias is rejected (MNB_ERR_UNSUPPORTED). The workspace
+ * (mnb_workspace_bytes) is required on every path: it starts with the
+ * M x 2N fp32 sum for the kernels whose epilogue cannot apply the
+ * activation (M = 2..4 and the fallbacks, followed by a separate pass). */
+int mnb_plan_create_gate_up(const mnb_desc *desc, const uint8_t *Bg, const float *Sg,
+                            const uint8_t *Zg, const uint8_t *Bu, const float *Su,
+                            const uint8_t *Zu, mnb_plan **out_plan);
+
 /* Releases the plan and the device memory it owns. NULL is accepted. */
 int mnb_plan_destroy(mnb_plan *plan);
 

@@ -57,6 +57,8 @@ def library():
         L.mnb_plan_create.argtypes = [ctypes.POINTER(MnbDesc), vp, vp, vp, ctypes.POINTER(vp)]
         L.mnb_plan_create_device.argtypes = [ctypes.POINTER(MnbDesc), vp, vp, vp,
                                              ctypes.POINTER(vp)]
+        L.mnb_plan_create_gate_up.argtypes = [ctypes.POINTER(MnbDesc), vp, vp, vp, vp, vp, vp,
+                                              ctypes.POINTER(vp)]
         L.mnb_plan_destroy.argtypes = [vp]
         L.mnb_workspace_bytes.argtypes = [vp, i64, ctypes.POINTER(sz)]
         L.mnb_run.argtypes = [vp, i64, vp, vp, vp, sz, vp]
@@ -73,7 +75,8 @@ def library():
         L.mnb_version.restype = ctypes.c_char_p
         for name in ("mnb_plan_create", "mnb_plan_create_device", "mnb_plan_destroy",
                      "mnb_workspace_bytes", "mnb_run", "mnb_run_path", "mnb_select_path",
-                     "mnb_weight_bytes", "mnb_run_ex", "mnb_qdq_repack"):
+                     "mnb_weight_bytes", "mnb_run_ex", "mnb_qdq_repack",
+                     "mnb_plan_create_gate_up"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib
@@ -235,6 +238,53 @@ class MatMulNBits:
         need = self.workspace_bytes(M) if path != PATH_GENERIC else 0
         if need == 0:
             return None
+        if self._work is None or self._work.numel() < need or self._work.device != device:
+            self._work = torch.empty(need, dtype=torch.uint8, device=device)
+        return self._work
+
+    run = __call__
+
+
+class GateUpSiLU(MatMulNBits):
+    """Gated-MLP front half as one plan: H[..., M, N] = silu(A Wg^T) * (A Wu^T)
+    for a gate and an up MatMulNBits weight of the same shape (K, N =
+    intermediate size, block_size, zero-point presence). The C ABI's
+    mnb_plan_create_gate_up interleaves the two weights' rows once; every call
+    needs the workspace (kept by the object). The unfused graph it replaces is
+    two MatMulNBits nodes, Sigmoid and two Muls."""
+
+    op_type = "MatMulNBitsGateUpSiLU"
+
+    def prepare(self, Bg, Sg, Zg, Bu, Su, Zu):
+        """Uploads host (numpy) gate and up constants once, rows interleaved."""
+        self.release()
+        if (Zg is None) != (Zu is None):
+            raise ValueError(f"{KERNEL_PREFIX}: gate and up must both have zero points or neither")
+        self.desc.has_zero_points = int(Zg is not None)
+        arrs = []
+        for B, S, Z in ((Bg, Sg, Zg), (Bu, Su, Zu)):
+            B = np.ascontiguousarray(B, dtype=np.uint8)
+            S = np.ascontiguousarray(S, dtype=np.float32)
+            Z = None if Z is None else np.ascontiguousarray(Z, dtype=np.uint8)
+            self._check_sizes(B.size, S.size, None if Z is None else Z.size)
+            arrs += [B, S, Z]
+        _check(library().mnb_plan_create_gate_up(ctypes.byref(self.desc),
+                                                 *[_host_ptr(a) for a in arrs],
+                                                 ctypes.byref(self._plan)),
+               "prepare")
+        return self
+
+    def prepare_device(self, *args, **kwargs):
+        raise NotImplementedError(f"{KERNEL_PREFIX}: gate/up plans are built from host weights")
+
+    def __call__(self, A, out=None, path: int = PATH_AUTO, stream=None, bias=None):
+        if bias is not None:
+            raise ValueError(f"{KERNEL_PREFIX}: a gate/up plan takes no bias")
+        return super().__call__(A, out=out, path=path, stream=stream)
+
+    def workspace(self, M: int, device, path: int = PATH_AUTO):
+        import torch
+        need = self.workspace_bytes(M)
         if self._work is None or self._work.numel() < need or self._work.device != device:
             self._work = torch.empty(need, dtype=torch.uint8, device=device)
         return self._work

@@ -13,12 +13,14 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <vector>
 
 struct mnb_plan {
-  mnb_desc desc;
+  mnb_desc desc;  // desc.N = weight rows the kernels see (2 I for a gate/up plan)
   mnb::WeightView view;
   int device;
   bool owns;
+  bool gate_up;   // rows are gate/up pairs; runs write silu(gate) * up, N / 2 columns
   uint8_t *dB;
   float *dS;
   uint8_t *dZ;
@@ -127,6 +129,33 @@ int CheckInputs(const mnb_desc *desc, const void *B, const void *scales, const v
 }
 
 } // namespace
+
+namespace mnb {
+
+__global__ __launch_bounds__(256) void SiluMulKernel(const float *__restrict__ Y,
+                                                     float *__restrict__ H, int64_t half_mn) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < half_mn) {
+    const float2 gu = reinterpret_cast<const float2 *>(Y)[i];
+    H[i] = SiluMul(gu.x, gu.y);
+  }
+}
+
+hipError_t LaunchSiluMul(const float *Y, float *H, int64_t M, int64_t N, hipStream_t s) {
+  const int64_t half_mn = M * N / 2;
+  hipLaunchKernelGGL(SiluMulKernel, dim3(static_cast<unsigned>((half_mn + 255) / 256)), dim3(256),
+                     0, s, Y, H, half_mn);
+  return hipGetLastError();
+}
+
+} // namespace mnb
+
+// Bytes of the gate/up plans' scratch sum y = A * W^T (M x N floats, N = 2 I)
+// at the front of the workspace, rounded up to keep what follows aligned.
+static size_t GateUpScratchBytes(const mnb_plan *plan, int64_t M) {
+  if (!plan->gate_up) return 0;
+  return (static_cast<size_t>(M) * static_cast<size_t>(plan->view.N) * 4 + 255) / 256 * 256;
+}
 
 // Y[m][n] += bias[n]: MatMulNBits' optional bias input, an epilogue over the
 // finished Y on the same stream (every path's kernels have completed their
@@ -243,6 +272,47 @@ int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float 
   return MNB_OK;
 }
 
+int mnb_plan_create_gate_up(const mnb_desc *desc, const uint8_t *Bg, const float *Sg,
+                            const uint8_t *Zg, const uint8_t *Bu, const float *Su,
+                            const uint8_t *Zu, mnb_plan **out_plan) {
+  int st = CheckInputs(desc, Bg, Sg, Zg, out_plan);
+  if (st != MNB_OK) return st;
+  st = CheckInputs(desc, Bu, Su, Zu, out_plan);
+  if (st != MNB_OK) return st;
+  if (desc->N > (int64_t{1} << 29)) return MNB_ERR_BAD_SHAPE;
+  // Rows interleaved once, on the host: row 2n = gate row n, 2n + 1 = up row n.
+  mnb_desc d2 = *desc;
+  d2.N = 2 * desc->N;
+  int64_t nb, row_bytes, zp_row_bytes;
+  Sizes(desc, &nb, &row_bytes, &zp_row_bytes);
+  const size_t I = static_cast<size_t>(desc->N);
+  std::vector<uint8_t> b2, z2;
+  std::vector<float> s2;
+  try {
+    b2.resize(2 * I * row_bytes);
+    s2.resize(2 * I * nb);
+    if (desc->has_zero_points) z2.resize(2 * I * zp_row_bytes);
+  } catch (const std::bad_alloc &) {
+    return MNB_ERR_ALLOC;
+  }
+  for (size_t n = 0; n < I; ++n) {
+    std::memcpy(&b2[(2 * n) * row_bytes], Bg + n * row_bytes, row_bytes);
+    std::memcpy(&b2[(2 * n + 1) * row_bytes], Bu + n * row_bytes, row_bytes);
+    std::memcpy(&s2[(2 * n) * nb], Sg + n * nb, nb * sizeof(float));
+    std::memcpy(&s2[(2 * n + 1) * nb], Su + n * nb, nb * sizeof(float));
+    if (desc->has_zero_points) {
+      std::memcpy(&z2[(2 * n) * zp_row_bytes], Zg + n * zp_row_bytes, zp_row_bytes);
+      std::memcpy(&z2[(2 * n + 1) * zp_row_bytes], Zu + n * zp_row_bytes, zp_row_bytes);
+    }
+  }
+  mnb_plan *p = nullptr;
+  st = mnb_plan_create(&d2, b2.data(), s2.data(), desc->has_zero_points ? z2.data() : nullptr, &p);
+  if (st != MNB_OK) return st;
+  p->gate_up = true;
+  *out_plan = p;
+  return MNB_OK;
+}
+
 int mnb_plan_destroy(mnb_plan *plan) {
   if (plan == nullptr) return MNB_OK;
   FreePlanMemory(plan);
@@ -270,10 +340,11 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
   // The size covers every path mnb_run_path may be asked to take for M rows:
   // the prefill GEMM (A rounded to fp16, tile layout, split-K partial sums)
   // and the MFMA decode kernel (split-K partial sums).
+  // A gate/up plan adds the scratch sum in front of either.
   size_t need = 0;
   if (M > 0 && mnb::GemmSupports(plan->view, M)) need = mnb::GemmWorkspaceBytes(plan->view, M);
   if (UsesMfmaDecode(plan, M)) need = std::max(need, mnb::GemvMfmaWorkspaceBytes(plan->view, M));
-  *bytes = need;
+  *bytes = need + GateUpScratchBytes(plan, M);
   return MNB_OK;
 }
 
@@ -304,10 +375,21 @@ int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dB
   if (path == 1 && !(a_aligned && M <= 16 && mnb::GemvSupports(plan->view, M)))
     return MNB_ERR_UNSUPPORTED;
   if (path == 2 && !(a_aligned && mnb::GemmSupports(plan->view, M))) return MNB_ERR_UNSUPPORTED;
+  if (plan->gate_up && dBias != nullptr) return MNB_ERR_UNSUPPORTED;
+  // A gate/up plan's runs start with the scratch sum; the path's own
+  // workspace follows it.
+  const size_t scratch = GateUpScratchBytes(plan, M);
+  if (scratch > 0 && (dWorkspace == nullptr || workspace_bytes < scratch ||
+                      (reinterpret_cast<uintptr_t>(dWorkspace) % 16) != 0))
+    return MNB_ERR_WORKSPACE;
+  float *Ys = scratch > 0 ? static_cast<float *>(dWorkspace) : dY;
+  float *H = scratch > 0 ? dY : nullptr;
+  void *work = scratch > 0 ? static_cast<void *>(static_cast<char *>(dWorkspace) + scratch)
+                           : dWorkspace;
+  const size_t work_bytes = scratch > 0 ? workspace_bytes - scratch : workspace_bytes;
   if (path == 2) {
     const size_t need = mnb::GemmWorkspaceBytes(plan->view, M);
-    if (dWorkspace == nullptr || workspace_bytes < need ||
-        (reinterpret_cast<uintptr_t>(dWorkspace) % 16) != 0)
+    if (work == nullptr || work_bytes < need || (reinterpret_cast<uintptr_t>(work) % 16) != 0)
       return MNB_ERR_WORKSPACE;
   }
 
@@ -319,21 +401,37 @@ int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dB
     return MNB_ERR_NO_DEVICE;
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Kernels with the gate/up epilogue take H and write it themselves; after
+  // the others, SiluMulKernel turns the scratch sum into H.
+  bool fused = false;
   switch (path) {
   case 1:
-    if (M == 1 && mnb::GemvM1Supports(plan->view))
-      e = mnb::LaunchGemvM1(plan->view, dA, dY, s, 0, 0);
-    else if (UsesMfmaDecode(plan, M) && HasWorkspace(dWorkspace, workspace_bytes,
-                                                      mnb::GemvMfmaWorkspaceBytes(plan->view, M)))
-      e = mnb::LaunchGemvMfma(plan->view, M, dA, dY, dWorkspace, s);
-    else if (mnb::GemvSmallMSupports(plan->view, M))
-      e = mnb::LaunchGemvSmallM(plan->view, M, dA, dY, s);
-    else
-      e = mnb::LaunchGemv(plan->view, M, dA, dY, s);
+    if (M == 1 && mnb::GemvM1Supports(plan->view)) {
+      e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0, H);
+      fused = true;
+      if (e == hipErrorInvalidValue && H != nullptr) {
+        // no shape with paired rows for this plan: plain launch, then the pass
+        e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0);
+        fused = false;
+      }
+    } else if (UsesMfmaDecode(plan, M) &&
+               HasWorkspace(work, work_bytes, mnb::GemvMfmaWorkspaceBytes(plan->view, M))) {
+      e = mnb::LaunchGemvMfma(plan->view, M, dA, Ys, work, s, H);
+      fused = true;
+    } else if (mnb::GemvSmallMSupports(plan->view, M)) {
+      e = mnb::LaunchGemvSmallM(plan->view, M, dA, Ys, s);
+    } else {
+      e = mnb::LaunchGemv(plan->view, M, dA, Ys, s);
+    }
     break;
-  case 2: e = mnb::LaunchGemm(plan->view, M, dA, dY, dWorkspace, s); break;
-  default: e = mnb::LaunchGeneric(plan->view, M, dA, dY, s); break;
+  case 2:
+    // The GEMM's fused stores address H with 32-bit byte offsets.
+    fused = H != nullptr && M * plan->view.N * 2 < (int64_t{1} << 31);
+    e = mnb::LaunchGemm(plan->view, M, dA, Ys, work, s, fused ? H : nullptr);
+    break;
+  default: e = mnb::LaunchGeneric(plan->view, M, dA, Ys, s); break;
   }
+  if (e == hipSuccess && H != nullptr && !fused) e = mnb::LaunchSiluMul(Ys, H, M, plan->view.N, s);
   if (e == hipSuccess && dBias != nullptr) e = LaunchAddBias(dY, dBias, M, plan->view.N, s);
   if (e != hipSuccess) {
     SetLastError("kernel launch", e);

@@ -176,7 +176,8 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
                                                      float *__restrict__ Y, int M, int K, int N,
                                                      int nb, int log2_bs, int row_bytes,
                                                      int zp_row_bytes, int kt_per_split,
-                                                     float *__restrict__ partials) {
+                                                     float *__restrict__ partials,
+                                                     float *__restrict__ H) {
   extern __shared__ uint4 lds[];
   constexpr int kAUnits = AUnits<BM>();
   uint4 *Astage = lds;                        // [kAStages][kAUnits]
@@ -372,6 +373,37 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
   // Output: split 0 writes Y, split s > 0 of a split-K launch its partial sum
   // at partials + (s - 1) * M * N. Lane holds column (lane & 15), rows
   // 4*(lane >> 4) + v of each 16 x 16 tile.
+  if (H != nullptr) {
+    // Gate/up epilogue of a one-split launch. Column gn + 1 (the up of gate
+    // gn, N even) is held by lane ^ 1 for the same four rows v = 0..3; the
+    // even lane finishes rows 0 and 1 of each fragment, the odd lane rows 2
+    // and 3, each receiving the two values it lacks through one DPP swap.
+    // Stores are buffer stores at byte offsets from this tile's first output
+    // row: rows past M fall beyond the resource and columns past N are sent
+    // there, so nothing branches (the host keeps M * N / 2 * 4 < 2^31).
+    const int half_n = N >> 1;
+    const bool odd = (lane & 1) != 0;
+    const auto hr = __builtin_amdgcn_make_buffer_rsrc(
+        H + static_cast<size_t>(m0) * half_n, 0, (M - m0) * half_n * 4, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const floatx4 a = acc[i][j];
+        const float r0 = PairSwap(odd ? a[0] : a[2]);
+        const float r1 = PairSwap(odd ? a[1] : a[3]);
+        const float h0 = odd ? SiluMul(r0, a[2]) : SiluMul(a[0], r0);
+        const float h1 = odd ? SiluMul(r1, a[3]) : SiluMul(a[1], r1);
+        const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
+        const int row = wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + (odd ? 2 : 0);
+        const int off = gn < N ? (row * half_n + (gn >> 1)) * 4 : 0x7FFFFFF0;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, h0), hr, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, h1), hr,
+                                              gn < N ? off + half_n * 4 : off, 0, 0);
+      }
+    }
+    return;
+  }
   if (split > 0) Y = partials + static_cast<size_t>(split - 1) * M * N;
 #pragma unroll
   for (int i = 0; i < kMI; ++i) {
@@ -394,7 +426,7 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
 template <bool VEC, int PARTS>
 __global__ __launch_bounds__(256) void SplitReduceKernel(float *__restrict__ Y,
                                                          const float *__restrict__ P,
-                                                         int64_t mn) {
+                                                         int64_t mn, float *__restrict__ H) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * (VEC ? 4 : 1);
   if (i >= mn) return;
@@ -406,7 +438,10 @@ __global__ __launch_bounds__(256) void SplitReduceKernel(float *__restrict__ Y,
     f32x4 y = *reinterpret_cast<const f32x4 *>(Y + i);
 #pragma unroll
     for (int p = 0; p < PARTS; ++p) y += v[p];
-    *reinterpret_cast<f32x4 *>(Y + i) = y;
+    if (H != nullptr)  // gate/up pairs (N even: a pair never straddles rows)
+      *reinterpret_cast<float2 *>(H + i / 2) = make_float2(SiluMul(y[0], y[1]), SiluMul(y[2], y[3]));
+    else
+      *reinterpret_cast<f32x4 *>(Y + i) = y;
   } else {
     float v[PARTS];
 #pragma unroll
@@ -414,28 +449,36 @@ __global__ __launch_bounds__(256) void SplitReduceKernel(float *__restrict__ Y,
     float y = Y[i];
 #pragma unroll
     for (int p = 0; p < PARTS; ++p) y += v[p];
-    Y[i] = y;
+    if (H != nullptr) {
+      // mn is even: lanes i and i ^ 1 are both in range, in the same wavefront
+      const float other = PairSwap(y);
+      if ((i & 1) == 0) H[i / 2] = SiluMul(y, other);
+    } else {
+      Y[i] = y;
+    }
   }
 }
 
 template <int PARTS>
-hipError_t LaunchReduce(float *Y, const float *P, int64_t mn, hipStream_t s) {
-  if (mn % 4 == 0 && reinterpret_cast<uintptr_t>(Y) % 16 == 0) {
+hipError_t LaunchReduce(float *Y, const float *P, int64_t mn, hipStream_t s, float *H) {
+  if (mn % 4 == 0 && reinterpret_cast<uintptr_t>(Y) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(H) % 8 == 0) {
     hipLaunchKernelGGL((SplitReduceKernel<true, PARTS>),
                        dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s, Y, P,
-                       mn);
+                       mn, H);
   } else {
     hipLaunchKernelGGL((SplitReduceKernel<false, PARTS>),
-                       dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, Y, P, mn);
+                       dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, Y, P, mn,
+                       H);
   }
   return hipGetLastError();
 }
 
 template <int... Ps>
 hipError_t DispatchReduce(int parts, float *Y, const float *P, int64_t mn, hipStream_t s,
-                          std::integer_sequence<int, Ps...>) {
+                          float *H, std::integer_sequence<int, Ps...>) {
   hipError_t e = hipErrorInvalidValue;
-  (void)((parts == Ps + 1 ? (e = LaunchReduce<Ps + 1>(Y, P, mn, s), true) : false) || ...);
+  (void)((parts == Ps + 1 ? (e = LaunchReduce<Ps + 1>(Y, P, mn, s, H), true) : false) || ...);
   return e;
 }
 
@@ -466,19 +509,19 @@ inline size_t PartialBytes(const WeightView &w, int64_t M, const Shape &sh) {
 
 template <int BM, bool HAS_ZP>
 hipError_t LaunchT(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, float *partials,
-                   const Shape &sh, hipStream_t s) {
+                   const Shape &sh, hipStream_t s, float *H) {
   const int tiles = static_cast<int>(((M + BM - 1) / BM) * ((w.N + kBN - 1) / kBN));
   hipLaunchKernelGGL((GemmKernel<BM, HAS_ZP>), dim3(tiles * sh.splits), dim3(256), LdsBytes<BM>(),
                      s, Ah, w.B, w.scales, w.zp, Y, static_cast<int>(M), static_cast<int>(w.K),
                      static_cast<int>(w.N), static_cast<int>(w.nb), w.log2_bs,
                      static_cast<int>(w.row_bytes), static_cast<int>(w.zp_row_bytes),
-                     sh.kt_per_split, partials);
+                     sh.kt_per_split, partials, H);
   return hipGetLastError();
 }
 
 template <int BM>
 hipError_t LaunchBM(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                    const Shape &sh, hipStream_t s) {
+                    const Shape &sh, hipStream_t s, float *H) {
   uint4 *Ah = static_cast<uint4 *>(work);
   float *partials = reinterpret_cast<float *>(static_cast<char *>(work) + AImageBytes(w, M));
   const int64_t units = (M + BM - 1) / BM * BM * (w.K / 8);
@@ -486,10 +529,13 @@ hipError_t LaunchBM(const WeightView &w, int64_t M, const float *A, float *Y, vo
                      dim3(256), 0, s, A, Ah, static_cast<int>(M), static_cast<int>(w.K), units);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  e = w.zp != nullptr ? LaunchT<BM, true>(w, M, Ah, Y, partials, sh, s)
-                      : LaunchT<BM, false>(w, M, Ah, Y, partials, sh, s);
+  // Gate/up activation: fused into the GEMM's stores with one split, into the
+  // reduction (split 0 then writes the scratch Y) with several.
+  float *Hk = sh.splits == 1 ? H : nullptr;
+  e = w.zp != nullptr ? LaunchT<BM, true>(w, M, Ah, Y, partials, sh, s, Hk)
+                      : LaunchT<BM, false>(w, M, Ah, Y, partials, sh, s, Hk);
   if (e != hipSuccess || sh.splits == 1) return e;
-  return DispatchReduce(sh.splits - 1, Y, partials, M * w.N, s,
+  return DispatchReduce(sh.splits - 1, Y, partials, M * w.N, s, H,
                         std::make_integer_sequence<int, kMaxSplits - 1>{});
 }
 
@@ -534,20 +580,20 @@ bool GemmSupports(const WeightView &w, int64_t M) {
 }
 
 hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                           hipStream_t s, int bm, int splits) {
+                           hipStream_t s, int bm, int splits, float *H) {
   Shape sh = PickShape(w, M);
   if (bm > 0) sh = MakeShape(w, bm, splits > 0 ? splits : 1);
   switch (sh.bm) {
-  case 32: return LaunchBM<32>(w, M, A, Y, work, sh, s);
-  case 64: return LaunchBM<64>(w, M, A, Y, work, sh, s);
-  case 128: return LaunchBM<128>(w, M, A, Y, work, sh, s);
+  case 32: return LaunchBM<32>(w, M, A, Y, work, sh, s, H);
+  case 64: return LaunchBM<64>(w, M, A, Y, work, sh, s, H);
+  case 128: return LaunchBM<128>(w, M, A, Y, work, sh, s, H);
   default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                      hipStream_t s) {
-  return LaunchGemmShape(w, M, A, Y, work, s, 0, 0);
+                      hipStream_t s, float *H) {
+  return LaunchGemmShape(w, M, A, Y, work, s, 0, 0, H);
 }
 
 } // namespace mnb

@@ -141,7 +141,8 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
                                                      const uint8_t *__restrict__ Z,
                                                      float *__restrict__ Y, int K, int N, int nb,
                                                      int chunk_shift, int row_bytes,
-                                                     int zp_row_bytes, int G) {
+                                                     int zp_row_bytes, int G,
+                                                     float *__restrict__ H) {
   extern __shared__ float4 lds4[];
   const int nchunks = K >> 5;
   const int tid = threadIdx.x, nthreads = blockDim.x;
@@ -311,7 +312,15 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
     const float t = WaveTotal(acc[r]);
     mine = lane == r ? t : mine;
   }
-  if (lane < R && wr0 + lane < rows) Y[row0 + wr0 + lane] = mine;
+  if (H != nullptr) {
+    // Gate/up pairs: band row 2n is a gate, 2n + 1 its up (R and G even, so a
+    // pair never straddles wavefronts or bands).
+    const float other = PairSwap(mine);
+    if (lane < R && (lane & 1) == 0 && wr0 + lane < rows)
+      H[(row0 + wr0 + lane) >> 1] = SiluMul(mine, other);
+  } else if (lane < R && wr0 + lane < rows) {
+    Y[row0 + wr0 + lane] = mine;
+  }
 }
 
 struct Shape {
@@ -377,7 +386,8 @@ inline Shape PickShape(const WeightView &w, int cpl, int G, int R) {
 }
 
 template <int CPL, int R, bool HAS_ZP>
-hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s, const Shape &sh) {
+hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s, const Shape &sh,
+                   float *H) {
   const bool full = (w.K / 32) == 64 * CPL;
   const bool quads = (w.nb % 4) == 0;
   const dim3 grid(static_cast<unsigned>(sh.grid)), block(static_cast<unsigned>(sh.waves * 64));
@@ -386,7 +396,7 @@ hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s,
   const int zb = static_cast<int>(w.zp_row_bytes);
 #define MNB_M1_LAUNCH(FULLV, PWV)                                                                  \
   hipLaunchKernelGGL((GemvM1Kernel<CPL, R, FULLV, HAS_ZP, PWV>), grid, block, sh.lds, s, A, w.B,  \
-                     w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G)
+                     w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G, H)
   if (full) {
     if (quads) MNB_M1_LAUNCH(true, 4);
     else MNB_M1_LAUNCH(true, 1);
@@ -399,37 +409,44 @@ hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s,
 }
 
 template <int CPL, bool HAS_ZP>
-hipError_t LaunchC(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R) {
-  const Shape sh = PickShape(w, CPL, G, R);
+hipError_t LaunchC(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R,
+                   float *H) {
+  Shape sh = PickShape(w, CPL, G, R);
+  if (H != nullptr && (sh.R < 2 || (sh.G & 1) != 0)) {
+    // Gate/up epilogue: an even number of rows per wavefront and per band.
+    const int r2 = std::max(sh.R, 2);
+    sh = PickShape(w, CPL, sh.G + (sh.G & 1), r2);
+  }
   // Rows per wavefront are capped so that R * CPL weight chunks stay within
   // 16 VGPR quads (no spills under the 1024-thread launch bound).
   constexpr int kRMax = CPL <= 2 ? 8 : (CPL <= 4 ? 4 : 2);
   if (sh.waves < 1 || sh.waves > kMaxWaves || sh.lds > 160 * 1024 || sh.R > kRMax)
     return hipErrorInvalidValue;
   switch (sh.R) {
-  case 1: return LaunchT<CPL, 1, HAS_ZP>(w, A, Y, s, sh);
-  case 2: return LaunchT<CPL, 2, HAS_ZP>(w, A, Y, s, sh);
+  case 1: return LaunchT<CPL, 1, HAS_ZP>(w, A, Y, s, sh, H);
+  case 2: return LaunchT<CPL, 2, HAS_ZP>(w, A, Y, s, sh, H);
   case 4:
-    if constexpr (kRMax >= 4) return LaunchT<CPL, 4, HAS_ZP>(w, A, Y, s, sh);
+    if constexpr (kRMax >= 4) return LaunchT<CPL, 4, HAS_ZP>(w, A, Y, s, sh, H);
     return hipErrorInvalidValue;
   case 8:
-    if constexpr (kRMax >= 8) return LaunchT<CPL, 8, HAS_ZP>(w, A, Y, s, sh);
+    if constexpr (kRMax >= 8) return LaunchT<CPL, 8, HAS_ZP>(w, A, Y, s, sh, H);
     return hipErrorInvalidValue;
   default: return hipErrorInvalidValue;
   }
 }
 
 template <bool HAS_ZP>
-hipError_t LaunchZ(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R) {
+hipError_t LaunchZ(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R,
+                   float *H) {
   switch ((w.K / 32 + 63) / 64) {
-  case 1: return LaunchC<1, HAS_ZP>(w, A, Y, s, G, R);
-  case 2: return LaunchC<2, HAS_ZP>(w, A, Y, s, G, R);
-  case 3: return LaunchC<3, HAS_ZP>(w, A, Y, s, G, R);
-  case 4: return LaunchC<4, HAS_ZP>(w, A, Y, s, G, R);
-  case 5: return LaunchC<5, HAS_ZP>(w, A, Y, s, G, R);
-  case 6: return LaunchC<6, HAS_ZP>(w, A, Y, s, G, R);
-  case 7: return LaunchC<7, HAS_ZP>(w, A, Y, s, G, R);
-  default: return LaunchC<8, HAS_ZP>(w, A, Y, s, G, R);
+  case 1: return LaunchC<1, HAS_ZP>(w, A, Y, s, G, R, H);
+  case 2: return LaunchC<2, HAS_ZP>(w, A, Y, s, G, R, H);
+  case 3: return LaunchC<3, HAS_ZP>(w, A, Y, s, G, R, H);
+  case 4: return LaunchC<4, HAS_ZP>(w, A, Y, s, G, R, H);
+  case 5: return LaunchC<5, HAS_ZP>(w, A, Y, s, G, R, H);
+  case 6: return LaunchC<6, HAS_ZP>(w, A, Y, s, G, R, H);
+  case 7: return LaunchC<7, HAS_ZP>(w, A, Y, s, G, R, H);
+  default: return LaunchC<8, HAS_ZP>(w, A, Y, s, G, R, H);
   }
 }
 
@@ -449,9 +466,9 @@ bool GemvM1Supports(const WeightView &w) {
 }
 
 hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
-                        int band_rows, int rows_per_wave) {
-  return w.zp ? m1::LaunchZ<true>(w, A, Y, s, band_rows, rows_per_wave)
-              : m1::LaunchZ<false>(w, A, Y, s, band_rows, rows_per_wave);
+                        int band_rows, int rows_per_wave, float *H) {
+  return w.zp ? m1::LaunchZ<true>(w, A, Y, s, band_rows, rows_per_wave, H)
+              : m1::LaunchZ<false>(w, A, Y, s, band_rows, rows_per_wave, H);
 }
 
 } // namespace mnb

@@ -409,7 +409,7 @@ __global__ __launch_bounds__(64 * kWaves) void GemvMfmaKernel(
 template <bool VEC>
 __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
                                                          const float *__restrict__ P, int64_t mn,
-                                                         int parts) {
+                                                         int parts, float *__restrict__ H) {
   constexpr int kBatch = 16;
   if constexpr (VEC) {
     const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
@@ -425,7 +425,12 @@ __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
       for (int q = 0; q < kBatch; ++q)
         if (p + q < parts) y += v[q];
     }
-    *reinterpret_cast<floatx4 *>(Y + i) = y;
+    if (H != nullptr) {
+      // gate/up pairs (N even, so a pair never straddles rows)
+      *reinterpret_cast<float2 *>(H + i / 2) = make_float2(SiluMul(y[0], y[1]), SiluMul(y[2], y[3]));
+    } else {
+      *reinterpret_cast<floatx4 *>(Y + i) = y;
+    }
   } else {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= mn) return;
@@ -439,7 +444,13 @@ __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
       for (int q = 0; q < kBatch; ++q)
         if (p + q < parts) y += v[q];
     }
-    Y[i] = y;
+    if (H != nullptr) {
+      // mn is even: lanes i and i ^ 1 are both in range, in the same wavefront
+      const float other = PairSwap(y);
+      if ((i & 1) == 0) H[i / 2] = SiluMul(y, other);
+    } else {
+      Y[i] = y;
+    }
   }
 }
 
@@ -514,7 +525,8 @@ size_t GemvMfmaWorkspaceBytes(const WeightView &w, int64_t M) {
 }
 
 hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, float *Y,
-                               void *work, hipStream_t s, int rows_per_wave, int wgs_per_cu) {
+                               void *work, hipStream_t s, int rows_per_wave, int wgs_per_cu,
+                               float *H) {
   const mf::Shape sh = mf::PickShape(w, rows_per_wave, wgs_per_cu);
   if (!(sh.rb == 1 || sh.rb == 2) || sh.pairs < 1 || sh.pairs > 2) return hipErrorInvalidValue;
   float *P = static_cast<float *>(work);
@@ -524,23 +536,26 @@ hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, f
   case 2: e = mf::LaunchBsc<2>(w, M, A, Y, P, sh, s); break;
   default: e = mf::LaunchBsc<4>(w, M, A, Y, P, sh, s); break;
   }
-  if (e != hipSuccess || sh.splits == 1) return e;
+  if (e != hipSuccess) return e;
   const int64_t mn = M * w.N;
+  // One 512-k range: Y is complete, only the gate/up activation is left.
+  if (sh.splits == 1) return H != nullptr ? LaunchSiluMul(Y, H, M, w.N, s) : hipSuccess;
   const bool vec = (mn % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0 &&
-                   (reinterpret_cast<uintptr_t>(P) % 16) == 0;
+                   (reinterpret_cast<uintptr_t>(P) % 16) == 0 &&
+                   (reinterpret_cast<uintptr_t>(H) % 8) == 0;
   if (vec)
     hipLaunchKernelGGL(mf::SumPartialsKernel<true>,
                        dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s, Y, P,
-                       mn, sh.splits - 1);
+                       mn, sh.splits - 1, H);
   else
     hipLaunchKernelGGL(mf::SumPartialsKernel<false>, dim3(static_cast<unsigned>((mn + 255) / 256)),
-                       dim3(256), 0, s, Y, P, mn, sh.splits - 1);
+                       dim3(256), 0, s, Y, P, mn, sh.splits - 1, H);
   return hipGetLastError();
 }
 
 hipError_t LaunchGemvMfma(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                          hipStream_t s) {
-  return LaunchGemvMfmaShape(w, M, A, Y, work, s, 0, 0);
+                          hipStream_t s, float *H) {
+  return LaunchGemvMfmaShape(w, M, A, Y, work, s, 0, 0, H);
 }
 
 } // namespace mnb

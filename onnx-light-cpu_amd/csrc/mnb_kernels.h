@@ -32,6 +32,28 @@ __device__ __forceinline__ void CopyToLds16(const void *gsrc, uint32_t lds_base)
 }
 #pragma clang diagnostic pop
 
+// Gated-MLP activation of one gate/up pair: silu(g) * u = g * sigmoid(g) * u,
+// with sigmoid(g) = 1 / (1 + exp(-g)) from the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32, 1 ulp each): a few instructions instead of the
+// libm-exact expf and division, which made the GEMM's fused epilogue cost
+// more than the pass it removes. Relative error about 3e-7 + |g| * 6e-8
+// (the rounding of -g * log2(e)). Large |g| saturate cleanly: exp2 of a
+// large argument is +inf and its reciprocal 0, of a very negative one 0.
+// Every kernel that applies the activation (fused epilogues and the separate
+// SiluMulKernel) uses this one expression, so a fused result equals the
+// unfused one bit for bit.
+__device__ __forceinline__ float SiluMul(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+  return g * u * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// The value of lane ^ 1 (DPP quad_perm [1,0,3,2]: one VALU move, no LDS
+// round trip). Both lanes of each pair must be active.
+__device__ __forceinline__ float PairSwap(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+}
+
 // Everything a kernel needs to address one plan's constants.
 struct WeightView {
   const uint8_t *B;       // [N, nb, bs/2] packed nibbles, low nibble first
@@ -64,8 +86,14 @@ hipError_t LaunchGemvSmallMShape(const WeightView &w, int64_t M, const float *A,
 // Decode GEMV for M == 1 (fp16-subnormal mixed FMA): one workgroup per band
 // of `band_rows` weight rows, `rows_per_wave` (1, 2, 4 or 8) rows per
 // wavefront; 0 picks both from the shape and the device's CU count.
+//
+// Gate/up epilogue (this and the MFMA decode and GEMM launches below): when
+// H is not null, the plan's rows are gate/up pairs (row 2n the gate of output
+// n, row 2n + 1 its up) and the launch writes H[m][n] = SiluMul(y[m][2n],
+// y[m][2n + 1]) instead of the product y; Y is then scratch (M x N floats)
+// for the launches that need an intermediate sum, unused by the others.
 hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
-                        int band_rows, int rows_per_wave);
+                        int band_rows, int rows_per_wave, float *H = nullptr);
 bool GemvM1Supports(const WeightView &w);
 
 // Decode GEMV for 2 <= M <= 16 on fp16 MFMA with exact products (each
@@ -73,27 +101,32 @@ bool GemvM1Supports(const WeightView &w);
 // multiple of 512 (at most 32768), power-of-two block_size >= 32. `work`
 // holds GemvMfmaWorkspaceBytes(w, M) bytes: the partial sums of K ranges 1..
 hipError_t LaunchGemvMfma(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                          hipStream_t s);
+                          hipStream_t s, float *H = nullptr);
 bool GemvMfmaSupports(const WeightView &w, int64_t M);
 size_t GemvMfmaWorkspaceBytes(const WeightView &w, int64_t M);
 // Same with an explicit shape (tuning): 16-row blocks per item (1 or 2) and
 // workgroups per CU; 0 picks.
 hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, float *Y,
-                               void *work, hipStream_t s, int rows_per_wave, int wgs_per_cu);
+                               void *work, hipStream_t s, int rows_per_wave, int wgs_per_cu,
+                               float *H = nullptr);
 
 // Prefill GEMM on fp16 MFMA, any M, K % 64 == 0, block_size >= 32. `work`
 // holds GemmWorkspaceBytes(w, M) bytes of device memory: A rounded to fp16,
 // then the partial sums of a split-K launch.
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                      hipStream_t s);
+                      hipStream_t s, float *H = nullptr);
 bool GemmSupports(const WeightView &w, int64_t M);
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M);
 // Same with an explicit tile height (32, 64 or 128; 0 picks both) and split
 // count (1..16), for tuning; `work` then holds
 // GemmShapeWorkspaceBytes(w, M, splits) bytes.
 hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                           hipStream_t s, int bm, int splits);
+                           hipStream_t s, int bm, int splits, float *H = nullptr);
 size_t GemmShapeWorkspaceBytes(const WeightView &w, int64_t M, int splits);
+
+// H[m][n] = SiluMul(Y[m][2n], Y[m][2n + 1]) for an M x N (N even) Y: the
+// gate/up activation after a kernel without the fused epilogue.
+hipError_t LaunchSiluMul(const float *Y, float *H, int64_t M, int64_t N, hipStream_t s);
 
 // Generic fallback: any K, any block_size, any M. Slow; for odd shapes and
 // cross-checks.

@@ -179,6 +179,28 @@ def dequantize_linear_4bit(x_packed, K, N, signed, scale, zp=None, block_size=0,
     return ((q - z_full).astype(np.float32) * s_full).astype(np.float32)
 
 
+def silu_mul_f64(g, u):
+    """silu(g) * u = g * sigmoid(g) * u in fp64, sigmoid(g) = 1 / (1 + exp(-g)):
+    the Sigmoid -> Mul -> Mul subgraph of a gated MLP that the gate/up plan
+    fuses (docs/next_steps/2026/2026_08_qwen3_inference.rst:371-377 lists the
+    fusion; the ONNX Sigmoid and Mul operators define the values). sigmoid
+    is taken as 1 / (1 + exp(-g)) for g >= 0 and exp(g) / (1 + exp(g)) below,
+    which neither overflows nor cancels."""
+    g = np.asarray(g, np.float64)
+    u = np.asarray(u, np.float64)
+    e = np.exp(-np.abs(g))
+    sig = np.where(g >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
+    return g * sig * u
+
+
+def gate_up_silu_f64(A, Bg, Sg, Zg, Bu, Su, Zu, K, N, bs, threads=None):
+    """H [M, N] fp64 = silu(A * Wg^T) * (A * Wu^T), both products from the
+    pinned fp64 MatMulNBits restatement (matmul_nbits_f64)."""
+    g = matmul_nbits_f64(A, Bg, Sg, Zg, K, N, bs, threads)
+    u = matmul_nbits_f64(A, Bu, Su, Zu, K, N, bs, threads)
+    return silu_mul_f64(g, u)
+
+
 def f32_to_f16_bits(x):
     x = np.ascontiguousarray(x, dtype=np.float32).ravel()
     out = np.empty(x.size, np.uint16)

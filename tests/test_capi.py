@@ -19,7 +19,8 @@ def test_library_exports_every_header_function(pkg):
     assert names == sorted([
         "mnb_plan_create", "mnb_plan_create_device", "mnb_plan_destroy", "mnb_workspace_bytes",
         "mnb_run", "mnb_run_path", "mnb_run_ex", "mnb_select_path", "mnb_status_str",
-        "mnb_last_error", "mnb_weight_bytes", "mnb_version", "mnb_qdq_repack"])
+        "mnb_last_error", "mnb_weight_bytes", "mnb_version", "mnb_qdq_repack",
+        "mnb_plan_create_gate_up"])
     for name in names:
         assert hasattr(L, name), name
 
@@ -97,6 +98,31 @@ def test_run_and_queries_reject_null_plan(pkg):
     assert L.mnb_workspace_bytes(None, 1, ctypes.byref(x)) == NULLP
     assert L.mnb_select_path(None, 1, ctypes.byref(p)) == NULLP
     assert L.mnb_plan_destroy(None) == MNB_OK
+
+
+def test_gate_up_plan_validates_before_the_device(pkg):
+    """mnb_plan_create_gate_up checks both weights' pointers and the doubled
+    row count before any HIP call."""
+    L = pkg.library()
+    plan = ctypes.c_void_p()
+    B = np.zeros(64 * 8 * 16, np.uint8)
+    S = np.zeros(64 * 8, np.float32)
+    Z = np.zeros(64 * 4, np.uint8)
+    P = lambda a: a.ctypes.data
+    d = _desc(pkg)
+    assert L.mnb_plan_create_gate_up(ctypes.byref(d), P(B), P(S), None, None, P(S), None,
+                                     ctypes.byref(plan)) == NULLP
+    assert L.mnb_plan_create_gate_up(ctypes.byref(d), P(B), P(S), None, P(B), P(S), None,
+                                     None) == NULLP
+    dz = _desc(pkg, zp=1)
+    assert L.mnb_plan_create_gate_up(ctypes.byref(dz), P(B), P(S), P(Z), P(B), P(S), None,
+                                     ctypes.byref(plan)) == NULLP
+    assert L.mnb_plan_create_gate_up(ctypes.byref(d), P(B), P(S), P(Z), P(B), P(S), None,
+                                     ctypes.byref(plan)) == UNSUP
+    big = _desc(pkg, N=(1 << 29) + 1)
+    assert L.mnb_plan_create_gate_up(ctypes.byref(big), P(B), P(S), None, P(B), P(S), None,
+                                     ctypes.byref(plan)) == SHAPE
+    assert not plan.value
 
 
 def test_plan_create_without_gpu_reports_no_device(pkg):
