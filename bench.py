@@ -56,7 +56,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline sampling budget over its four modes (0 disables)")
     ap.add_argument("--only", default="",
-                    help="comma list of legs: decode,gemm,sweep,c5,gate_up,cpu,copy "
+                    help="comma list of legs: decode,gemm,sweep,c5,gate_up,rmsnorm,cpu,copy "
                          "(default: all but copy)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step directly instead of replaying a HIP graph "
@@ -256,6 +256,56 @@ def gate_up_leg(torch, pkg, dev, Ms, steps, warmup, stream):
     return out
 
 
+def rmsnorm_leg(torch, pkg, dev, Ms, steps, warmup, stream):
+    """Measured fusion: RMSNorm into the c5 QKV projection's input (K=4096,
+    N=6144, bs=128, zero points) through mnb_run_rmsnorm, against the unfused
+    graph (torch's rms_norm, then the MatMulNBits node) and against the node
+    alone. M = 1 and M > 16 run fused; 2 <= M <= 16 takes the library's own
+    normalization pass before the decode kernel. Decode shapes rotate 8
+    weight copies (0.3 GB per variant), prefill shapes use one."""
+    import torch.nn.functional as F
+    W = pkg.workloads
+    p = W.Projection("qkv", 4096, 6144, 128, True, 1.0, 0.005, 0.02)
+    copies = 8
+    sets = make_device_weights(torch, p, copies, 31, dev)
+    ops = [pkg.MatMulNBits(p.K, p.N, 4, p.block_size).prepare_device(*st) for st in sets]
+    g = torch.Generator(device=dev)
+    g.manual_seed(37)
+    gamma = torch.rand(p.K, device=dev, generator=g) + 0.5
+    eps = 1e-5
+    out = []
+    for M in Ms:
+        n = copies if M <= 16 else 1
+        X = torch.randn((M, p.K), device=dev, generator=g) * 3.0
+        Y = torch.empty(M, p.N, device=dev)
+
+        def run_fused():
+            for op in ops[:n]:
+                op.run_rmsnorm(X, gamma, eps, out=Y, stream=torch.cuda.current_stream())
+
+        def run_unfused():
+            for op in ops[:n]:
+                Xn = F.rms_norm(X, (p.K,), weight=gamma, eps=eps)
+                op(Xn, out=Y, stream=torch.cuda.current_stream())
+
+        def run_plain():
+            for op in ops[:n]:
+                op(X, out=Y, stream=torch.cuda.current_stream())
+
+        r = {"M": M, "weight_copies": n}
+        for name, fn in (("fused_us", run_fused), ("unfused_us", run_unfused),
+                         ("matmul_only_us", run_plain)):
+            ms, _ = time_graph(torch, fn, steps, warmup, stream)
+            r[name] = ms * 1e3 / n
+        r["gain"] = r["unfused_us"] / r["fused_us"]
+        out.append(r)
+    for op in ops:
+        op.release()
+    del sets
+    torch.cuda.empty_cache()
+    return out
+
+
 def c5_leg(torch, pkg, dev, M, steps, warmup, stream):
     """BASELINE config c5: 32 Llama-3-8B-shaped layers (QKV, O, gate+up, down;
     bs = 128, zero points; 3.74 GB of 4-bit weights) run back to back, one
@@ -403,7 +453,7 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(device=dev)
     legs = (set(args.only.split(",")) if args.only
-            else {"decode", "gemm", "sweep", "c5", "gate_up", "cpu"})
+            else {"decode", "gemm", "sweep", "c5", "gate_up", "rmsnorm", "cpu"})
     W = pkg.workloads
 
     t_start = time.perf_counter()
@@ -446,6 +496,13 @@ def main():
             print(f"# gate/up + SiLU M={r['M']}: fused {r['fused_us']:.1f} us, unfused "
                   f"{r['unfused_us']:.1f} us ({r['gain']:.2f}x), matmul alone "
                   f"{r['matmul_only_us']:.1f} us", file=sys.stderr, flush=True)
+    rms = []
+    if "rmsnorm" in legs:
+        rms = rmsnorm_leg(torch, pkg, dev, (1, 16, 512), max(3, args.steps // 4), 2, stream)
+        for r in rms:
+            print(f"# RMSNorm + qkv M={r['M']}: fused {r['fused_us']:.1f} us, unfused "
+                  f"{r['unfused_us']:.1f} us ({r['gain']:.2f}x), matmul alone "
+                  f"{r['matmul_only_us']:.1f} us", file=sys.stderr, flush=True)
     copy = None
     if "copy" in legs:
         copy = copy_leg(torch, dev, args.steps, args.warmup, stream)
@@ -483,6 +540,7 @@ def main():
         "decode_sweep": sweep,
         "c5_layer_stack": c5,
         "gate_up_fusion": gate_up,
+        "rmsnorm_fusion": rms,
         "copy_calibration": copy,
         "timing": "eager launches" if EAGER else "HIP graph replay",
         "bench_wall_s": time.perf_counter() - t_start,

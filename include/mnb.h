@@ -136,6 +136,24 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
 int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dBias, float *dY,
                void *dWorkspace, size_t workspace_bytes, void *stream, int path);
 
+/* RMSNorm into the projection input: Y = MatMulNBits(RMSNormalization(X)),
+ * RMSNormalization(X)[m][k] = X[m][k] / sqrt(mean_k(X[m][k]^2) + epsilon)
+ * * gamma[k] (ONNX RMSNormalization-23 over the last axis with fp32 stash,
+ * the schema the roadmap targets: docs/next_steps/2026/2026_08_qwen3_inference.rst:143, 282),
+ * fused as the roadmap's "RMSNorm into packed projection input" (:371-373).
+ * dX fp32 [M, K] and dGamma fp32 [K] are device pointers, 16-byte aligned,
+ * K % 4 == 0 (else MNB_ERR_UNSUPPORTED); epsilon >= 0. M = 1 on the decode
+ * path: one kernel (the GEMV reduces the row's mean square while staging it);
+ * the GEMM path: a per-row 1/rms pass, then gamma and 1/rms folded into the
+ * GEMM's conversion of A to fp16; every other path: the normalized input is
+ * written to the workspace first. Works on gate/up plans too (H of the
+ * normalized input). The workspace is required:
+ * mnb_rmsnorm_workspace_bytes. */
+int mnb_rmsnorm_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
+int mnb_run_rmsnorm(const mnb_plan *plan, int64_t M, const float *dX, const float *dGamma,
+                    float epsilon, float *dY, void *dWorkspace, size_t workspace_bytes,
+                    void *stream);
+
 /* Which path mnb_run takes for M rows (1, 2 or 3 as in mnb_run_path). */
 int mnb_select_path(const mnb_plan *plan, int64_t M, int *path);
 

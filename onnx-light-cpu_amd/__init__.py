@@ -59,6 +59,8 @@ def library():
                                              ctypes.POINTER(vp)]
         L.mnb_plan_create_gate_up.argtypes = [ctypes.POINTER(MnbDesc), vp, vp, vp, vp, vp, vp,
                                               ctypes.POINTER(vp)]
+        L.mnb_rmsnorm_workspace_bytes.argtypes = [vp, i64, ctypes.POINTER(sz)]
+        L.mnb_run_rmsnorm.argtypes = [vp, i64, vp, vp, ctypes.c_float, vp, vp, sz, vp]
         L.mnb_plan_destroy.argtypes = [vp]
         L.mnb_workspace_bytes.argtypes = [vp, i64, ctypes.POINTER(sz)]
         L.mnb_run.argtypes = [vp, i64, vp, vp, vp, sz, vp]
@@ -76,7 +78,8 @@ def library():
         for name in ("mnb_plan_create", "mnb_plan_create_device", "mnb_plan_destroy",
                      "mnb_workspace_bytes", "mnb_run", "mnb_run_path", "mnb_select_path",
                      "mnb_weight_bytes", "mnb_run_ex", "mnb_qdq_repack",
-                     "mnb_plan_create_gate_up"):
+                     "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes",
+                     "mnb_run_rmsnorm"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib
@@ -225,6 +228,34 @@ class MatMulNBits:
                                     _dev_ptr(work), 0 if work is None else work.numel(),
                                     ctypes.c_void_p(s.cuda_stream), path),
                "run")
+        return out
+
+    def run_rmsnorm(self, X, gamma, eps: float = 1e-5, out=None, stream=None):
+        """Y = this node applied to RMSNormalization(X) (last axis, scale
+        gamma [K]), the normalization fused into the run (mnb_run_rmsnorm)."""
+        import torch
+        if not self._plan:
+            raise ValueError(f"{KERNEL_PREFIX}: prepare() was not called")
+        K = self.desc.K
+        if (not X.is_cuda or X.dtype != torch.float32 or X.shape[-1] != K
+                or gamma.numel() != K or gamma.dtype != torch.float32):
+            raise ValueError(f"{KERNEL_PREFIX}: X must be float32 [..., K] and gamma float32 [K] "
+                             "device tensors")
+        X2 = X.reshape(-1, K).contiguous()
+        g = gamma.contiguous()
+        M = X2.shape[0]
+        if out is None:
+            out = torch.empty(*X.shape[:-1], self.desc.N, device=X.device, dtype=torch.float32)
+        n = ctypes.c_size_t()
+        _check(library().mnb_rmsnorm_workspace_bytes(self._plan, M, ctypes.byref(n)),
+               "rmsnorm workspace")
+        if self._work is None or self._work.numel() < n.value or self._work.device != X.device:
+            self._work = torch.empty(max(n.value, 1), dtype=torch.uint8, device=X.device)
+        s = stream if stream is not None else torch.cuda.current_stream(X.device)
+        _check(library().mnb_run_rmsnorm(self._plan, M, _dev_ptr(X2), _dev_ptr(g), float(eps),
+                                         _dev_ptr(out), _dev_ptr(self._work), self._work.numel(),
+                                         ctypes.c_void_p(s.cuda_stream)),
+               "run_rmsnorm")
         return out
 
     def workspace_bytes(self, M: int) -> int:

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -148,7 +149,61 @@ hipError_t LaunchSiluMul(const float *Y, float *H, int64_t M, int64_t N, hipStre
   return hipGetLastError();
 }
 
+// Sum over the 256 threads of a workgroup (4 wavefronts); every thread gets it.
+__device__ __forceinline__ float BlockSum256(float v, float *red) {
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// One workgroup per row: 1 / sqrt(mean(x^2) + eps), and with gamma the
+// normalized row x * inv_rms * gamma.
+template <bool WRITE>
+__global__ __launch_bounds__(256) void RmsNormKernel(const float *__restrict__ X,
+                                                     const float *__restrict__ gamma,
+                                                     float *__restrict__ Xn,
+                                                     float *__restrict__ inv_out, int64_t K,
+                                                     float eps) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float4 *x = reinterpret_cast<const float4 *>(X + row * K);
+  const int64_t n4 = K / 4;
+  float s = 0.0f;
+  for (int64_t i = threadIdx.x; i < n4; i += 256) {
+    const float4 v = x[i];
+    s += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+  }
+  const float inv = 1.0f / sqrtf(BlockSum256(s, red) / static_cast<float>(K) + eps);
+  if constexpr (WRITE) {
+    const float4 *g = reinterpret_cast<const float4 *>(gamma);
+    float4 *y = reinterpret_cast<float4 *>(Xn + row * K);
+    for (int64_t i = threadIdx.x; i < n4; i += 256) {
+      const float4 v = x[i], gg = g[i];
+      y[i] = make_float4(v.x * inv * gg.x, v.y * inv * gg.y, v.z * inv * gg.z, v.w * inv * gg.w);
+    }
+  } else if (threadIdx.x == 0) {
+    inv_out[row] = inv;
+  }
+}
+
+hipError_t LaunchRowInvRms(const float *X, float *inv_rms, int64_t M, int64_t K, float eps,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(RmsNormKernel<false>, dim3(static_cast<unsigned>(M)), dim3(256), 0, s, X,
+                     nullptr, nullptr, inv_rms, K, eps);
+  return hipGetLastError();
+}
+
+hipError_t LaunchRmsNorm(const float *X, const float *gamma, float *Xn, int64_t M, int64_t K,
+                         float eps, hipStream_t s) {
+  hipLaunchKernelGGL(RmsNormKernel<true>, dim3(static_cast<unsigned>(M)), dim3(256), 0, s, X,
+                     gamma, Xn, nullptr, K, eps);
+  return hipGetLastError();
+}
+
 } // namespace mnb
+
+static size_t Round256(size_t v) { return (v + 255) / 256 * 256; }
 
 // Bytes of the gate/up plans' scratch sum y = A * W^T (M x N floats, N = 2 I)
 // at the front of the workspace, rounded up to keep what follows aligned.
@@ -363,8 +418,12 @@ int mnb_select_path(const mnb_plan *plan, int64_t M, int *path) {
   return MNB_OK;
 }
 
-int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dBias, float *dY,
-               void *dWorkspace, size_t workspace_bytes, void *stream, int path) {
+// One run of the plan. With gamma, dA is the un-normalized input of a fused
+// RMSNorm: only the M = 1 GEMV (which reduces the row itself) and the GEMM
+// (given inv_rms) take it; mnb_run_rmsnorm normalizes the input for the rest.
+static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float *dBias, float *dY,
+                   void *dWorkspace, size_t workspace_bytes, void *stream, int path,
+                   const float *gamma, float eps, const float *inv_rms) {
   if (plan == nullptr) return MNB_ERR_NULL_POINTER;
   if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
   if (M == 0) return MNB_OK;
@@ -407,11 +466,11 @@ int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dB
   switch (path) {
   case 1:
     if (M == 1 && mnb::GemvM1Supports(plan->view)) {
-      e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0, H);
+      e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0, H, gamma, eps);
       fused = true;
       if (e == hipErrorInvalidValue && H != nullptr) {
         // no shape with paired rows for this plan: plain launch, then the pass
-        e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0);
+        e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0, nullptr, gamma, eps);
         fused = false;
       }
     } else if (UsesMfmaDecode(plan, M) &&
@@ -427,7 +486,7 @@ int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dB
   case 2:
     // The GEMM's fused stores address H with 32-bit byte offsets.
     fused = H != nullptr && M * plan->view.N * 2 < (int64_t{1} << 31);
-    e = mnb::LaunchGemm(plan->view, M, dA, Ys, work, s, fused ? H : nullptr);
+    e = mnb::LaunchGemm(plan->view, M, dA, Ys, work, s, fused ? H : nullptr, gamma, inv_rms);
     break;
   default: e = mnb::LaunchGeneric(plan->view, M, dA, Ys, s); break;
   }
@@ -438,6 +497,71 @@ int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dB
     return MNB_ERR_HIP;
   }
   return MNB_OK;
+}
+
+int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dBias, float *dY,
+               void *dWorkspace, size_t workspace_bytes, void *stream, int path) {
+  return RunImpl(plan, M, dA, dBias, dY, dWorkspace, workspace_bytes, stream, path, nullptr, 0.0f,
+                 nullptr);
+}
+
+// Workspace of mnb_run_rmsnorm: the normalized input (paths without the
+// fused RMSNorm), the rows' 1 / rms (GEMM), then mnb_run's workspace.
+static size_t RmsFrontBytes(const mnb_plan *plan, int64_t M) {
+  return Round256(static_cast<size_t>(M) * plan->view.K * 4) + Round256(static_cast<size_t>(M) * 4);
+}
+
+int mnb_rmsnorm_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
+  if (plan == nullptr || bytes == nullptr) return MNB_ERR_NULL_POINTER;
+  size_t rest = 0;
+  const int st = mnb_workspace_bytes(plan, M, &rest);
+  if (st != MNB_OK) return st;
+  *bytes = RmsFrontBytes(plan, M) + rest;
+  return MNB_OK;
+}
+
+int mnb_run_rmsnorm(const mnb_plan *plan, int64_t M, const float *dX, const float *dGamma,
+                    float epsilon, float *dY, void *dWorkspace, size_t workspace_bytes,
+                    void *stream) {
+  if (plan == nullptr) return MNB_ERR_NULL_POINTER;
+  if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
+  if (M == 0) return MNB_OK;
+  if (dX == nullptr || dGamma == nullptr || dY == nullptr) return MNB_ERR_NULL_POINTER;
+  if (!(epsilon >= 0.0f) || !std::isfinite(epsilon)) return MNB_ERR_BAD_ATTRIBUTE;
+  if ((plan->view.K % 4) != 0 || (reinterpret_cast<uintptr_t>(dX) % 16) != 0 ||
+      (reinterpret_cast<uintptr_t>(dGamma) % 16) != 0)
+    return MNB_ERR_UNSUPPORTED;
+  const size_t front = RmsFrontBytes(plan, M);
+  if (dWorkspace == nullptr || workspace_bytes < front ||
+      (reinterpret_cast<uintptr_t>(dWorkspace) % 16) != 0)
+    return MNB_ERR_WORKSPACE;
+  float *Xn = static_cast<float *>(dWorkspace);
+  float *inv = reinterpret_cast<float *>(static_cast<char *>(dWorkspace) +
+                                         Round256(static_cast<size_t>(M) * plan->view.K * 4));
+  void *rest = static_cast<char *>(dWorkspace) + front;
+  const size_t rest_bytes = workspace_bytes - front;
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur != plan->device) return MNB_ERR_NO_DEVICE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int path = SelectPath(plan, M, dX);
+  hipError_t e = hipSuccess;
+  if (path == 1 && M == 1 && mnb::GemvM1Supports(plan->view))
+    return RunImpl(plan, M, dX, nullptr, dY, rest, rest_bytes, stream, path, dGamma, epsilon,
+                   nullptr);
+  if (path == 2) {
+    e = mnb::LaunchRowInvRms(dX, inv, M, plan->view.K, epsilon, s);
+    if (e != hipSuccess) {
+      SetLastError("kernel launch", e);
+      return MNB_ERR_HIP;
+    }
+    return RunImpl(plan, M, dX, nullptr, dY, rest, rest_bytes, stream, path, dGamma, epsilon, inv);
+  }
+  e = mnb::LaunchRmsNorm(dX, dGamma, Xn, M, plan->view.K, epsilon, s);
+  if (e != hipSuccess) {
+    SetLastError("kernel launch", e);
+    return MNB_ERR_HIP;
+  }
+  return RunImpl(plan, M, Xn, nullptr, dY, rest, rest_bytes, stream, path, nullptr, 0.0f, nullptr);
 }
 
 int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,

@@ -129,7 +129,9 @@ __device__ __forceinline__ uint4 DequantWord(uint32_t w, const DequantRow &r,
 template <int BM>
 __global__ __launch_bounds__(256) void ConvertAKernel(const float *__restrict__ A,
                                                       uint4 *__restrict__ Ah, int M, int K,
-                                                      int64_t total_units) {
+                                                      int64_t total_units,
+                                                      const float *__restrict__ gamma,
+                                                      const float *__restrict__ inv_rms) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (g >= total_units) return;
   const int units_per_row = K / 8;
@@ -138,7 +140,15 @@ __global__ __launch_bounds__(256) void ConvertAKernel(const float *__restrict__ 
   uint4 out = make_uint4(0u, 0u, 0u, 0u);
   if (row < M) {
     const float4 *src = reinterpret_cast<const float4 *>(A + row * K + 8 * ku);
-    const float4 x = src[0], y = src[1];
+    float4 x = src[0], y = src[1];
+    if (gamma != nullptr) {
+      // RMSNorm folded into the rounding: x * inv_rms[row] * gamma[k]
+      const float r = inv_rms[row];
+      const float4 g0 = reinterpret_cast<const float4 *>(gamma + 8 * ku)[0];
+      const float4 g1 = reinterpret_cast<const float4 *>(gamma + 8 * ku)[1];
+      x = make_float4(x.x * r * g0.x, x.y * r * g0.y, x.z * r * g0.z, x.w * r * g0.w);
+      y = make_float4(y.x * r * g1.x, y.y * r * g1.y, y.z * r * g1.z, y.w * r * g1.w);
+    }
     out = make_uint4(PackHalf2(x.x, y.x), PackHalf2(x.y, y.y), PackHalf2(x.z, y.z),
                      PackHalf2(x.w, y.w));
   }
@@ -521,12 +531,14 @@ hipError_t LaunchT(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, fl
 
 template <int BM>
 hipError_t LaunchBM(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                    const Shape &sh, hipStream_t s, float *H) {
+                    const Shape &sh, hipStream_t s, float *H, const float *gamma,
+                    const float *inv_rms) {
   uint4 *Ah = static_cast<uint4 *>(work);
   float *partials = reinterpret_cast<float *>(static_cast<char *>(work) + AImageBytes(w, M));
   const int64_t units = (M + BM - 1) / BM * BM * (w.K / 8);
   hipLaunchKernelGGL(ConvertAKernel<BM>, dim3(static_cast<unsigned>((units + 255) / 256)),
-                     dim3(256), 0, s, A, Ah, static_cast<int>(M), static_cast<int>(w.K), units);
+                     dim3(256), 0, s, A, Ah, static_cast<int>(M), static_cast<int>(w.K), units,
+                     gamma, inv_rms);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // Gate/up activation: fused into the GEMM's stores with one split, into the
@@ -580,20 +592,21 @@ bool GemmSupports(const WeightView &w, int64_t M) {
 }
 
 hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                           hipStream_t s, int bm, int splits, float *H) {
+                           hipStream_t s, int bm, int splits, float *H, const float *gamma,
+                           const float *inv_rms) {
   Shape sh = PickShape(w, M);
   if (bm > 0) sh = MakeShape(w, bm, splits > 0 ? splits : 1);
   switch (sh.bm) {
-  case 32: return LaunchBM<32>(w, M, A, Y, work, sh, s, H);
-  case 64: return LaunchBM<64>(w, M, A, Y, work, sh, s, H);
-  case 128: return LaunchBM<128>(w, M, A, Y, work, sh, s, H);
+  case 32: return LaunchBM<32>(w, M, A, Y, work, sh, s, H, gamma, inv_rms);
+  case 64: return LaunchBM<64>(w, M, A, Y, work, sh, s, H, gamma, inv_rms);
+  case 128: return LaunchBM<128>(w, M, A, Y, work, sh, s, H, gamma, inv_rms);
   default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                      hipStream_t s, float *H) {
-  return LaunchGemmShape(w, M, A, Y, work, s, 0, 0, H);
+                      hipStream_t s, float *H, const float *gamma, const float *inv_rms) {
+  return LaunchGemmShape(w, M, A, Y, work, s, 0, 0, H, gamma, inv_rms);
 }
 
 } // namespace mnb

@@ -112,18 +112,30 @@ __host__ __device__ inline size_t AsumOffsetF4(int nchunks) { return static_cast
 __host__ __device__ inline size_t PairsOffsetF2(int nchunks) {
   return (AsumOffsetF4(nchunks) * 16 + (static_cast<size_t>(nchunks) + 1) * 4 + 7) / 8;
 }
-inline size_t LdsBytes(int nchunks, int wave_rows, int64_t nb) {
+// Byte offset of the 16 per-wavefront partial sums of squares (RMSNorm).
+__host__ __device__ inline size_t SqOffsetBytes(int nchunks, int wave_rows, int64_t nb) {
   return (PairsOffsetF2(nchunks) + static_cast<size_t>(wave_rows) * nb + 4) * 8;
+}
+inline size_t LdsBytes(int nchunks, int wave_rows, int64_t nb) {
+  return SqOffsetBytes(nchunks, wave_rows, nb) + 16 * sizeof(float);
 }
 
 // A float4 f of the chunk layout: stored swizzled, odd k divided by 16, the
 // 8-lane DPP sum of the original values gives the chunk sum. total is a
 // multiple of 8, so the 8 lanes of a chunk are all valid or all clamped;
 // clamped lanes write to the spare slots.
+// With RMS (RMSNorm fused into the input): the stored value is x * gamma and
+// sq accumulates x * x of the valid lanes.
+template <bool RMS>
 __device__ __forceinline__ void StoreA(float4 *lds4, float *asum_lds, int nchunks, int f, int total,
-                                       float4 t) {
+                                       float4 t, float4 g, float &sq) {
   const int c = f >> 3, v = f & 7;
   const bool valid = f < total;
+  if constexpr (RMS) {
+    const float q = (t.x * t.x + t.y * t.y) + (t.z * t.z + t.w * t.w);
+    sq += valid ? q : 0.0f;
+    t = make_float4(t.x * g.x, t.y * g.y, t.z * g.z, t.w * g.w);
+  }
   float sum = (t.x + t.y) + (t.z + t.w);
   sum = DppAdd<0xB1>(sum);   // quad_perm [1,0,3,2]
   sum = DppAdd<0x4E>(sum);   // quad_perm [2,3,0,1]
@@ -134,7 +146,7 @@ __device__ __forceinline__ void StoreA(float4 *lds4, float *asum_lds, int nchunk
   asum_lds[valid && v == 0 ? c : nchunks] = sum;
 }
 
-template <int CPL, int R, bool FULL, bool HAS_ZP, int PW>
+template <int CPL, int R, bool FULL, bool HAS_ZP, int PW, bool RMS>
 __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A,
                                                      const uint8_t *__restrict__ B,
                                                      const float *__restrict__ S,
@@ -142,7 +154,8 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
                                                      float *__restrict__ Y, int K, int N, int nb,
                                                      int chunk_shift, int row_bytes,
                                                      int zp_row_bytes, int G,
-                                                     float *__restrict__ H) {
+                                                     float *__restrict__ H,
+                                                     const float *__restrict__ gamma, float eps) {
   extern __shared__ float4 lds4[];
   const int nchunks = K >> 5;
   const int tid = threadIdx.x, nthreads = blockDim.x;
@@ -175,11 +188,17 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
   // around a load makes the compiler wait for it at the join.
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, 0x7FFFFFFF, 0x00020000);
-  float4 ta[kAPasses];
+  float4 ta[kAPasses], tg[kAPasses];
+  const __amdgpu_buffer_rsrc_t rgm = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(RMS ? gamma : A), 0, 0x7FFFFFFF, 0x00020000);
 #pragma unroll
-  for (int p = 0; p < kAPasses; ++p)
+  for (int p = 0; p < kAPasses; ++p) {
     ta[p] = __builtin_bit_cast(
         float4, __builtin_amdgcn_raw_buffer_load_b128(ra, min(nthreads * p + tid, total - 1) * 16, 0, 0));
+    if constexpr (RMS)
+      tg[p] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rgm, min(nthreads * p + tid, total - 1) * 16, 0, 0));
+  }
   // (scale, zp): with one row per wavefront (long rows), each lane loads the
   // scale and zero-point byte of its own chunks straight into registers;
   // otherwise the wavefront stages its rows' pairs in LDS (fewer load
@@ -234,13 +253,30 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
 
   // 3. LDS stores of A; further passes (long K) load and store behind the
   //    weights.
+  float sq = 0.0f;
 #pragma unroll
-  for (int p = 0; p < kAPasses; ++p) StoreA(lds4, asum_lds, nchunks, nthreads * p + tid, total, ta[p]);
+  for (int p = 0; p < kAPasses; ++p)
+    StoreA<RMS>(lds4, asum_lds, nchunks, nthreads * p + tid, total, ta[p], tg[p], sq);
   for (int f0 = nthreads * kAPasses; f0 < total; f0 += nthreads) {
     const int f = f0 + tid;
-    StoreA(lds4, asum_lds, nchunks, f, total, src[min(f, total - 1)]);
+    const float4 g = RMS ? reinterpret_cast<const float4 *>(gamma)[min(f, total - 1)] : float4{};
+    StoreA<RMS>(lds4, asum_lds, nchunks, f, total, src[min(f, total - 1)], g, sq);
+  }
+  float *sq_lds = reinterpret_cast<float *>(reinterpret_cast<char *>(lds4) +
+                                            SqOffsetBytes(nchunks, nthreads / 64 * R, nb));
+  if constexpr (RMS) {
+    const float wsq = WaveTotal(sq);
+    if (lane == 0) sq_lds[wave] = wsq;
   }
   __syncthreads();
+  // RMSNorm: 1 / sqrt(mean(x^2) + eps), applied to the row totals (the staged
+  // A already carries gamma).
+  float inv_rms = 1.0f;
+  if constexpr (RMS) {
+    float tot = 0.0f;
+    for (int w = 0; w < nthreads / 64; ++w) tot += sq_lds[w];
+    inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+  }
 
   // The wavefront's own pairs: stored after the barrier, which therefore
   // never waits for the (cold) scales.
@@ -312,6 +348,7 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
     const float t = WaveTotal(acc[r]);
     mine = lane == r ? t : mine;
   }
+  if constexpr (RMS) mine *= inv_rms;
   if (H != nullptr) {
     // Gate/up pairs: band row 2n is a gate, 2n + 1 its up (R and G even, so a
     // pair never straddles wavefronts or bands).
@@ -387,7 +424,7 @@ inline Shape PickShape(const WeightView &w, int cpl, int G, int R) {
 
 template <int CPL, int R, bool HAS_ZP>
 hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s, const Shape &sh,
-                   float *H) {
+                   float *H, const float *gamma, float eps) {
   const bool full = (w.K / 32) == 64 * CPL;
   const bool quads = (w.nb % 4) == 0;
   const dim3 grid(static_cast<unsigned>(sh.grid)), block(static_cast<unsigned>(sh.waves * 64));
@@ -395,8 +432,12 @@ hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s,
   const int cs = w.log2_bs - 5, rb = static_cast<int>(w.row_bytes);
   const int zb = static_cast<int>(w.zp_row_bytes);
 #define MNB_M1_LAUNCH(FULLV, PWV)                                                                  \
-  hipLaunchKernelGGL((GemvM1Kernel<CPL, R, FULLV, HAS_ZP, PWV>), grid, block, sh.lds, s, A, w.B,  \
-                     w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G, H)
+  if (gamma != nullptr)                                                                            \
+    hipLaunchKernelGGL((GemvM1Kernel<CPL, R, FULLV, HAS_ZP, PWV, true>), grid, block, sh.lds, s,  \
+                       A, w.B, w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G, H, gamma, eps);    \
+  else                                                                                             \
+    hipLaunchKernelGGL((GemvM1Kernel<CPL, R, FULLV, HAS_ZP, PWV, false>), grid, block, sh.lds, s, \
+                       A, w.B, w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G, H, gamma, eps)
   if (full) {
     if (quads) MNB_M1_LAUNCH(true, 4);
     else MNB_M1_LAUNCH(true, 1);
@@ -410,7 +451,7 @@ hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s,
 
 template <int CPL, bool HAS_ZP>
 hipError_t LaunchC(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R,
-                   float *H) {
+                   float *H, const float *gamma, float eps) {
   Shape sh = PickShape(w, CPL, G, R);
   if (H != nullptr && (sh.R < 2 || (sh.G & 1) != 0)) {
     // Gate/up epilogue: an even number of rows per wavefront and per band.
@@ -423,13 +464,13 @@ hipError_t LaunchC(const WeightView &w, const float *A, float *Y, hipStream_t s,
   if (sh.waves < 1 || sh.waves > kMaxWaves || sh.lds > 160 * 1024 || sh.R > kRMax)
     return hipErrorInvalidValue;
   switch (sh.R) {
-  case 1: return LaunchT<CPL, 1, HAS_ZP>(w, A, Y, s, sh, H);
-  case 2: return LaunchT<CPL, 2, HAS_ZP>(w, A, Y, s, sh, H);
+  case 1: return LaunchT<CPL, 1, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps);
+  case 2: return LaunchT<CPL, 2, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps);
   case 4:
-    if constexpr (kRMax >= 4) return LaunchT<CPL, 4, HAS_ZP>(w, A, Y, s, sh, H);
+    if constexpr (kRMax >= 4) return LaunchT<CPL, 4, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps);
     return hipErrorInvalidValue;
   case 8:
-    if constexpr (kRMax >= 8) return LaunchT<CPL, 8, HAS_ZP>(w, A, Y, s, sh, H);
+    if constexpr (kRMax >= 8) return LaunchT<CPL, 8, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps);
     return hipErrorInvalidValue;
   default: return hipErrorInvalidValue;
   }
@@ -437,16 +478,16 @@ hipError_t LaunchC(const WeightView &w, const float *A, float *Y, hipStream_t s,
 
 template <bool HAS_ZP>
 hipError_t LaunchZ(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R,
-                   float *H) {
+                   float *H, const float *gamma, float eps) {
   switch ((w.K / 32 + 63) / 64) {
-  case 1: return LaunchC<1, HAS_ZP>(w, A, Y, s, G, R, H);
-  case 2: return LaunchC<2, HAS_ZP>(w, A, Y, s, G, R, H);
-  case 3: return LaunchC<3, HAS_ZP>(w, A, Y, s, G, R, H);
-  case 4: return LaunchC<4, HAS_ZP>(w, A, Y, s, G, R, H);
-  case 5: return LaunchC<5, HAS_ZP>(w, A, Y, s, G, R, H);
-  case 6: return LaunchC<6, HAS_ZP>(w, A, Y, s, G, R, H);
-  case 7: return LaunchC<7, HAS_ZP>(w, A, Y, s, G, R, H);
-  default: return LaunchC<8, HAS_ZP>(w, A, Y, s, G, R, H);
+  case 1: return LaunchC<1, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
+  case 2: return LaunchC<2, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
+  case 3: return LaunchC<3, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
+  case 4: return LaunchC<4, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
+  case 5: return LaunchC<5, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
+  case 6: return LaunchC<6, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
+  case 7: return LaunchC<7, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
+  default: return LaunchC<8, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
   }
 }
 
@@ -466,9 +507,10 @@ bool GemvM1Supports(const WeightView &w) {
 }
 
 hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
-                        int band_rows, int rows_per_wave, float *H) {
-  return w.zp ? m1::LaunchZ<true>(w, A, Y, s, band_rows, rows_per_wave, H)
-              : m1::LaunchZ<false>(w, A, Y, s, band_rows, rows_per_wave, H);
+                        int band_rows, int rows_per_wave, float *H, const float *gamma,
+                        float eps) {
+  return w.zp ? m1::LaunchZ<true>(w, A, Y, s, band_rows, rows_per_wave, H, gamma, eps)
+              : m1::LaunchZ<false>(w, A, Y, s, band_rows, rows_per_wave, H, gamma, eps);
 }
 
 } // namespace mnb

@@ -92,8 +92,14 @@ hipError_t LaunchGemvSmallMShape(const WeightView &w, int64_t M, const float *A,
 // n, row 2n + 1 its up) and the launch writes H[m][n] = SiluMul(y[m][2n],
 // y[m][2n + 1]) instead of the product y; Y is then scratch (M x N floats)
 // for the launches that need an intermediate sum, unused by the others.
+//
+// RMSNorm input (M = 1 GEMV, GEMM): with gamma (K floats, 16-byte aligned)
+// the launch multiplies RMSNorm(A) = A / sqrt(mean_k(A^2) + eps) * gamma
+// instead of A. The GEMV computes the row's mean square itself; the GEMM takes
+// inv_rms[m] = 1 / sqrt(mean_k(A[m]^2) + eps) from LaunchRowInvRms.
 hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
-                        int band_rows, int rows_per_wave, float *H = nullptr);
+                        int band_rows, int rows_per_wave, float *H = nullptr,
+                        const float *gamma = nullptr, float eps = 0.0f);
 bool GemvM1Supports(const WeightView &w);
 
 // Decode GEMV for 2 <= M <= 16 on fp16 MFMA with exact products (each
@@ -114,19 +120,29 @@ hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, f
 // holds GemmWorkspaceBytes(w, M) bytes of device memory: A rounded to fp16,
 // then the partial sums of a split-K launch.
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                      hipStream_t s, float *H = nullptr);
+                      hipStream_t s, float *H = nullptr, const float *gamma = nullptr,
+                      const float *inv_rms = nullptr);
 bool GemmSupports(const WeightView &w, int64_t M);
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M);
 // Same with an explicit tile height (32, 64 or 128; 0 picks both) and split
 // count (1..16), for tuning; `work` then holds
 // GemmShapeWorkspaceBytes(w, M, splits) bytes.
 hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                           hipStream_t s, int bm, int splits, float *H = nullptr);
+                           hipStream_t s, int bm, int splits, float *H = nullptr,
+                           const float *gamma = nullptr, const float *inv_rms = nullptr);
 size_t GemmShapeWorkspaceBytes(const WeightView &w, int64_t M, int splits);
 
 // H[m][n] = SiluMul(Y[m][2n], Y[m][2n + 1]) for an M x N (N even) Y: the
 // gate/up activation after a kernel without the fused epilogue.
 hipError_t LaunchSiluMul(const float *Y, float *H, int64_t M, int64_t N, hipStream_t s);
+
+// RMSNorm over the rows of X [M, K] (K % 4 == 0, X 16-byte aligned):
+// inv_rms[m] = 1 / sqrt(mean_k(X[m]^2) + eps); LaunchRmsNorm also writes
+// Xn[m][k] = X[m][k] * inv_rms[m] * gamma[k].
+hipError_t LaunchRowInvRms(const float *X, float *inv_rms, int64_t M, int64_t K, float eps,
+                           hipStream_t s);
+hipError_t LaunchRmsNorm(const float *X, const float *gamma, float *Xn, int64_t M, int64_t K,
+                         float eps, hipStream_t s);
 
 // Generic fallback: any K, any block_size, any M. Slow; for odd shapes and
 // cross-checks.

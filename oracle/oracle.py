@@ -201,6 +201,15 @@ def gate_up_silu_f64(A, Bg, Sg, Zg, Bu, Su, Zu, K, N, bs, threads=None):
     return silu_mul_f64(g, u)
 
 
+def rmsnorm_f64(X, gamma, eps):
+    """ONNX RMSNormalization-23 over the last axis in fp64:
+    X / sqrt(mean(X^2) + eps) * gamma (the schema the roadmap targets,
+    docs/next_steps/2026/2026_08_qwen3_inference.rst:143, 282)."""
+    X = np.asarray(X, np.float64)
+    ms = np.mean(X * X, axis=-1, keepdims=True)
+    return X / np.sqrt(ms + eps) * np.asarray(gamma, np.float64)
+
+
 def f32_to_f16_bits(x):
     x = np.ascontiguousarray(x, dtype=np.float32).ravel()
     out = np.empty(x.size, np.uint16)

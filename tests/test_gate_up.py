@@ -50,3 +50,23 @@ def test_gate_up_oracle_against_dequantized_weights(pkg, orc, zp):
     want = g / (1.0 + np.exp(-g)) * u
     got = orc.gate_up_silu_f64(A, Bg, Sg, Zg, Bu, Su, Zu, K, N, bs)
     np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_rmsnorm_oracle_closed_forms(orc):
+    """ONNX RMSNormalization pinned by what it must satisfy: a constant row c
+    maps to gamma * c / sqrt(c^2 + eps); with eps = 0 the output is invariant
+    to scaling the row and has unit root-mean-square before gamma; a row of
+    unit RMS passes through as x * gamma / sqrt(1 + eps)."""
+    K = 64
+    g = np.linspace(0.5, 2.0, K)
+    c = -3.0
+    np.testing.assert_allclose(orc.rmsnorm_f64(np.full(K, c), g, 1e-5),
+                               g * c / np.sqrt(c * c + 1e-5), rtol=1e-15)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((3, K))
+    y = orc.rmsnorm_f64(x, np.ones(K), 0.0)
+    np.testing.assert_allclose(np.sqrt(np.mean(y * y, axis=-1)), 1.0, rtol=1e-14)
+    np.testing.assert_allclose(orc.rmsnorm_f64(1e3 * x, g, 0.0), orc.rmsnorm_f64(x, g, 0.0),
+                               rtol=1e-13)
+    u = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True))
+    np.testing.assert_allclose(orc.rmsnorm_f64(u, g, 0.25), u * g / np.sqrt(1.25), rtol=1e-14)
