@@ -105,8 +105,9 @@ int mnb_plan_destroy(mnb_plan *plan);
  *    ceil(M/128)*128*K*2 bytes, then, when the GEMM splits K into S > 1
  *    parts, (S - 1)*M*N*4 bytes of fp32 partial sums (S <= 16, chosen from
  *    the shape);
- *  - for 5 <= M <= 16, the MFMA decode kernel's: (K/512 - 1)*M*N*4 bytes of
- *    fp32 partial sums of its 512-k ranges.
+ *  - where the MFMA decode kernel serves M (5 <= M <= 16, from M = 4 or 3 for
+ *    wide weights, as mnb_run), its (K/512 - 1)*M*N*4 bytes of fp32
+ *    partial sums of its 512-k ranges.
  * Without it (NULL or smaller) the decode path runs its fp32-FMA kernels. */
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
 
@@ -114,11 +115,12 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
  * plan's device. M == 0 is a no-op. Replaces the operator's compute call,
  * MatMulKernel::operator() -> MatMulPlan<float>::Execute
  * (onnx_light_cpu/kernels/math/matmul_kernel.cc:117-134, gemm_plan.cc:539-570).
- * M <= 4: fp32-FMA decode GEMV; 5 <= M <= 16: decode GEMV on fp16 MFMA with
- * exact products (A split into three fp16 terms after a power-of-two
- * scaling) and fp32 sums; M > 16: fp16-MFMA prefill GEMM with A rounded to
- * fp16 (round to nearest even, half_conversion.h:42-78) and fp32
- * accumulation. The launch is asynchronous on `stream`. */
+ * M <= 4: fp32-FMA decode GEMV; 5 <= M <= 16 (from M = 4 when N >= 3K,
+ * M = 3 when N >= 6K): decode GEMV on fp16 MFMA with exact products (A split
+ * into three fp16 terms after a power-of-two scaling) and fp32 sums;
+ * M > 16: fp16-MFMA prefill GEMM with A rounded to fp16 (round to nearest
+ * even, half_conversion.h:42-78) and fp32 accumulation. The launch is
+ * asynchronous on `stream`. */
 int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
             size_t workspace_bytes, void *stream);
 

@@ -377,11 +377,23 @@ int mnb_plan_destroy(mnb_plan *plan) {
 
 // Rows from which the decode path multiplies on MFMA (when the caller passes
 // the workspace): below it the fp32-FMA kernels are faster, their cost
-// growing with M while the MFMA kernel's barely does.
-constexpr int64_t kMfmaDecodeMinRows = 5;
+// growing by about one M = 1 pass per token while the MFMA kernel's barely
+// changes with M. Where the MFMA kernel starts ahead depends on the shape: it
+// splits K into 512-k ranges, so wide, short weights (N large against K) give
+// it more rows per range and fewer partial sums. Measured on MI355X (FMA
+// against MFMA with its partial-sum pass, c1-c5 shapes, M = 2..5): at M = 4
+// it wins for N >= 3K (c2 16.8 against 19.7 us, c5 gate+up 25.6 against
+// 32.2) and loses below (c1, c3, c5 qkv, o, down by 20-40%); at M = 3 it wins
+// for N >= 6K (gate+up 25.1 against 27.0), ties at c2; from M = 5 it is
+// ahead or within 5% everywhere.
+static int64_t MfmaDecodeMinRows(const mnb::WeightView &w) {
+  if (w.N >= 6 * w.K) return 3;
+  if (w.N >= 3 * w.K) return 4;
+  return 5;
+}
 
 static bool UsesMfmaDecode(const mnb_plan *plan, int64_t M) {
-  return M >= kMfmaDecodeMinRows && M <= 16 && mnb::GemvMfmaSupports(plan->view, M);
+  return M >= MfmaDecodeMinRows(plan->view) && M <= 16 && mnb::GemvMfmaSupports(plan->view, M);
 }
 
 static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
