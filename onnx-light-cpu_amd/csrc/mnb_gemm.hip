@@ -415,6 +415,33 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
     return;
   }
   if (split > 0) Y = partials + static_cast<size_t>(split - 1) * M * N;
+  if (N < (1 << 22)) {
+    // Buffer stores at byte offsets from this tile's first output row (below
+    // 2^31 for N < 2^22): rows past M fall beyond the resource and columns
+    // past N are sent there, so no store needs a branch.
+    const auto yr = __builtin_amdgcn_make_buffer_rsrc(Y + static_cast<size_t>(m0) * N, 0,
+                                                      min(M - m0, BM) * N * 4, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int gn = n0 + wn * 64 + j * 16 + (lane & 15);
+        const int row = wm * (BM / 2) + i * 16 + 4 * (lane >> 4);
+        const int off = gn < N ? (row * N + gn) * 4 : 0x7FFFFFF0;
+        // (one element of the MFMA result vector at a time, through a scalar:
+        // a bit cast of the vector element itself was compiled into a store of
+        // element 0 for every v on ROCm 7.2)
+        const floatx4 a = acc[i][j];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float val = a[v];
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), yr,
+                                                gn < N ? off + v * N * 4 : off, 0, 0);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < kMI; ++i) {
 #pragma unroll
