@@ -458,16 +458,22 @@ struct Shape {
   int bsc, rb, splits, wgs_per_split, waves_per_split, pairs;
 };
 
-// Row blocks of 16 per item (RB) and the grid: about two workgroups per CU
-// (a whole number of them per split), each wavefront with one or two pairs
-// of items (more workgroups when the rows need it).
+// Row blocks of 16 per item (RB) and the grid: a target number of
+// workgroups per CU (a whole number of them per split), each wavefront with
+// one or two pairs of items (more workgroups when the rows need it).
+// Defaults from a sweep of RB in {1, 2} against 1..4 workgroups per CU on
+// MI355X (c2, c3, c5 shapes, M = 8 and 16): one row block for long rows
+// (K >= 8192: c3 and c5 down 13% faster than two), two for short ones; one
+// workgroup per CU (c5 qkv 20%, c2 3-5% faster than two) except for weights
+// at least six times wider than deep (c5 gate+up: two).
 inline Shape PickShape(const WeightView &w, int rb, int wgs_per_cu) {
   Shape sh;
   sh.bsc = std::min(4, w.block_size / 32);
   sh.splits = static_cast<int>(w.K / kKR);
-  sh.rb = rb > 0 ? rb : 2;
+  sh.rb = rb > 0 ? rb : (w.K >= 8192 ? 1 : 2);
   const int64_t items = (w.N + 16 * sh.rb - 1) / (16 * sh.rb);  // per split
-  const int64_t target = static_cast<int64_t>(w.num_cus) * (wgs_per_cu > 0 ? wgs_per_cu : 2);
+  const int wpc = wgs_per_cu > 0 ? wgs_per_cu : (w.N >= 6 * w.K ? 2 : 1);
+  const int64_t target = static_cast<int64_t>(w.num_cus) * wpc;
   int64_t wps = std::max<int64_t>(1, (target + sh.splits - 1) / sh.splits);
   wps = std::min(wps, (items + kWaves - 1) / kWaves);       // no workgroup without an item
   wps = std::max(wps, (items + 4 * kWaves - 1) / (4 * kWaves));  // at most two pairs
