@@ -41,11 +41,11 @@ ROTATION_BYTES = 1 << 30
 
 # HBM bytes per launch of the headline kernel (GemvM1Kernel on c2 M=1), from
 # two rocprofv3 --pmc passes over `bench.py --only decode,gemm,sweep,copy
-# --eager --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15524.7 KiB and
+# --eager --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15526.5 KiB and
 # WRITE_SIZE 80.0 KiB per dispatch, each scaled by what the same counter reads
-# for the copy leg's 512 MiB device copy (FETCH_SIZE 262157.1 KiB -> x1.99990,
+# for the copy leg's 512 MiB device copy (FETCH_SIZE 262156.8 KiB -> x1.99990,
 # WRITE_SIZE 524288.0 KiB -> x1.00000). Re-measure when the kernel changes.
-GEMV_M1_C2_TRAFFIC_BYTES = round((15524.7 * (524288.0 / 262157.1) + 80.0) * 1024)
+GEMV_M1_C2_TRAFFIC_BYTES = round((15526.5 * (524288.0 / 262156.8) + 80.0) * 1024)
 
 
 def parse_args():
