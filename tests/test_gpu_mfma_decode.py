@@ -133,3 +133,32 @@ def test_mfma_decode_workspace_reuse_and_fallback(pkg, orc, cuda):
             y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
             assert orc.normwise_max_error(y, y64) <= GEMV_TOL
     op.release()
+
+
+@pytest.mark.parametrize("K,N,M,mfma", [
+    (1024, 3072, 4, True),    # N >= 3K: MFMA from M = 4
+    (1024, 3072, 3, False),
+    (1024, 6144, 3, True),    # N >= 6K: MFMA from M = 3
+    (2048, 2048, 4, False),   # square: FMA up to M = 4
+])
+def test_decode_crossover_by_shape(pkg, orc, cuda, K, N, M, mfma):
+    """The automatic decode path takes the MFMA kernel from M = 4 when N >= 3K
+    and from M = 3 when N >= 6K (FMA below): it is then bit-identical to the
+    MFMA run (workspace given) or to the FMA run (no workspace), and both are
+    within the decode bound of the fp64 oracle."""
+    import torch
+    bs = 128
+    B, S, Z = _weights(pkg, K, N, bs, True, seed=K + N + M)
+    A = pkg.workloads.make_activations(M, K, 1.0, seed=M + 3)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    print(f"case decode-crossover K={K} N={N} M={M} expect_mfma={mfma}", flush=True)
+    y_ws = _run_path1(pkg, cuda, op, A, True)
+    y_fma = _run_path1(pkg, cuda, op, A, False)
+    y_auto = op(torch.from_numpy(A).to(cuda)).cpu().numpy()
+    y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
+    assert orc.normwise_max_error(y_ws, y64) <= GEMV_TOL
+    assert orc.normwise_max_error(y_fma, y64) <= GEMV_TOL
+    np.testing.assert_array_equal(y_auto, y_ws)
+    # with the workspace the MFMA kernel's summation order differs from FMA's
+    assert (not np.array_equal(y_ws, y_fma)) == mfma
+    op.release()
