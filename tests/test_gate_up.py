@@ -70,3 +70,17 @@ def test_rmsnorm_oracle_closed_forms(orc):
                                rtol=1e-13)
     u = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True))
     np.testing.assert_allclose(orc.rmsnorm_f64(u, g, 0.25), u * g / np.sqrt(1.25), rtol=1e-14)
+
+
+def test_gate_up_python_rejects_mismatched_zero_points(pkg):
+    """GateUpSiLU.prepare needs zero points on both weights or on neither (the
+    plan shares one description); the check runs before any library call."""
+    K, N, bs = 64, 8, 32
+    W = pkg.workloads
+    p = W.Projection("g", K, N, bs, True, 1.0, 0.005, 0.02)
+    Bg, Sg, Zg = W.make_weights(p, 1)
+    Bu, Su, _ = W.make_weights(p, 2)
+    with pytest.raises(ValueError, match="both have zero points or neither"):
+        pkg.GateUpSiLU(K, N, 4, bs).prepare(Bg, Sg, Zg, Bu, Su, None)
+    with pytest.raises(ValueError, match="B has"):
+        pkg.GateUpSiLU(K, N, 4, bs).prepare(Bg[:-1], Sg, Zg, Bu, Su, Zg)
