@@ -301,3 +301,20 @@ def test_c5_layer_projections(pkg, orc, cuda, proj, M):
         print(f"c5 {p.name} M=512: L2 relative error on {rows.size} rows {err:.3e}")
         assert err <= GEMM_TOL
         assert np.isfinite(Y).all()
+
+
+@pytest.mark.parametrize("K,N,bs,M", [
+    (16384, 200, 64, 1),    # the M = 1 kernel's largest K (8 chunks per lane)
+    (16416, 130, 32, 1),    # one chunk past it: another decode kernel serves M = 1
+    (32768, 96, 128, 8),    # the MFMA decode's largest K (64 ranges of 512)
+    (33280, 96, 128, 8),    # one range past it: the fp32-FMA kernel serves it
+])
+def test_decode_at_the_kernels_k_limits(pkg, orc, cuda, K, N, bs, M):
+    """At and just past each decode kernel's largest K the path stays correct
+    (the dispatcher switches kernels instead of overflowing a limit)."""
+    p, B, S, Z = _case(pkg, K, N, bs, True, seed=K % 1000 + N)
+    A = pkg.workloads.make_activations(M, K, 1.0, seed=M + 5)
+    Y, path = _run(pkg, cuda, K, N, bs, B, S, Z, A)
+    assert path == pkg.PATH_GEMV
+    y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
+    assert orc.normwise_max_error(Y, y64) <= GEMV_TOL
