@@ -57,7 +57,8 @@ typedef struct mnb_desc {
   int64_t N;                /* attribute N */
   int32_t bits;             /* attribute bits: 4 only */
   int32_t block_size;       /* attribute block_size: power of two >= 16 */
-  int32_t accuracy_level;   /* attribute accuracy_level: 0..4 accepted; see mnb_run */
+  int32_t accuracy_level;   /* attribute accuracy_level, 0..4: 1 keeps fp32 activations on
+                               every path (see mnb_run) */
   int32_t has_zero_points;  /* input 3 present */
 } mnb_desc;
 
@@ -101,13 +102,15 @@ int mnb_plan_destroy(mnb_plan *plan);
 
 /* Device workspace (16-byte aligned) that mnb_run and mnb_run_path need for M
  * rows, whichever path serves them (0 when none): the larger of
- *  - the prefill GEMM's: A rounded to fp16 in its tile layout,
- *    ceil(M/128)*128*K*2 bytes, then, when the GEMM splits K into S > 1
- *    parts, (S - 1)*M*N*4 bytes of fp32 partial sums (S <= 16, chosen from
- *    the shape);
- *  - where the MFMA decode kernel serves M (5 <= M <= 16, from M = 4 or 3 for
- *    wide weights, as mnb_run), its (K/512 - 1)*M*N*4 bytes of fp32
- *    partial sums of its 512-k ranges.
+ *  - the prefill GEMM's: A scaled per row by a power of two and rounded to
+ *    fp16 in its tile layout, ceil(M/128)*128*K*2 bytes, the rows' exponents
+ *    (ceil(M/128)*128 int32, rounded up to 256 bytes), then, when the GEMM
+ *    splits K into S > 1 parts, (S - 1)*M*N*4 bytes of fp32 partial sums
+ *    (S <= 16, chosen from the shape);
+ *  - where the MFMA decode kernel serves min(M, 16) rows (5 <= M <= 16, from
+ *    M = 4 or 3 for wide weights, as mnb_run; the exact route serves larger M
+ *    16 rows at a time), its (K/512 - 1)*min(M,16)*N*4 bytes of fp32 partial
+ *    sums of its 512-k ranges.
  * Without it (NULL or smaller) the decode path runs its fp32-FMA kernels. */
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
 
@@ -118,15 +121,25 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
  * M <= 4: fp32-FMA decode GEMV; 5 <= M <= 16 (from M = 4 when N >= 3K,
  * M = 3 when N >= 6K): decode GEMV on fp16 MFMA with exact products (A split
  * into three fp16 terms after a power-of-two scaling) and fp32 sums;
- * M > 16: fp16-MFMA prefill GEMM with A rounded to fp16 (round to nearest
- * even, half_conversion.h:42-78) and fp32 accumulation. The launch is
- * asynchronous on `stream`. */
+ * M > 16: fp16-MFMA prefill GEMM. Its A row m is scaled by a power of two
+ * 2^f_m (largest magnitude in [2^14, 2^15)) and rounded to fp16 (round to
+ * nearest even, half_conversion.h:42-78); each weight row's block scales are
+ * scaled by a power of two at plan time so they are normal fp16 numbers; the
+ * fp32 epilogue undoes both exactly. No finite input overflows.
+ * accuracy_level (ONNX Runtime's minimum accuracy of A: 0 unset, 1 fp32,
+ * 2 fp16, 3 bf16, 4 int8): at level 1, M > 16 runs the exact-product decode
+ * kernels 16 rows at a time (path 4) instead of the fp16 GEMM; levels 0
+ * (unset, this library's default) and 2-4 take the GEMM, whose 11-bit
+ * activations meet what levels 2-4 permit. The launch is asynchronous on
+ * `stream`. */
 int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
             size_t workspace_bytes, void *stream);
 
-/* Same as mnb_run with the kernel chosen by the caller:
- * path 0 = automatic, 1 = decode GEMV (any M <= 16), 2 = MFMA GEMM (any M),
- * 3 = generic fallback (any shape; slow, for cross-checks). */
+/* Same as mnb_run with the kernel chosen by the caller (whatever the plan's
+ * accuracy_level): path 0 = automatic, 1 = decode GEMV (any M <= 16),
+ * 2 = MFMA GEMM (any M), 3 = generic fallback (any shape; slow, for
+ * cross-checks), 4 = the decode kernels over consecutive groups of 16 rows
+ * (any M; the exact route of accuracy_level 1). */
 int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
                  size_t workspace_bytes, void *stream, int path);
 
@@ -156,7 +169,7 @@ int mnb_run_rmsnorm(const mnb_plan *plan, int64_t M, const float *dX, const floa
                     float epsilon, float *dY, void *dWorkspace, size_t workspace_bytes,
                     void *stream);
 
-/* Which path mnb_run takes for M rows (1, 2 or 3 as in mnb_run_path). */
+/* Which path mnb_run takes for M rows (1 to 4 as in mnb_run_path). */
 int mnb_select_path(const mnb_plan *plan, int64_t M, int *path);
 
 /* Text for a status code (static storage). */

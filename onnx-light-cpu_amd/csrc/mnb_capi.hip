@@ -25,6 +25,7 @@ struct mnb_plan {
   uint8_t *dB;
   float *dS;
   uint8_t *dZ;
+  int32_t *dColExp;  // always plan-owned: per weight row power-of-two scale exponent
 };
 
 namespace {
@@ -96,6 +97,7 @@ void FillView(mnb_plan *p) {
   p->view.B = p->dB;
   p->view.scales = p->dS;
   p->view.zp = p->desc.has_zero_points ? p->dZ : nullptr;
+  p->view.col_exp = p->dColExp;
   p->view.K = p->desc.K;
   p->view.N = p->desc.N;
   p->view.nb = nb;
@@ -112,9 +114,31 @@ void FreePlanMemory(mnb_plan *p) {
     if (p->dS) (void)hipFree(p->dS);
     if (p->dZ) (void)hipFree(p->dZ);
   }
+  if (p->dColExp) (void)hipFree(p->dColExp);
   p->dB = nullptr;
   p->dS = nullptr;
   p->dZ = nullptr;
+  p->dColExp = nullptr;
+}
+
+// Plan-time constants derived from the device copies of the weights (run
+// once, synchronously, on the null stream): the per-row scale exponents.
+int DerivePlanConstants(mnb_plan *p) {
+  hipError_t e = hipMalloc(reinterpret_cast<void **>(&p->dColExp),
+                           static_cast<size_t>(p->desc.N) * sizeof(int32_t));
+  if (e != hipSuccess) {
+    SetLastError("hipMalloc", e);
+    return MNB_ERR_ALLOC;
+  }
+  int64_t nb, row_bytes, zp_row_bytes;
+  Sizes(&p->desc, &nb, &row_bytes, &zp_row_bytes);
+  e = mnb::LaunchColExp(p->dS, p->dColExp, p->desc.N, nb, nullptr);
+  if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+  if (e != hipSuccess) {
+    SetLastError("plan constants", e);
+    return MNB_ERR_HIP;
+  }
+  return MNB_OK;
 }
 
 int CheckInputs(const mnb_desc *desc, const void *B, const void *scales, const void *zp,
@@ -157,13 +181,11 @@ __device__ __forceinline__ float BlockSum256(float v, float *red) {
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// One workgroup per row: 1 / sqrt(mean(x^2) + eps), and with gamma the
-// normalized row x * inv_rms * gamma.
-template <bool WRITE>
+// One workgroup per row: the normalized row x * inv_rms * gamma,
+// inv_rms = 1 / sqrt(mean(x^2) + eps).
 __global__ __launch_bounds__(256) void RmsNormKernel(const float *__restrict__ X,
                                                      const float *__restrict__ gamma,
-                                                     float *__restrict__ Xn,
-                                                     float *__restrict__ inv_out, int64_t K,
+                                                     float *__restrict__ Xn, int64_t K,
                                                      float eps) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
@@ -175,29 +197,35 @@ __global__ __launch_bounds__(256) void RmsNormKernel(const float *__restrict__ X
     s += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
   }
   const float inv = 1.0f / sqrtf(BlockSum256(s, red) / static_cast<float>(K) + eps);
-  if constexpr (WRITE) {
-    const float4 *g = reinterpret_cast<const float4 *>(gamma);
-    float4 *y = reinterpret_cast<float4 *>(Xn + row * K);
-    for (int64_t i = threadIdx.x; i < n4; i += 256) {
-      const float4 v = x[i], gg = g[i];
-      y[i] = make_float4(v.x * inv * gg.x, v.y * inv * gg.y, v.z * inv * gg.z, v.w * inv * gg.w);
-    }
-  } else if (threadIdx.x == 0) {
-    inv_out[row] = inv;
+  const float4 *g = reinterpret_cast<const float4 *>(gamma);
+  float4 *y = reinterpret_cast<float4 *>(Xn + row * K);
+  for (int64_t i = threadIdx.x; i < n4; i += 256) {
+    const float4 v = x[i], gg = g[i];
+    y[i] = make_float4(v.x * inv * gg.x, v.y * inv * gg.y, v.z * inv * gg.z, v.w * inv * gg.w);
   }
 }
 
-hipError_t LaunchRowInvRms(const float *X, float *inv_rms, int64_t M, int64_t K, float eps,
-                           hipStream_t s) {
-  hipLaunchKernelGGL(RmsNormKernel<false>, dim3(static_cast<unsigned>(M)), dim3(256), 0, s, X,
-                     nullptr, nullptr, inv_rms, K, eps);
+__global__ __launch_bounds__(256) void ColExpKernel(const float *__restrict__ S,
+                                                    int32_t *__restrict__ E, int64_t N,
+                                                    int64_t nb) {
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (n >= N) return;
+  float m = 0.0f;
+  for (int64_t b = 0; b < nb; ++b) m = fmaxf(m, fabsf(S[n * nb + b]));
+  E[n] = RangeExponent(m, kScaleExpTarget);
+}
+
+hipError_t LaunchColExp(const float *scales, int32_t *col_exp, int64_t N, int64_t nb,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(ColExpKernel, dim3(static_cast<unsigned>((N + 255) / 256)), dim3(256), 0, s,
+                     scales, col_exp, N, nb);
   return hipGetLastError();
 }
 
 hipError_t LaunchRmsNorm(const float *X, const float *gamma, float *Xn, int64_t M, int64_t K,
                          float eps, hipStream_t s) {
-  hipLaunchKernelGGL(RmsNormKernel<true>, dim3(static_cast<unsigned>(M)), dim3(256), 0, s, X,
-                     gamma, Xn, nullptr, K, eps);
+  hipLaunchKernelGGL(RmsNormKernel, dim3(static_cast<unsigned>(M)), dim3(256), 0, s, X, gamma,
+                     Xn, K, eps);
   return hipGetLastError();
 }
 
@@ -301,6 +329,12 @@ int mnb_plan_create(const mnb_desc *desc, const uint8_t *B, const float *scales,
     delete p;
     return MNB_ERR_HIP;
   }
+  st = DerivePlanConstants(p);
+  if (st != MNB_OK) {
+    FreePlanMemory(p);
+    delete p;
+    return st;
+  }
   FillView(p);
   *out_plan = p;
   return MNB_OK;
@@ -322,6 +356,12 @@ int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float 
   p->dB = const_cast<uint8_t *>(dB);
   p->dS = const_cast<float *>(dScales);
   p->dZ = const_cast<uint8_t *>(dZeroPoints);
+  st = DerivePlanConstants(p);
+  if (st != MNB_OK) {
+    FreePlanMemory(p);
+    delete p;
+    return st;
+  }
   FillView(p);
   *out_plan = p;
   return MNB_OK;
@@ -396,6 +436,9 @@ static bool UsesMfmaDecode(const mnb_plan *plan, int64_t M) {
   return M >= MfmaDecodeMinRows(plan->view) && M <= 16 && mnb::GemvMfmaSupports(plan->view, M);
 }
 
+// Rows per launch of the exact route (path 4): the decode kernels' limit.
+constexpr int64_t kExactGroupRows = 16;
+
 static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
   return need == 0 ||
          (work != nullptr && bytes >= need && (reinterpret_cast<uintptr_t>(work) % 16) == 0);
@@ -408,16 +451,34 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
   // the prefill GEMM (A rounded to fp16, tile layout, split-K partial sums)
   // and the MFMA decode kernel (split-K partial sums).
   // A gate/up plan adds the scratch sum in front of either.
+  // The exact route (path 4) runs the decode kernels over groups of at most
+  // 16 rows, one after another in the same workspace.
   size_t need = 0;
   if (M > 0 && mnb::GemmSupports(plan->view, M)) need = mnb::GemmWorkspaceBytes(plan->view, M);
-  if (UsesMfmaDecode(plan, M)) need = std::max(need, mnb::GemvMfmaWorkspaceBytes(plan->view, M));
+  const int64_t md = std::min<int64_t>(M, kExactGroupRows);
+  if (UsesMfmaDecode(plan, md)) need = std::max(need, mnb::GemvMfmaWorkspaceBytes(plan->view, md));
   *bytes = need + GateUpScratchBytes(plan, M);
   return MNB_OK;
+}
+
+// accuracy_level is ONNX Runtime's MatMulNBits attribute: the lowest accuracy
+// at which A may enter the computation (0 unset, 1 fp32, 2 fp16, 3 bf16,
+// 4 int8). Level 1 asks for fp32 activations, so its rows never take the
+// fp16 GEMM: above 16 rows they go through the exact-product decode kernels,
+// 16 rows at a time (path 4). Levels 0 (unset: the library's default), 2, 3
+// and 4 take the fp16 GEMM above 16 rows, whose activations keep an 11-bit
+// significand with per-row range scaling: at least the accuracy levels 2-4
+// permit. Every level runs the exact decode kernels up to 16 rows.
+static bool Fp32ActivationsOnly(const mnb_plan *plan) { return plan->desc.accuracy_level == 1; }
+
+static bool ExactGroupsSupported(const mnb_plan *plan, bool a_aligned) {
+  return a_aligned && mnb::GemvSupports(plan->view, kExactGroupRows);
 }
 
 static int SelectPath(const mnb_plan *plan, int64_t M, const float *dA) {
   const bool a_aligned = (reinterpret_cast<uintptr_t>(dA) % 16) == 0;
   if (a_aligned && M <= 16 && mnb::GemvSupports(plan->view, M)) return 1;
+  if (Fp32ActivationsOnly(plan)) return ExactGroupsSupported(plan, a_aligned) ? 4 : 3;
   if (a_aligned && mnb::GemmSupports(plan->view, M)) return 2;
   return 3;
 }
@@ -431,22 +492,36 @@ int mnb_select_path(const mnb_plan *plan, int64_t M, int *path) {
 }
 
 // One run of the plan. With gamma, dA is the un-normalized input of a fused
-// RMSNorm: only the M = 1 GEMV (which reduces the row itself) and the GEMM
-// (given inv_rms) take it; mnb_run_rmsnorm normalizes the input for the rest.
+// RMSNorm: only the M = 1 GEMV and the GEMM take it (each reduces the rows
+// itself); mnb_run_rmsnorm normalizes the input for the rest.
 static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float *dBias, float *dY,
                    void *dWorkspace, size_t workspace_bytes, void *stream, int path,
-                   const float *gamma, float eps, const float *inv_rms) {
+                   const float *gamma, float eps) {
   if (plan == nullptr) return MNB_ERR_NULL_POINTER;
   if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
   if (M == 0) return MNB_OK;
   if (dA == nullptr || dY == nullptr) return MNB_ERR_NULL_POINTER;
-  if (path < 0 || path > 3) return MNB_ERR_UNSUPPORTED;
+  if (path < 0 || path > 4) return MNB_ERR_UNSUPPORTED;
   const bool a_aligned = (reinterpret_cast<uintptr_t>(dA) % 16) == 0;
   if (path == 0) path = SelectPath(plan, M, dA);
   if (path == 1 && !(a_aligned && M <= 16 && mnb::GemvSupports(plan->view, M)))
     return MNB_ERR_UNSUPPORTED;
   if (path == 2 && !(a_aligned && mnb::GemmSupports(plan->view, M))) return MNB_ERR_UNSUPPORTED;
+  if (path == 4 && !ExactGroupsSupported(plan, a_aligned)) return MNB_ERR_UNSUPPORTED;
   if (plan->gate_up && dBias != nullptr) return MNB_ERR_UNSUPPORTED;
+  if (path == 4) {
+    // The decode kernels over consecutive groups of rows, in stream order on
+    // the one workspace (each group's launches finish reading it before the
+    // next group's start writing it).
+    const int64_t K = plan->view.K, cols = plan->gate_up ? plan->view.N / 2 : plan->view.N;
+    for (int64_t m0 = 0; m0 < M; m0 += kExactGroupRows) {
+      const int64_t mg = std::min(kExactGroupRows, M - m0);
+      const int st = RunImpl(plan, mg, dA + m0 * K, dBias, dY + m0 * cols, dWorkspace,
+                             workspace_bytes, stream, 1, nullptr, 0.0f);
+      if (st != MNB_OK) return st;
+    }
+    return MNB_OK;
+  }
   // A gate/up plan's runs start with the scratch sum; the path's own
   // workspace follows it.
   const size_t scratch = GateUpScratchBytes(plan, M);
@@ -498,7 +573,7 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   case 2:
     // The GEMM's fused stores address H with 32-bit byte offsets.
     fused = H != nullptr && M * plan->view.N * 2 < (int64_t{1} << 31);
-    e = mnb::LaunchGemm(plan->view, M, dA, Ys, work, s, fused ? H : nullptr, gamma, inv_rms);
+    e = mnb::LaunchGemm(plan->view, M, dA, Ys, work, s, fused ? H : nullptr, gamma, eps);
     break;
   default: e = mnb::LaunchGeneric(plan->view, M, dA, Ys, s); break;
   }
@@ -513,14 +588,13 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
 
 int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dBias, float *dY,
                void *dWorkspace, size_t workspace_bytes, void *stream, int path) {
-  return RunImpl(plan, M, dA, dBias, dY, dWorkspace, workspace_bytes, stream, path, nullptr, 0.0f,
-                 nullptr);
+  return RunImpl(plan, M, dA, dBias, dY, dWorkspace, workspace_bytes, stream, path, nullptr, 0.0f);
 }
 
 // Workspace of mnb_run_rmsnorm: the normalized input (paths without the
-// fused RMSNorm), the rows' 1 / rms (GEMM), then mnb_run's workspace.
+// fused RMSNorm), then mnb_run's workspace.
 static size_t RmsFrontBytes(const mnb_plan *plan, int64_t M) {
-  return Round256(static_cast<size_t>(M) * plan->view.K * 4) + Round256(static_cast<size_t>(M) * 4);
+  return Round256(static_cast<size_t>(M) * plan->view.K * 4);
 }
 
 int mnb_rmsnorm_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
@@ -548,32 +622,20 @@ int mnb_run_rmsnorm(const mnb_plan *plan, int64_t M, const float *dX, const floa
       (reinterpret_cast<uintptr_t>(dWorkspace) % 16) != 0)
     return MNB_ERR_WORKSPACE;
   float *Xn = static_cast<float *>(dWorkspace);
-  float *inv = reinterpret_cast<float *>(static_cast<char *>(dWorkspace) +
-                                         Round256(static_cast<size_t>(M) * plan->view.K * 4));
   void *rest = static_cast<char *>(dWorkspace) + front;
   const size_t rest_bytes = workspace_bytes - front;
   int cur = -1;
   if (hipGetDevice(&cur) != hipSuccess || cur != plan->device) return MNB_ERR_NO_DEVICE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int path = SelectPath(plan, M, dX);
-  hipError_t e = hipSuccess;
-  if (path == 1 && M == 1 && mnb::GemvM1Supports(plan->view))
-    return RunImpl(plan, M, dX, nullptr, dY, rest, rest_bytes, stream, path, dGamma, epsilon,
-                   nullptr);
-  if (path == 2) {
-    e = mnb::LaunchRowInvRms(dX, inv, M, plan->view.K, epsilon, s);
-    if (e != hipSuccess) {
-      SetLastError("kernel launch", e);
-      return MNB_ERR_HIP;
-    }
-    return RunImpl(plan, M, dX, nullptr, dY, rest, rest_bytes, stream, path, dGamma, epsilon, inv);
-  }
-  e = mnb::LaunchRmsNorm(dX, dGamma, Xn, M, plan->view.K, epsilon, s);
+  if ((path == 1 && M == 1 && mnb::GemvM1Supports(plan->view)) || path == 2)
+    return RunImpl(plan, M, dX, nullptr, dY, rest, rest_bytes, stream, path, dGamma, epsilon);
+  const hipError_t e = mnb::LaunchRmsNorm(dX, dGamma, Xn, M, plan->view.K, epsilon, s);
   if (e != hipSuccess) {
     SetLastError("kernel launch", e);
     return MNB_ERR_HIP;
   }
-  return RunImpl(plan, M, Xn, nullptr, dY, rest, rest_bytes, stream, path, nullptr, 0.0f, nullptr);
+  return RunImpl(plan, M, Xn, nullptr, dY, rest, rest_bytes, stream, path, nullptr, 0.0f);
 }
 
 int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,

@@ -123,40 +123,114 @@ __device__ __forceinline__ uint4 DequantWord(uint32_t w, const DequantRow &r,
                     PkMulF16(PkAddF16(h2, r.neg_lo), r.s), PkMulF16(PkAddF16(h3, r.neg_hi), r.s));
 }
 
-// One thread per 16-byte LDS unit of the converted A: 8 consecutive fp32 of a
-// row -> 8 fp16 in [0,4,1,5,2,6,3,7] order, written where GemmKernel's direct
-// copy expects it. Rows >= M are written as zeros.
-template <int BM>
+// Largest value over the 256 threads of a workgroup (4 wavefronts); every
+// thread gets it. `red` holds 4 floats of LDS.
+__device__ __forceinline__ float BlockMax256(float v, float *red) {
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  __syncthreads();  // red may still be read by an earlier reduction
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__device__ __forceinline__ float BlockSum256(float v, float *red) {
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// One workgroup per row of A (rows past M, up to the tile padding, are written
+// as zeros). The row is scaled by 2^f, f = RangeExponent(max_k |A[m][k]|, 14),
+// and rounded to fp16 (round to nearest even, as FloatToFloat16Bits,
+// onnx_light_cpu/impl/math/half_conversion.h:42-78): no finite input becomes
+// inf, and only values below 2^-24 of the row's largest magnitude flush to
+// zero. f goes to row_exp[m]; the GEMM's epilogue multiplies by 2^-f. Each
+// 16-byte unit holds 8 consecutive k in [0,4,1,5,2,6,3,7] order and lands
+// where GemmKernel's direct copy expects it.
+// With gamma (RMSNorm folded in), the row is x * gamma * inv_rms with
+// inv_rms = 1 / sqrt(mean_k x^2 + eps) reduced here as well.
+// NV > 0: each thread keeps its NV units of the row in registers between the
+// reduction and the conversion (K <= 2048 NV); NV = 0 reads the row twice.
+template <int BM, int NV, bool RMS>
 __global__ __launch_bounds__(256) void ConvertAKernel(const float *__restrict__ A,
-                                                      uint4 *__restrict__ Ah, int M, int K,
-                                                      int64_t total_units,
+                                                      uint4 *__restrict__ Ah,
+                                                      int *__restrict__ row_exp, int M, int K,
                                                       const float *__restrict__ gamma,
-                                                      const float *__restrict__ inv_rms) {
-  const int64_t g = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (g >= total_units) return;
-  const int units_per_row = K / 8;
-  const int64_t row = g / units_per_row;
-  const int ku = static_cast<int>(g - row * units_per_row);  // unit index along K
-  uint4 out = make_uint4(0u, 0u, 0u, 0u);
-  if (row < M) {
-    const float4 *src = reinterpret_cast<const float4 *>(A + row * K + 8 * ku);
-    float4 x = src[0], y = src[1];
-    if (gamma != nullptr) {
-      // RMSNorm folded into the rounding: x * inv_rms[row] * gamma[k]
-      const float r = inv_rms[row];
-      const float4 g0 = reinterpret_cast<const float4 *>(gamma + 8 * ku)[0];
-      const float4 g1 = reinterpret_cast<const float4 *>(gamma + 8 * ku)[1];
-      x = make_float4(x.x * r * g0.x, x.y * r * g0.y, x.z * r * g0.z, x.w * r * g0.w);
-      y = make_float4(y.x * r * g1.x, y.y * r * g1.y, y.z * r * g1.z, y.w * r * g1.w);
-    }
-    out = make_uint4(PackHalf2(x.x, y.x), PackHalf2(x.y, y.y), PackHalf2(x.z, y.z),
-                     PackHalf2(x.w, y.w));
-  }
+                                                      float eps) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int units = K / 8;
   const int ktiles = K / kBK;
-  const int64_t mt = row / BM;
-  const int r = static_cast<int>(row - mt * BM);
-  const int kt = ku / kUnits, u = ku % kUnits;
-  Ah[(mt * ktiles + kt) * AUnits<BM>() + Swz(r, u)] = out;
+  const int mt = row / BM;
+  const int r = row - mt * BM;
+  uint4 *base = Ah + static_cast<size_t>(mt) * ktiles * AUnits<BM>();
+  auto dst = [&](int u) -> uint4 & { return base[(u / kUnits) * AUnits<BM>() + Swz(r, u % kUnits)]; };
+  if (row >= M) {
+    for (int u = tid; u < units; u += 256) dst(u) = make_uint4(0u, 0u, 0u, 0u);
+    if (tid == 0) row_exp[row] = 0;
+    return;
+  }
+  const float *src = A + static_cast<size_t>(row) * K;
+  auto load = [&](int u, float4 &x, float4 &y, float &amax, float &ss) {
+    x = reinterpret_cast<const float4 *>(src + 8 * u)[0];
+    y = reinterpret_cast<const float4 *>(src + 8 * u)[1];
+    if constexpr (RMS) {
+      ss += ((x.x * x.x + x.y * x.y) + (x.z * x.z + x.w * x.w)) +
+            ((y.x * y.x + y.y * y.y) + (y.z * y.z + y.w * y.w));
+      const float4 g0 = reinterpret_cast<const float4 *>(gamma + 8 * u)[0];
+      const float4 g1 = reinterpret_cast<const float4 *>(gamma + 8 * u)[1];
+      x = make_float4(x.x * g0.x, x.y * g0.y, x.z * g0.z, x.w * g0.w);
+      y = make_float4(y.x * g1.x, y.y * g1.y, y.z * g1.z, y.w * g1.w);
+    }
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+  };
+  // x * mul, then * 2^f (exact): the value FloatToFloat16Bits rounds
+  auto store = [&](int u, float4 x, float4 y, float mul, int f) {
+    if constexpr (RMS) {
+      x = make_float4(x.x * mul, x.y * mul, x.z * mul, x.w * mul);
+      y = make_float4(y.x * mul, y.y * mul, y.z * mul, y.w * mul);
+    }
+    auto sc = [f](float v) { return __builtin_amdgcn_ldexpf(v, f); };
+    dst(u) = make_uint4(PackHalf2(sc(x.x), sc(y.x)), PackHalf2(sc(x.y), sc(y.y)),
+                        PackHalf2(sc(x.z), sc(y.z)), PackHalf2(sc(x.w), sc(y.w)));
+  };
+  float amax = 0.0f, ss = 0.0f;
+  float4 kx[NV > 0 ? NV : 1], ky[NV > 0 ? NV : 1];
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int u = tid + 256 * i;
+      if (u < units) load(u, kx[i], ky[i], amax, ss);
+    }
+  } else {
+    for (int u = tid; u < units; u += 256) load(u, kx[0], ky[0], amax, ss);
+  }
+  amax = BlockMax256(amax, red);
+  float mul = 1.0f;
+  if constexpr (RMS) {
+    mul = 1.0f / sqrtf(BlockSum256(ss, red) / static_cast<float>(K) + eps);
+    amax *= mul;
+  }
+  const int f = RangeExponent(amax, kRowExpTarget);
+  if (tid == 0) row_exp[row] = f;
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int u = tid + 256 * i;
+      if (u < units) store(u, kx[i], ky[i], mul, f);
+    }
+  } else {
+    for (int u = tid; u < units; u += 256) {
+      float dummy_a = 0.0f, dummy_s = 0.0f;
+      float4 x, y;
+      load(u, x, y, dummy_a, dummy_s);
+      store(u, x, y, mul, f);
+    }
+  }
 }
 
 // s_waitcnt vmcnt(N) with the other counters left free (gfx9 encoding: vmcnt
@@ -187,7 +261,9 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
                                                      int nb, int log2_bs, int row_bytes,
                                                      int zp_row_bytes, int kt_per_split,
                                                      float *__restrict__ partials,
-                                                     float *__restrict__ H) {
+                                                     float *__restrict__ H,
+                                                     const int *__restrict__ row_exp,
+                                                     const int *__restrict__ col_exp) {
   extern __shared__ uint4 lds[];
   constexpr int kAUnits = AUnits<BM>();
   uint4 *Astage = lds;                        // [kAStages][kAUnits]
@@ -280,9 +356,13 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
     }
   };
   const DequantConsts dq = MakeDequantConsts();
+  // The weight row's power-of-two exponent (plan time): its block scales times
+  // 2^e_b are normal fp16 numbers and (q - zp) * scale stays below 65504.
+  const int e_b = col_exp[min(n0 + b_row, N - 1)];
   auto store_b = [&](const BRegs &r, int buf) {
     const uint32_t words[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-    const DequantRow dr = MakeDequantRow(r.s, (r.z >> r.zshift) & 0xFu);
+    const DequantRow dr =
+        MakeDequantRow(__builtin_amdgcn_ldexpf(r.s, e_b), (r.z >> r.zshift) & 0xFu);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       Bbuf[buf * kBUnits + Swz(b_row, 4 * b_half + u)] = DequantWord(words[u], dr, dq);
@@ -382,7 +462,27 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
 
   // Output: split 0 writes Y, split s > 0 of a split-K launch its partial sum
   // at partials + (s - 1) * M * N. Lane holds column (lane & 15), rows
-  // 4*(lane >> 4) + v of each 16 x 16 tile.
+  // 4*(lane >> 4) + v of each 16 x 16 tile. The accumulators are in units of
+  // 2^(f_m + e_n) (A row m scaled by 2^f_m, weight row n by 2^e_n): one ldexp
+  // per element undoes both exactly (a single rounding, only if the result is
+  // an fp32 subnormal).
+  {
+    int ec[4], er[kMI][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ec[j] = col_exp[min(n0 + wn * 64 + j * 16 + (lane & 15), N - 1)];
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        er[i][v] = row_exp[m0 + wm * (BM / 2) + i * 16 + 4 * (lane >> 4) + v];
+#pragma unroll
+    for (int i = 0; i < kMI; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          acc[i][j][v] = __builtin_amdgcn_ldexpf(acc[i][j][v], -(er[i][v] + ec[j]));
+  }
   if (H != nullptr) {
     // Gate/up epilogue of a one-split launch. Column gn + 1 (the up of gate
     // gn, N even) is held by lane ^ 1 for the same four rows v = 0..3; the
@@ -535,9 +635,17 @@ inline Shape MakeShape(const WeightView &w, int bm, int splits) {
   return Shape{bm, (ktiles + per - 1) / per, per};
 }
 
+inline int64_t PaddedRows(int64_t M) { return (M + kMaxBM - 1) / kMaxBM * kMaxBM; }
+
+// The workspace starts with the fp16 image of A (every tile height's padding
+// is covered by kMaxBM), then the rows' power-of-two exponents (int32 per
+// padded row, rounded up to 256 bytes), then the split-K partial sums.
 inline size_t AImageBytes(const WeightView &w, int64_t M) {
-  const int64_t mpad = (M + kMaxBM - 1) / kMaxBM * kMaxBM;  // covers every tile height
-  return static_cast<size_t>(mpad) * static_cast<size_t>(w.K) * 2;
+  return static_cast<size_t>(PaddedRows(M)) * static_cast<size_t>(w.K) * 2;
+}
+
+inline size_t RowExpBytes(int64_t M) {
+  return (static_cast<size_t>(PaddedRows(M)) * 4 + 255) / 256 * 256;
 }
 
 inline size_t PartialBytes(const WeightView &w, int64_t M, const Shape &sh) {
@@ -546,33 +654,50 @@ inline size_t PartialBytes(const WeightView &w, int64_t M, const Shape &sh) {
 
 template <int BM, bool HAS_ZP>
 hipError_t LaunchT(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, float *partials,
-                   const Shape &sh, hipStream_t s, float *H) {
+                   const Shape &sh, hipStream_t s, float *H, const int *row_exp) {
   const int tiles = static_cast<int>(((M + BM - 1) / BM) * ((w.N + kBN - 1) / kBN));
   hipLaunchKernelGGL((GemmKernel<BM, HAS_ZP>), dim3(tiles * sh.splits), dim3(256), LdsBytes<BM>(),
                      s, Ah, w.B, w.scales, w.zp, Y, static_cast<int>(M), static_cast<int>(w.K),
                      static_cast<int>(w.N), static_cast<int>(w.nb), w.log2_bs,
                      static_cast<int>(w.row_bytes), static_cast<int>(w.zp_row_bytes),
-                     sh.kt_per_split, partials, H);
+                     sh.kt_per_split, partials, H, row_exp, w.col_exp);
+  return hipGetLastError();
+}
+
+// ConvertAKernel over the padded rows of a BM tiling, keeping each thread's
+// share of the row in registers when K allows.
+template <int BM, bool RMS>
+hipError_t LaunchConvertA(const WeightView &w, int64_t M, const float *A, uint4 *Ah, int *row_exp,
+                          hipStream_t s, const float *gamma, float eps) {
+  const dim3 grid(static_cast<unsigned>((M + BM - 1) / BM * BM)), block(256);
+  const int K = static_cast<int>(w.K), m = static_cast<int>(M);
+  if (K <= 2048 * 2)
+    hipLaunchKernelGGL((ConvertAKernel<BM, 2, RMS>), grid, block, 0, s, A, Ah, row_exp, m, K, gamma, eps);
+  else if (K <= 2048 * 4)
+    hipLaunchKernelGGL((ConvertAKernel<BM, 4, RMS>), grid, block, 0, s, A, Ah, row_exp, m, K, gamma, eps);
+  else if (K <= 2048 * 8)
+    hipLaunchKernelGGL((ConvertAKernel<BM, 8, RMS>), grid, block, 0, s, A, Ah, row_exp, m, K, gamma, eps);
+  else
+    hipLaunchKernelGGL((ConvertAKernel<BM, 0, RMS>), grid, block, 0, s, A, Ah, row_exp, m, K, gamma, eps);
   return hipGetLastError();
 }
 
 template <int BM>
 hipError_t LaunchBM(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                    const Shape &sh, hipStream_t s, float *H, const float *gamma,
-                    const float *inv_rms) {
+                    const Shape &sh, hipStream_t s, float *H, const float *gamma, float eps) {
   uint4 *Ah = static_cast<uint4 *>(work);
-  float *partials = reinterpret_cast<float *>(static_cast<char *>(work) + AImageBytes(w, M));
-  const int64_t units = (M + BM - 1) / BM * BM * (w.K / 8);
-  hipLaunchKernelGGL(ConvertAKernel<BM>, dim3(static_cast<unsigned>((units + 255) / 256)),
-                     dim3(256), 0, s, A, Ah, static_cast<int>(M), static_cast<int>(w.K), units,
-                     gamma, inv_rms);
-  hipError_t e = hipGetLastError();
+  int *row_exp = reinterpret_cast<int *>(static_cast<char *>(work) + AImageBytes(w, M));
+  float *partials = reinterpret_cast<float *>(static_cast<char *>(work) + AImageBytes(w, M) +
+                                              RowExpBytes(M));
+  hipError_t e = gamma != nullptr
+                     ? LaunchConvertA<BM, true>(w, M, A, Ah, row_exp, s, gamma, eps)
+                     : LaunchConvertA<BM, false>(w, M, A, Ah, row_exp, s, nullptr, 0.0f);
   if (e != hipSuccess) return e;
   // Gate/up activation: fused into the GEMM's stores with one split, into the
   // reduction (split 0 then writes the scratch Y) with several.
   float *Hk = sh.splits == 1 ? H : nullptr;
-  e = w.zp != nullptr ? LaunchT<BM, true>(w, M, Ah, Y, partials, sh, s, Hk)
-                      : LaunchT<BM, false>(w, M, Ah, Y, partials, sh, s, Hk);
+  e = w.zp != nullptr ? LaunchT<BM, true>(w, M, Ah, Y, partials, sh, s, Hk, row_exp)
+                      : LaunchT<BM, false>(w, M, Ah, Y, partials, sh, s, Hk, row_exp);
   if (e != hipSuccess || sh.splits == 1) return e;
   return DispatchReduce(sh.splits - 1, Y, partials, M * w.N, s, H,
                         std::make_integer_sequence<int, kMaxSplits - 1>{});
@@ -600,11 +725,11 @@ inline Shape PickShape(const WeightView &w, int64_t M) {
 } // namespace
 
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M) {
-  return AImageBytes(w, M) + PartialBytes(w, M, PickShape(w, M));
+  return AImageBytes(w, M) + RowExpBytes(M) + PartialBytes(w, M, PickShape(w, M));
 }
 
 size_t GemmShapeWorkspaceBytes(const WeightView &w, int64_t M, int splits) {
-  return AImageBytes(w, M) + PartialBytes(w, M, MakeShape(w, 32, splits));
+  return AImageBytes(w, M) + RowExpBytes(M) + PartialBytes(w, M, MakeShape(w, 32, splits));
 }
 
 bool GemmSupports(const WeightView &w, int64_t M) {
@@ -620,20 +745,20 @@ bool GemmSupports(const WeightView &w, int64_t M) {
 
 hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                            hipStream_t s, int bm, int splits, float *H, const float *gamma,
-                           const float *inv_rms) {
+                           float eps) {
   Shape sh = PickShape(w, M);
   if (bm > 0) sh = MakeShape(w, bm, splits > 0 ? splits : 1);
   switch (sh.bm) {
-  case 32: return LaunchBM<32>(w, M, A, Y, work, sh, s, H, gamma, inv_rms);
-  case 64: return LaunchBM<64>(w, M, A, Y, work, sh, s, H, gamma, inv_rms);
-  case 128: return LaunchBM<128>(w, M, A, Y, work, sh, s, H, gamma, inv_rms);
+  case 32: return LaunchBM<32>(w, M, A, Y, work, sh, s, H, gamma, eps);
+  case 64: return LaunchBM<64>(w, M, A, Y, work, sh, s, H, gamma, eps);
+  case 128: return LaunchBM<128>(w, M, A, Y, work, sh, s, H, gamma, eps);
   default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                      hipStream_t s, float *H, const float *gamma, const float *inv_rms) {
-  return LaunchGemmShape(w, M, A, Y, work, s, 0, 0, H, gamma, inv_rms);
+                      hipStream_t s, float *H, const float *gamma, float eps) {
+  return LaunchGemmShape(w, M, A, Y, work, s, 0, 0, H, gamma, eps);
 }
 
 } // namespace mnb

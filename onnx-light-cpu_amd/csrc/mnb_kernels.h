@@ -54,11 +54,32 @@ __device__ __forceinline__ float PairSwap(float v) {
       float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
 }
 
+// Power-of-two exponent f that brings a largest magnitude amax into
+// [2^target, 2^(target+1)), so that values up to amax times 2^f stay in fp16's
+// range; the scaling itself is exact in fp32. 0 for a zero, infinite or NaN
+// maximum (those then propagate as they would in fp32).
+__device__ __forceinline__ int RangeExponent(float amax, int target) {
+  if (!(amax > 0.0f) || !(amax <= 3.402823466e38f)) return 0;
+  int e;
+  (void)frexpf(amax, &e);  // amax = m * 2^e, m in [0.5, 1): floor(log2 amax) = e - 1
+  return target - (e - 1);
+}
+
+// Exponent target of the plan's per-weight-row scale exponents: the largest
+// block scale of row n times 2^col_exp[n] lies in [2^11, 2^12), so every
+// block scale down to 2^-25 of it is a normal fp16 number and
+// (q - zp) * scale, |q - zp| <= 15, stays below 65504.
+constexpr int kScaleExpTarget = 11;
+// Exponent target of the prefill path's per-row activation exponents: the
+// row's largest magnitude times 2^f lies in [2^14, 2^15).
+constexpr int kRowExpTarget = 14;
+
 // Everything a kernel needs to address one plan's constants.
 struct WeightView {
   const uint8_t *B;       // [N, nb, bs/2] packed nibbles, low nibble first
   const float *scales;    // [N, nb]
   const uint8_t *zp;      // [N, zp_row_bytes] packed nibbles, or nullptr (zp = 8)
+  const int32_t *col_exp; // [N] RangeExponent(max_b |scales[n][b]|, kScaleExpTarget)
   int64_t K;
   int64_t N;
   int64_t nb;             // ceil(K / bs)
@@ -95,8 +116,7 @@ hipError_t LaunchGemvSmallMShape(const WeightView &w, int64_t M, const float *A,
 //
 // RMSNorm input (M = 1 GEMV, GEMM): with gamma (K floats, 16-byte aligned)
 // the launch multiplies RMSNorm(A) = A / sqrt(mean_k(A^2) + eps) * gamma
-// instead of A. The GEMV computes the row's mean square itself; the GEMM takes
-// inv_rms[m] = 1 / sqrt(mean_k(A[m]^2) + eps) from LaunchRowInvRms.
+// instead of A; both compute the rows' mean squares themselves.
 hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
                         int band_rows, int rows_per_wave, float *H = nullptr,
                         const float *gamma = nullptr, float eps = 0.0f);
@@ -117,11 +137,12 @@ hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, f
                                float *H = nullptr);
 
 // Prefill GEMM on fp16 MFMA, any M, K % 64 == 0, block_size >= 32. `work`
-// holds GemmWorkspaceBytes(w, M) bytes of device memory: A rounded to fp16,
-// then the partial sums of a split-K launch.
+// holds GemmWorkspaceBytes(w, M) bytes of device memory: A scaled per row by
+// a power of two and rounded to fp16, the rows' exponents, then the partial
+// sums of a split-K launch.
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                       hipStream_t s, float *H = nullptr, const float *gamma = nullptr,
-                      const float *inv_rms = nullptr);
+                      float eps = 0.0f);
 bool GemmSupports(const WeightView &w, int64_t M);
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M);
 // Same with an explicit tile height (32, 64 or 128; 0 picks both) and split
@@ -129,7 +150,7 @@ size_t GemmWorkspaceBytes(const WeightView &w, int64_t M);
 // GemmShapeWorkspaceBytes(w, M, splits) bytes.
 hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                            hipStream_t s, int bm, int splits, float *H = nullptr,
-                           const float *gamma = nullptr, const float *inv_rms = nullptr);
+                           const float *gamma = nullptr, float eps = 0.0f);
 size_t GemmShapeWorkspaceBytes(const WeightView &w, int64_t M, int splits);
 
 // H[m][n] = SiluMul(Y[m][2n], Y[m][2n + 1]) for an M x N (N even) Y: the
@@ -137,12 +158,15 @@ size_t GemmShapeWorkspaceBytes(const WeightView &w, int64_t M, int splits);
 hipError_t LaunchSiluMul(const float *Y, float *H, int64_t M, int64_t N, hipStream_t s);
 
 // RMSNorm over the rows of X [M, K] (K % 4 == 0, X 16-byte aligned):
-// inv_rms[m] = 1 / sqrt(mean_k(X[m]^2) + eps); LaunchRmsNorm also writes
-// Xn[m][k] = X[m][k] * inv_rms[m] * gamma[k].
-hipError_t LaunchRowInvRms(const float *X, float *inv_rms, int64_t M, int64_t K, float eps,
-                           hipStream_t s);
+// Xn[m][k] = X[m][k] * inv_rms[m] * gamma[k], inv_rms[m] =
+// 1 / sqrt(mean_k(X[m]^2) + eps).
 hipError_t LaunchRmsNorm(const float *X, const float *gamma, float *Xn, int64_t M, int64_t K,
                          float eps, hipStream_t s);
+
+// col_exp[n] = RangeExponent(max_b |scales[n][b]|, kScaleExpTarget) for the
+// plan's N weight rows (run once, at plan creation).
+hipError_t LaunchColExp(const float *scales, int32_t *col_exp, int64_t N, int64_t nb,
+                        hipStream_t s);
 
 // Generic fallback: any K, any block_size, any M. Slow; for odd shapes and
 // cross-checks.

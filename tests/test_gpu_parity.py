@@ -237,17 +237,20 @@ def test_prepare_device_borrows(pkg, orc, cuda):
 
 
 def test_gemm_workspace_contract(pkg, cuda):
-    """mnb_workspace_bytes is ceil(M/128)*128*K*2 (A in fp16) plus (S-1)*M*N*4
-    for a GEMM that splits K into S <= 16 parts; path 2 refuses a missing,
-    short or misaligned workspace with MNB_ERR_WORKSPACE before any launch, and
-    a reused larger workspace with stale contents gives the same bits."""
+    """mnb_workspace_bytes is ceil(M/128)*128*K*2 (A in fp16), the rows'
+    int32 exponents (ceil(M/128)*128 of them, rounded up to 256 bytes), plus
+    (S-1)*M*N*4 for a GEMM that splits K into S <= 16 parts; path 2 refuses a
+    missing, short or misaligned workspace with MNB_ERR_WORKSPACE before any
+    launch, and a reused larger workspace with stale contents gives the same
+    bits."""
     import ctypes
     import torch
     K, N, bs = 512, 256, 64
     p, B, S, Z = _case(pkg, K, N, bs, True, seed=31)
     op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
     for M in (1, 16, 17, 128, 129, 300):
-        a_image = -(-M // 128) * 128 * K * 2
+        mpad = -(-M // 128) * 128
+        a_image = mpad * K * 2 + -(-mpad * 4 // 256) * 256
         extra = op.workspace_bytes(M) - a_image
         assert extra >= 0 and extra % (M * N * 4) == 0 and extra // (M * N * 4) < 16, (M, extra)
     assert op.workspace_bytes(0) == 0
