@@ -169,6 +169,24 @@ int mnb_run_rmsnorm(const mnb_plan *plan, int64_t M, const float *dX, const floa
                     float epsilon, float *dY, void *dWorkspace, size_t workspace_bytes,
                     void *stream);
 
+/* Bytes of the device scratch array behind mnb_run_no_alloc (32 MiB). */
+#define MNB_NO_ALLOC_SCRATCH_BYTES (32u << 20)
+
+/* mnb_run without a caller workspace and without any allocation: the
+ * kernels' workspace is a fixed device array of MNB_NO_ALLOC_SCRATCH_BYTES
+ * inside the library, one copy per GPU, held until the process ends (its
+ * address is looked up on the first call on each device). No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Fails with MNB_ERR_WORKSPACE, before any launch, when
+ * mnb_workspace_bytes(plan, M) exceeds the array (e.g. the prefill GEMM above
+ * M * K * 2 of about 32 MiB, or a gate/up plan's M x 2N scratch sum). Every
+ * call on a GPU shares that GPU's array: calls that overlap in time on one
+ * GPU (several streams or threads) race and must be ordered by the caller.
+ * No kernel reads scratch bytes it did not write in the same call, so the
+ * previous call's leftovers never reach a result. */
+int mnb_run_no_alloc(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *stream);
+
 /* Which path mnb_run takes for M rows (1 to 4 as in mnb_run_path). */
 int mnb_select_path(const mnb_plan *plan, int64_t M, int *path);
 

@@ -66,6 +66,7 @@ def library():
         L.mnb_run.argtypes = [vp, i64, vp, vp, vp, sz, vp]
         L.mnb_run_path.argtypes = [vp, i64, vp, vp, vp, sz, vp, ctypes.c_int]
         L.mnb_run_ex.argtypes = [vp, i64, vp, vp, vp, vp, sz, vp, ctypes.c_int]
+        L.mnb_run_no_alloc.argtypes = [vp, i64, vp, vp, vp]
         i32 = ctypes.c_int32
         L.mnb_qdq_repack.argtypes = [i64, i64, i32, i32, vp, vp, vp, vp, vp, vp,
                                      ctypes.POINTER(i32)]
@@ -79,7 +80,7 @@ def library():
                      "mnb_workspace_bytes", "mnb_run", "mnb_run_path", "mnb_select_path",
                      "mnb_weight_bytes", "mnb_run_ex", "mnb_qdq_repack",
                      "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes",
-                     "mnb_run_rmsnorm"):
+                     "mnb_run_rmsnorm", "mnb_run_no_alloc"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib

@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -232,6 +233,42 @@ hipError_t LaunchRmsNorm(const float *X, const float *gamma, float *Xn, int64_t 
 } // namespace mnb
 
 static size_t Round256(size_t v) { return (v + 255) / 256 * 256; }
+
+// Workspace of mnb_run_no_alloc: a file-scope device array, one copy per GPU
+// the library runs on, held until the process ends. In host code `scratch`
+// names a host-side stand-in, never the device memory: host code uses only
+// the per-device address from hipGetSymbolAddress.
+constexpr size_t kScratchBytes = size_t{MNB_NO_ALLOC_SCRATCH_BYTES};
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device (with
+// that device current) and kept. Returns MNB_OK or MNB_ERR_HIP.
+int ScratchAddress(int device, void **out) {
+  if (device < 0 || device >= kMaxScratchDevices) {
+    std::snprintf(g_last_error, sizeof(g_last_error), "device %d: no scratch slot", device);
+    return MNB_ERR_NO_DEVICE;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      SetLastError("hipGetSymbolAddress(scratch)", e);
+      return MNB_ERR_HIP;
+    }
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return MNB_OK;
+}
+
+} // namespace
 
 // Bytes of the gate/up plans' scratch sum y = A * W^T (M x N floats, N = 2 I)
 // at the front of the workspace, rounded up to keep what follows aligned.
@@ -646,6 +683,32 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
 int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
             size_t workspace_bytes, void *stream) {
   return mnb_run_ex(plan, M, dA, nullptr, dY, dWorkspace, workspace_bytes, stream, 0);
+}
+
+int mnb_run_no_alloc(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *stream) {
+  if (plan == nullptr) return MNB_ERR_NULL_POINTER;
+  if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
+  if (M == 0) return MNB_OK;
+  if (dA == nullptr || dY == nullptr) return MNB_ERR_NULL_POINTER;
+  size_t need = 0;
+  int st = mnb_workspace_bytes(plan, M, &need);
+  if (st != MNB_OK) return st;
+  if (need > kScratchBytes) {
+    std::snprintf(g_last_error, sizeof(g_last_error),
+                  "mnb_run_no_alloc: %zu workspace bytes needed for M = %lld, the scratch holds %zu",
+                  need, static_cast<long long>(M), kScratchBytes);
+    return MNB_ERR_WORKSPACE;
+  }
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur != plan->device) {
+    std::snprintf(g_last_error, sizeof(g_last_error), "plan lives on device %d, current is %d",
+                  plan->device, cur);
+    return MNB_ERR_NO_DEVICE;
+  }
+  void *work = nullptr;
+  st = ScratchAddress(cur, &work);
+  if (st != MNB_OK) return st;
+  return mnb_run_ex(plan, M, dA, nullptr, dY, need > 0 ? work : nullptr, need, stream, 0);
 }
 
 } // extern "C"

@@ -20,7 +20,8 @@ def test_library_exports_every_header_function(pkg):
         "mnb_plan_create", "mnb_plan_create_device", "mnb_plan_destroy", "mnb_workspace_bytes",
         "mnb_run", "mnb_run_path", "mnb_run_ex", "mnb_select_path", "mnb_status_str",
         "mnb_last_error", "mnb_weight_bytes", "mnb_version", "mnb_qdq_repack",
-        "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes", "mnb_run_rmsnorm"])
+        "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes", "mnb_run_rmsnorm",
+        "mnb_run_no_alloc"])
     for name in names:
         assert hasattr(L, name), name
 
@@ -97,6 +98,7 @@ def test_run_and_queries_reject_null_plan(pkg):
     assert L.mnb_run_ex(None, 1, None, None, None, None, 0, None, 1) == NULLP
     assert L.mnb_workspace_bytes(None, 1, ctypes.byref(x)) == NULLP
     assert L.mnb_select_path(None, 1, ctypes.byref(p)) == NULLP
+    assert L.mnb_run_no_alloc(None, 1, None, None, None) == NULLP
     assert L.mnb_plan_destroy(None) == MNB_OK
     assert L.mnb_run_rmsnorm(None, 1, None, None, 1e-5, None, None, 0, None) == NULLP
     assert L.mnb_rmsnorm_workspace_bytes(None, 1, ctypes.byref(x)) == NULLP
