@@ -137,9 +137,12 @@ int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *d
 
 /* Same as mnb_run with the kernel chosen by the caller (whatever the plan's
  * accuracy_level): path 0 = automatic, 1 = decode GEMV (any M <= 16),
- * 2 = MFMA GEMM (any M), 3 = generic fallback (any shape; slow, for
- * cross-checks), 4 = the decode kernels over consecutive groups of 16 rows
- * (any M; the exact route of accuracy_level 1). */
+ * 2 = MFMA GEMM (any M; the kernel picked by shape), 3 = generic fallback
+ * (any shape; slow, for cross-checks), 4 = the decode kernels over
+ * consecutive groups of 16 rows (any M; the exact route of accuracy_level 1),
+ * 5 = the MFMA GEMM's prefill kernel over the plan's fragment-ordered weight
+ * copy (any M; MNB_ERR_UNSUPPORTED when the plan holds none: K % 64 != 0,
+ * N % 4 != 0, block_size < 32 or N >= 2^22). */
 int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
                  size_t workspace_bytes, void *stream, int path);
 
@@ -187,7 +190,8 @@ int mnb_run_rmsnorm(const mnb_plan *plan, int64_t M, const float *dX, const floa
  * previous call's leftovers never reach a result. */
 int mnb_run_no_alloc(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *stream);
 
-/* Which path mnb_run takes for M rows (1 to 4 as in mnb_run_path). */
+/* Which path mnb_run takes for M rows (1 to 4 as in mnb_run_path; the
+ * automatic GEMM path reports 2 whichever GEMM kernel serves). */
 int mnb_select_path(const mnb_plan *plan, int64_t M, int *path);
 
 /* Text for a status code (static storage). */

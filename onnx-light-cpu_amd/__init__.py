@@ -34,7 +34,7 @@ STATUS = {
     4: "MNB_ERR_UNSUPPORTED", 5: "MNB_ERR_WORKSPACE", 6: "MNB_ERR_HIP", 7: "MNB_ERR_NO_DEVICE",
     8: "MNB_ERR_ALLOC",
 }
-PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GENERIC, PATH_EXACT = 0, 1, 2, 3, 4
+PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GENERIC, PATH_EXACT, PATH_PREFILL = 0, 1, 2, 3, 4, 5
 
 
 class MnbDesc(ctypes.Structure):

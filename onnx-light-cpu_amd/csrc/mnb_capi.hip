@@ -27,6 +27,8 @@ struct mnb_plan {
   float *dS;
   uint8_t *dZ;
   int32_t *dColExp;  // always plan-owned: per weight row power-of-two scale exponent
+  uint8_t *dBp;      // plan-owned prefill layout of the weights (nullptr: shape not served)
+  uint8_t *dSp;
 };
 
 namespace {
@@ -99,6 +101,8 @@ void FillView(mnb_plan *p) {
   p->view.scales = p->dS;
   p->view.zp = p->desc.has_zero_points ? p->dZ : nullptr;
   p->view.col_exp = p->dColExp;
+  p->view.Bp = p->dBp;
+  p->view.Sp = p->dSp;
   p->view.K = p->desc.K;
   p->view.N = p->desc.N;
   p->view.nb = nb;
@@ -116,28 +120,52 @@ void FreePlanMemory(mnb_plan *p) {
     if (p->dZ) (void)hipFree(p->dZ);
   }
   if (p->dColExp) (void)hipFree(p->dColExp);
+  if (p->dBp) (void)hipFree(p->dBp);
+  if (p->dSp) (void)hipFree(p->dSp);
   p->dB = nullptr;
   p->dS = nullptr;
   p->dZ = nullptr;
   p->dColExp = nullptr;
+  p->dBp = nullptr;
+  p->dSp = nullptr;
 }
 
 // Plan-time constants derived from the device copies of the weights (run
-// once, synchronously, on the null stream): the per-row scale exponents.
+// once, synchronously, on the null stream): the per-row scale exponents and,
+// for shapes the prefill kernel serves, its fragment-ordered copy of the
+// weights with per-step scale / zero-point words (1.25x the packed B bytes).
+// Fills the plan's view.
 int DerivePlanConstants(mnb_plan *p) {
+  FillView(p);
   hipError_t e = hipMalloc(reinterpret_cast<void **>(&p->dColExp),
                            static_cast<size_t>(p->desc.N) * sizeof(int32_t));
   if (e != hipSuccess) {
     SetLastError("hipMalloc", e);
     return MNB_ERR_ALLOC;
   }
-  int64_t nb, row_bytes, zp_row_bytes;
-  Sizes(&p->desc, &nb, &row_bytes, &zp_row_bytes);
-  e = mnb::LaunchColExp(p->dS, p->dColExp, p->desc.N, nb, nullptr);
+  e = mnb::LaunchColExp(p->dS, p->dColExp, p->desc.N, p->view.nb, nullptr);
   if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
   if (e != hipSuccess) {
     SetLastError("plan constants", e);
     return MNB_ERR_HIP;
+  }
+  FillView(p);
+  if (mnb::PrefillLayoutWanted(p->view)) {
+    size_t sp_bytes = 0;
+    const size_t bp_bytes = mnb::PrefillLayoutBytes(p->view, &sp_bytes);
+    e = hipMalloc(reinterpret_cast<void **>(&p->dBp), bp_bytes);
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&p->dSp), sp_bytes);
+    if (e != hipSuccess) {
+      SetLastError("hipMalloc", e);
+      return MNB_ERR_ALLOC;
+    }
+    e = mnb::LaunchPrefillRelayout(p->view, p->dBp, p->dSp, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+      SetLastError("prefill re-layout", e);
+      return MNB_ERR_HIP;
+    }
+    FillView(p);
   }
   return MNB_OK;
 }
@@ -372,7 +400,6 @@ int mnb_plan_create(const mnb_desc *desc, const uint8_t *B, const float *scales,
     delete p;
     return st;
   }
-  FillView(p);
   *out_plan = p;
   return MNB_OK;
 }
@@ -399,7 +426,6 @@ int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float 
     delete p;
     return st;
   }
-  FillView(p);
   *out_plan = p;
   return MNB_OK;
 }
@@ -538,13 +564,14 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
   if (M == 0) return MNB_OK;
   if (dA == nullptr || dY == nullptr) return MNB_ERR_NULL_POINTER;
-  if (path < 0 || path > 4) return MNB_ERR_UNSUPPORTED;
+  if (path < 0 || path > 5) return MNB_ERR_UNSUPPORTED;
   const bool a_aligned = (reinterpret_cast<uintptr_t>(dA) % 16) == 0;
   if (path == 0) path = SelectPath(plan, M, dA);
   if (path == 1 && !(a_aligned && M <= 16 && mnb::GemvSupports(plan->view, M)))
     return MNB_ERR_UNSUPPORTED;
   if (path == 2 && !(a_aligned && mnb::GemmSupports(plan->view, M))) return MNB_ERR_UNSUPPORTED;
   if (path == 4 && !ExactGroupsSupported(plan, a_aligned)) return MNB_ERR_UNSUPPORTED;
+  if (path == 5 && !(a_aligned && mnb::PrefillSupports(plan->view, M))) return MNB_ERR_UNSUPPORTED;
   if (plan->gate_up && dBias != nullptr) return MNB_ERR_UNSUPPORTED;
   if (path == 4) {
     // The decode kernels over consecutive groups of rows, in stream order on
@@ -570,7 +597,7 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   void *work = scratch > 0 ? static_cast<void *>(static_cast<char *>(dWorkspace) + scratch)
                            : dWorkspace;
   const size_t work_bytes = scratch > 0 ? workspace_bytes - scratch : workspace_bytes;
-  if (path == 2) {
+  if (path == 2 || path == 5) {
     const size_t need = mnb::GemmWorkspaceBytes(plan->view, M);
     if (work == nullptr || work_bytes < need || (reinterpret_cast<uintptr_t>(work) % 16) != 0)
       return MNB_ERR_WORKSPACE;
@@ -586,7 +613,7 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // Kernels with the gate/up epilogue take H and write it themselves; after
   // the others, SiluMulKernel turns the scratch sum into H.
-  bool fused = false;
+  bool fused = false, bias_done = false;
   switch (path) {
   case 1:
     if (M == 1 && mnb::GemvM1Supports(plan->view)) {
@@ -610,12 +637,19 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   case 2:
     // The GEMM's fused stores address H with 32-bit byte offsets.
     fused = H != nullptr && M * plan->view.N * 2 < (int64_t{1} << 31);
-    e = mnb::LaunchGemm(plan->view, M, dA, Ys, work, s, fused ? H : nullptr, gamma, eps);
+    e = mnb::LaunchGemm(plan->view, M, dA, Ys, work, s, fused ? H : nullptr, gamma, eps, dBias,
+                        &bias_done);
+    break;
+  case 5:
+    fused = H != nullptr && M * plan->view.N * 2 < (int64_t{1} << 31);
+    e = mnb::LaunchPrefill(plan->view, M, dA, Ys, work, s, fused ? H : nullptr, gamma, eps, dBias,
+                           &bias_done);
     break;
   default: e = mnb::LaunchGeneric(plan->view, M, dA, Ys, s); break;
   }
   if (e == hipSuccess && H != nullptr && !fused) e = mnb::LaunchSiluMul(Ys, H, M, plan->view.N, s);
-  if (e == hipSuccess && dBias != nullptr) e = LaunchAddBias(dY, dBias, M, plan->view.N, s);
+  if (e == hipSuccess && dBias != nullptr && !bias_done)
+    e = LaunchAddBias(dY, dBias, M, plan->view.N, s);
   if (e != hipSuccess) {
     SetLastError("kernel launch", e);
     return MNB_ERR_HIP;

@@ -557,13 +557,17 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
 }
 
 // Split-K epilogue: Y += partials[0] + ... + partials[PARTS - 1], summed in
-// that order for every element, so results do not depend on scheduling.
-// PARTS is a template argument so that every load is in flight before the
-// first add (one HBM round trip per thread, not PARTS of them).
+// that order for every element, so results do not depend on scheduling; then
+// + bias[n] when a bias is given (Y is [mn / N, N]), after the sum, as a
+// separate bias pass would add it. PARTS is a template argument so that every
+// load is in flight before the first add (one HBM round trip per thread, not
+// PARTS of them).
 template <bool VEC, int PARTS>
 __global__ __launch_bounds__(256) void SplitReduceKernel(float *__restrict__ Y,
                                                          const float *__restrict__ P,
-                                                         int64_t mn, float *__restrict__ H) {
+                                                         int64_t mn, float *__restrict__ H,
+                                                         const float *__restrict__ bias,
+                                                         int64_t N) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * (VEC ? 4 : 1);
   if (i >= mn) return;
@@ -575,6 +579,10 @@ __global__ __launch_bounds__(256) void SplitReduceKernel(float *__restrict__ Y,
     f32x4 y = *reinterpret_cast<const f32x4 *>(Y + i);
 #pragma unroll
     for (int p = 0; p < PARTS; ++p) y += v[p];
+    if (bias != nullptr) {  // N % 4 == 0 on this path: the 4 elements share a row
+      const int64_t n = i % N;
+      y += f32x4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
+    }
     if (H != nullptr)  // gate/up pairs (N even: a pair never straddles rows)
       *reinterpret_cast<float2 *>(H + i / 2) = make_float2(SiluMul(y[0], y[1]), SiluMul(y[2], y[3]));
     else
@@ -586,6 +594,7 @@ __global__ __launch_bounds__(256) void SplitReduceKernel(float *__restrict__ Y,
     float y = Y[i];
 #pragma unroll
     for (int p = 0; p < PARTS; ++p) y += v[p];
+    if (bias != nullptr) y += bias[i % N];
     if (H != nullptr) {
       // mn is even: lanes i and i ^ 1 are both in range, in the same wavefront
       const float other = PairSwap(y);
@@ -597,25 +606,28 @@ __global__ __launch_bounds__(256) void SplitReduceKernel(float *__restrict__ Y,
 }
 
 template <int PARTS>
-hipError_t LaunchReduce(float *Y, const float *P, int64_t mn, hipStream_t s, float *H) {
+hipError_t LaunchReduce(float *Y, const float *P, int64_t mn, hipStream_t s, float *H,
+                        const float *bias, int64_t N) {
   if (mn % 4 == 0 && reinterpret_cast<uintptr_t>(Y) % 16 == 0 &&
-      reinterpret_cast<uintptr_t>(H) % 8 == 0) {
+      reinterpret_cast<uintptr_t>(H) % 8 == 0 && (bias == nullptr || N % 4 == 0)) {
     hipLaunchKernelGGL((SplitReduceKernel<true, PARTS>),
                        dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s, Y, P,
-                       mn, H);
+                       mn, H, bias, N);
   } else {
     hipLaunchKernelGGL((SplitReduceKernel<false, PARTS>),
                        dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, Y, P, mn,
-                       H);
+                       H, bias, N);
   }
   return hipGetLastError();
 }
 
 template <int... Ps>
 hipError_t DispatchReduce(int parts, float *Y, const float *P, int64_t mn, hipStream_t s,
-                          float *H, std::integer_sequence<int, Ps...>) {
+                          float *H, std::integer_sequence<int, Ps...>, const float *bias = nullptr,
+                          int64_t N = 1) {
   hipError_t e = hipErrorInvalidValue;
-  (void)((parts == Ps + 1 ? (e = LaunchReduce<Ps + 1>(Y, P, mn, s, H), true) : false) || ...);
+  (void)((parts == Ps + 1 ? (e = LaunchReduce<Ps + 1>(Y, P, mn, s, H, bias, N), true) : false) ||
+         ...);
   return e;
 }
 
@@ -722,10 +734,481 @@ inline Shape PickShape(const WeightView &w, int64_t M) {
   return MakeShape(w, bm, static_cast<int>(splits));
 }
 
+// ---------------------------------------------------------------------------
+// Prefill GEMM over the plan's fragment-ordered weights (PrefillKernel).
+//
+// At plan creation the weights are re-laid for this kernel (RelayoutBKernel,
+// RelayoutSKernel): for each group g of 64 weight rows and each 32-k step s,
+// the 1 KiB record Bp[g][s][lane][j] holds in lane l's 16 bytes the packed
+// word (8 nibbles, original order) of weight row 64g + 16j + (l & 15) at k =
+// 32s + 8(l >> 4): exactly lane l's MFMA operand for the 16 rows of slice j.
+// The 256-byte record Sp[g][s][c][j] holds, per step, the fp16 scale (times
+// the row's 2^e) in the low half and the zero point in the high half, for
+// row 64g + 16j + c and the step's block. Rows past N are zero (scale 0).
+//
+// A workgroup of 8 wavefronts (two per SIMD, one workgroup per CU) computes a
+// 128 x 256 output tile. Wavefronts w and w + 4 own columns 64(w % 4) ..
+// 64(w % 4) + 63 of all 128 rows and split K: w takes the first 32-k step of
+// every 64-k tile, w + 4 the second, so each dequantized weight fragment
+// feeds 8 MFMAs (13 VALU per 8 nibbles: 1.6 VALU per MFMA) and each SIMD
+// holds two independent instruction streams to fill the other's waits. At
+// the end the two halves meet in LDS (each wavefront adds the other's sum
+// for 64 of the rows, in a fixed order). The MFMA takes the weights as its A
+// operand and the activations as its B operand, so each lane's result is 4
+// consecutive output columns of one row: 16-byte stores, and a gate/up pair
+// (columns 2n, 2n + 1) lands in one lane.
+// Every operand streams global -> LDS through direct copies (no registers)
+// into a ring of kPNS stages of one 64-k tile each (A 16 KiB, weights 8 KiB,
+// scales 4 KiB); the copies of tile t + kPSA are issued as tile t starts.
+// The copy order per k-tile is fixed (2 A copies and 1 weight copy per
+// thread, plus 1 scale copy in the first four wavefronts), so each wait is an
+// exact vmcnt. One barrier per k-tile, at its top, makes tile t + 1 visible:
+// tile t's MFMAs then run on fragments read during the previous tile, while
+// tile t + 1's fragments are read and dequantized.
+constexpr int kPTM = 128;                             // output tile rows
+constexpr int kPTN = 256;                             // output tile columns
+constexpr int kPThreads = 512;                        // 8 wavefronts
+constexpr int kPNS = 5;                               // LDS stages (k-tiles)
+constexpr int kPSA = kPNS - 1;                        // copy distance (k-tiles)
+constexpr int kPAU = kPTM * kUnits;                   // A units per stage (1024)
+constexpr int kPBU = 128;                             // weight units per column group per stage
+constexpr int kPSU = 64;                              // scale units per column group per stage
+constexpr int kPStage = kPAU + 4 * (kPBU + kPSU);     // 1792 units, 28 KiB
+constexpr size_t kPLds = size_t{kPNS} * kPStage * 16; // 140 KiB
+constexpr int kPOps0 = kPAU / kPThreads + 2;          // copies per k-tile, wavefronts 0-3
+constexpr int kPOps1 = kPAU / kPThreads + 1;          // wavefronts 4-7 (no scale copy)
+
+// (scale fp16 | zp << 16) -> the operands of DequantWord.
+template <bool HAS_ZP>
+__device__ __forceinline__ DequantRow RowFromSz(uint32_t w) {
+  DequantRow r;
+  r.s = __builtin_amdgcn_perm(w, w, 0x01000100u);  // the fp16 scale in both halves
+  if constexpr (HAS_ZP) {
+    const uint32_t z = w >> 16;
+    r.neg_lo = 0xE400E400u + z * 0x00010001u;  // fp16 -(1024 + z): ulp 1 at 1024
+    r.neg_hi = 0xD400D400u + z * 0x00100010u;  // fp16 -(64 + z): ulp 1/16 at 64
+  } else {
+    r.neg_lo = 0xE408E408u;  // -(1024 + 8)
+    r.neg_hi = 0xD480D480u;  // -(64 + 8)
+  }
+  return r;
+}
+
+template <bool HAS_ZP, bool BS32>
+__global__ __launch_bounds__(kPThreads, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+PrefillKernel(const uint4 *__restrict__ Ah, const uint8_t *__restrict__ Bp,
+              const uint8_t *__restrict__ Sp, float *__restrict__ Y, int M, int N, int K,
+              int kt_per_split, float *__restrict__ partials, float *__restrict__ H,
+              const int *__restrict__ row_exp, const int *__restrict__ col_exp,
+              const float *__restrict__ bias) {
+  extern __shared__ uint4 lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cg = wave & 3;   // column group: columns 64 cg .. 64 cg + 63 of the tile
+
+  // Workgroup b -> (split, output tile). XCD x (b % 8) takes a contiguous run
+  // of the tile order, which walks groups of 4 M tiles N tile by N tile, so
+  // an XCD's L2 holds about 4 A bands and a run of weight bands.
+  const int tiles_m = (M + kPTM - 1) / kPTM;
+  const int tiles_n = (N + kPTN - 1) / kPTN;
+  const int tiles = tiles_m * tiles_n;
+  const int split = static_cast<int>(blockIdx.x) / tiles;
+  int tm, tn;
+  {
+    int L = static_cast<int>(blockIdx.x) - split * tiles;
+    if (tiles % 8 == 0) L = (L & 7) * (tiles / 8) + (L >> 3);
+    constexpr int kGM = 4;
+    const int group = L / (kGM * tiles_n);
+    const int gm = min(kGM, tiles_m - group * kGM);
+    const int rem = L - group * kGM * tiles_n;
+    tm = group * kGM + rem % gm;
+    tn = rem / gm;
+  }
+  const int m0 = tm * kPTM;
+  const int n0 = tn * kPTN;
+  const int T = K / 32;
+  const int kt0 = split * kt_per_split;
+  const int ktiles = min(kt_per_split, K / kBK - kt0);
+  const int klast = ktiles - 1;
+  const int g = n0 / 64 + cg;
+
+  // The body, for the 32-k step sg (0 for wavefronts 0-3, 1 for 4-7) as a
+  // template argument: no branch inside the loop, every index a constant.
+  auto body = [&](auto sg_c) __attribute__((always_inline)) {
+  constexpr int sg = decltype(sg_c)::value;
+  // Copies per k-tile: A instruction i of wavefront w takes units
+  // i * 512 + 64 w + lane; wavefront w the weight record of (g, step sg);
+  // wavefronts 0-3 the scale record of g (both steps; lanes 32-63 repeat
+  // lanes 0-31).
+  const uint4 *a_src = Ah + (static_cast<size_t>(tm) * (K / kBK) + kt0) * kPAU + wave * 64 + lane;
+  const uint8_t *b_src = Bp + (static_cast<size_t>(g) * T + 2 * kt0 + sg) * 1024 + lane * 16;
+  const uint8_t *s_src = Sp + (static_cast<size_t>(g) * T + 2 * kt0) * 256 + (lane & 31) * 16;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  auto issue = [&](int kt, int st) {
+    const uint32_t base = lds0 + static_cast<uint32_t>(st * kPStage * 16);
+#pragma unroll
+    for (int i = 0; i < kPAU / kPThreads; ++i)
+      CopyToLds16(a_src + static_cast<size_t>(kt) * kPAU + i * kPThreads,
+                  base + static_cast<uint32_t>((i * kPThreads + wave * 64) * 16));
+    CopyToLds16(b_src + static_cast<size_t>(kt) * 2048,
+                base + static_cast<uint32_t>((kPAU + cg * kPBU + sg * 64) * 16));
+    if constexpr (sg == 0)
+      CopyToLds16(s_src + static_cast<size_t>(kt) * 512,
+                  base + static_cast<uint32_t>((kPAU + 4 * kPBU + cg * kPSU) * 16));
+  };
+  // Tile t + 1 has landed once only the copies of tiles t + 2 .. t + kPSA - 1
+  // (issued at the tops of the iterations since) are outstanding.
+  constexpr int kOps = sg == 0 ? kPOps0 : kPOps1;
+  auto readA = [&](const uint4 *sb, int i) {
+    return __builtin_bit_cast(half8, sb[Swz(i * 16 + (lane & 15), 4 * sg + (lane >> 4))]);
+  };
+  auto readB = [&](const uint4 *sb) { return sb[kPAU + cg * kPBU + sg * 64 + lane]; };
+  auto readS = [&](const uint4 *sb) {
+    return sb[kPAU + 4 * kPBU + cg * kPSU + sg * 16 + (lane & 15)];
+  };
+
+  floatx4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const DequantConsts dq = MakeDequantConsts();
+  // Dequantized weight fragments of one 32-k step (MFMA A operands, slices j).
+  auto dequant = [&](uint4 bw, uint4 sw, half8 (&bf)[4]) __attribute__((always_inline)) {
+    const uint32_t w[4] = {bw.x, bw.y, bw.z, bw.w};
+    const uint32_t z[4] = {sw.x, sw.y, sw.z, sw.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      bf[j] = __builtin_bit_cast(half8, DequantWord(w[j], RowFromSz<HAS_ZP>(z[j]), dq));
+  };
+  // The 32 MFMAs of one step; activation fragment i is refilled with the next
+  // tile's right after its last use, so one set of 8 fragment registers
+  // serves every tile.
+  auto mma = [&](half8 (&a)[8], const half8 (&bf)[4], const uint4 *sbn)
+                 __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], a[i], acc[i][j], 0, 0, 0);
+      a[i] = readA(sbn, i);
+    }
+  };
+  // Issue order of one step for the scheduler: 8 MFMAs while the raw next
+  // reads (pinned ahead by a sched_barrier) arrive, then each MFMA followed by
+  // up to 3 VALU of the next tile's dequantization (an MFMA occupies the pipe
+  // for 16 cycles, a VALU issues in 4), with the 8 fragment refills spread
+  // behind the MFMAs that free them.
+  auto schedule_step = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // fragment refill
+    }
+#pragma unroll
+    for (int i = 2; i < 8; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+
+  // Prologue: tiles 0 .. kPSA-1 into stages 0 .. kPSA-1; wait for tile 0.
+#pragma unroll
+  for (int p = 0; p < kPSA; ++p) issue(min(p, klast), p);
+  WaitVm<kOps * (kPSA - 1)>();
+  __syncthreads();
+  half8 a[8], bf[4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = readA(lds, i);
+  dequant(readB(lds), readS(lds), bf);
+  for (int t = 0; t < ktiles; ++t) {
+    const uint4 *sb1 = lds + ((t + 1) % kPNS) * kPStage;
+    // Tile t + 1 complete and visible (only the copies of tiles t + 2 ..
+    // t + kPSA - 1 are outstanding); every wavefront is past tile t - 1.
+    WaitVm<kOps * (kPSA - 2)>();
+    __syncthreads();
+    // Tile t + kPSA into stage (t - 1) % kPNS, last read in iteration t - 2.
+    issue(min(t + kPSA, klast), (t + kPSA) % kPNS);
+    const uint4 bwn = readB(sb1);
+    const uint4 swn = readS(sb1);
+    __builtin_amdgcn_sched_barrier(0);
+    half8 bfn[4];
+    dequant(bwn, swn, bfn);
+    mma(a, bf, sb1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bf[j] = bfn[j];
+    schedule_step();
+  }
+  // No copy into this workgroup's LDS may land after it exits, or after the
+  // LDS is reused below.
+  WaitVm<0>();
+  __syncthreads();
+
+  // The two K halves meet: wavefront w + 4s finishes rows 64s .. 64s + 63
+  // (fragments i = 4s .. 4s + 3) of column group cg and hands the other rows
+  // to its partner through LDS (16 KiB per wavefront, as 16 x 16 fragments of
+  // 16 bytes per lane). Sum order: step 0's half, then step 1's. The half is
+  // a template argument so every accumulator index is a constant.
+  float *out = split > 0 ? partials + static_cast<size_t>(split - 1) * M * N : Y;
+  const int nl = n0 + cg * 64 + 4 * (lane >> 4);
+  const int rows = min(M - m0, kPTM);
+  {
+    constexpr int S = sg;
+    uint4 *xb = lds + wave * 1024;  // this wavefront's outgoing fragments
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const floatx4 v = acc[4 * (1 - S) + q][j];
+        xb[(q * 4 + j) * 64 + lane] = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                                 __float_as_uint(v[2]), __float_as_uint(v[3]));
+      }
+    __syncthreads();
+    const uint4 *pb = lds + (wave ^ 4) * 1024;  // the partner's fragments for my rows
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 u = pb[(q * 4 + j) * 64 + lane];
+        const floatx4 o = {__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                           __uint_as_float(u.w)};
+        acc[4 * S + q][j] = S == 0 ? acc[4 * S + q][j] + o : o + acc[4 * S + q][j];
+      }
+
+    // Epilogue over this wavefront's 64 rows. Lane l holds, for fragment i
+    // (rows 16i .. 16i + 15) and slice j, row m0 + 16i + (l & 15) and the 4
+    // columns n0 + 64 cg + 16j + 4(l >> 4) + v. The accumulators are in units
+    // of 2^(f_m + e_n): one ldexp per element undoes both. Split 0 writes Y
+    // (and adds the bias), split s > 0 its partial sum.
+    int er[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) er[q] = row_exp[m0 + (4 * S + q) * 16 + (lane & 15)];
+    if (H != nullptr) {
+      const int half_n = N >> 1;
+      const auto hr = __builtin_amdgcn_make_buffer_rsrc(H + static_cast<size_t>(m0) * half_n, 0,
+                                                        rows * half_n * 4, 0x00020000);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = nl + 16 * j;
+        const int nc = min(n, N - 4);
+        const int e0 = col_exp[nc], e1 = col_exp[nc + 1], e2 = col_exp[nc + 2],
+                  e3 = col_exp[nc + 3];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const floatx4 a = acc[4 * S + q][j];
+          const float x0 = a[0], x1 = a[1], x2 = a[2], x3 = a[3];
+          const float h0 = SiluMul(__builtin_amdgcn_ldexpf(x0, -(er[q] + e0)),
+                                   __builtin_amdgcn_ldexpf(x1, -(er[q] + e1)));
+          const float h1 = SiluMul(__builtin_amdgcn_ldexpf(x2, -(er[q] + e2)),
+                                   __builtin_amdgcn_ldexpf(x3, -(er[q] + e3)));
+          const int row = (4 * S + q) * 16 + (lane & 15);
+          const int off = n < N ? (row * half_n + (n >> 1)) * 4 : 0x7FFFFFF0;
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h0), hr, off, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h1), hr, n < N ? off + 4 : off,
+                                                0, 0);
+        }
+      }
+      return;
+    }
+    const auto yr = __builtin_amdgcn_make_buffer_rsrc(out + static_cast<size_t>(m0) * N, 0,
+                                                      rows * N * 4, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = nl + 16 * j;
+      const int nc = min(n, N - 4);
+      const int e0 = col_exp[nc], e1 = col_exp[nc + 1], e2 = col_exp[nc + 2], e3 = col_exp[nc + 3];
+      float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+      if (bias != nullptr && split == 0) {
+        b0 = bias[nc];
+        b1 = bias[nc + 1];
+        b2 = bias[nc + 2];
+        b3 = bias[nc + 3];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const floatx4 a = acc[4 * S + q][j];
+        const float x0 = a[0], x1 = a[1], x2 = a[2], x3 = a[3];
+        typedef unsigned int u32x4 __attribute__((vector_size(16)));
+        const u32x4 v = {__float_as_uint(__builtin_amdgcn_ldexpf(x0, -(er[q] + e0)) + b0),
+                         __float_as_uint(__builtin_amdgcn_ldexpf(x1, -(er[q] + e1)) + b1),
+                         __float_as_uint(__builtin_amdgcn_ldexpf(x2, -(er[q] + e2)) + b2),
+                         __float_as_uint(__builtin_amdgcn_ldexpf(x3, -(er[q] + e3)) + b3)};
+        const int row = (4 * S + q) * 16 + (lane & 15);
+        const int off = n < N ? (row * N + n) * 4 : 0x7FFFFFF0;
+        __builtin_amdgcn_raw_buffer_store_b128(v, yr, off, 0, 0);
+      }
+    }
+  }
+  };
+  if ((wave >> 2) == 0)
+    body(std::integral_constant<int, 0>{});
+  else
+    body(std::integral_constant<int, 1>{});
+}
+
+// Splits of a prefill launch: enough workgroups for one per CU when the
+// tiles alone do not fill the chip, each split at least 8 k-tiles long.
+inline int PrefillSplits(const WeightView &w, int64_t M) {
+  const int64_t tiles = (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN);
+  const int ktiles = static_cast<int>(w.K / kBK);
+  int64_t splits = std::max<int64_t>(1, w.num_cus / tiles);
+  splits = std::min<int64_t>({splits, kMaxSplits, std::max(1, ktiles / 8)});
+  const int per = static_cast<int>((ktiles + splits - 1) / splits);
+  return (ktiles + per - 1) / per;
+}
+
+template <bool HAS_ZP, bool BS32>
+hipError_t LaunchPrefillT(const WeightView &w, int64_t M, const uint4 *Ah, float *Y,
+                          float *partials, int splits, hipStream_t s, float *H,
+                          const int *row_exp, const float *bias) {
+  const int ktiles = static_cast<int>(w.K / kBK);
+  const int per = (ktiles + splits - 1) / splits;
+  const int tiles = static_cast<int>((M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN));
+  hipLaunchKernelGGL((PrefillKernel<HAS_ZP, BS32>), dim3(tiles * splits), dim3(kPThreads), kPLds, s, Ah,
+                     w.Bp, w.Sp, Y, static_cast<int>(M), static_cast<int>(w.N),
+                     static_cast<int>(w.K), per, partials, H, row_exp, w.col_exp, bias);
+  return hipGetLastError();
+}
+
+// The plan-time re-layout (once per plan, see PrefillKernel).
+__global__ __launch_bounds__(256) void RelayoutBKernel(const uint8_t *__restrict__ B,
+                                                       uint32_t *__restrict__ Bp, int64_t N,
+                                                       int64_t row_bytes, int64_t T,
+                                                       int64_t words) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= words) return;
+  const int j = static_cast<int>(idx & 3);
+  const int l = static_cast<int>((idx >> 2) & 63);
+  const int64_t gs = idx >> 8;
+  const int64_t s = gs % T, g = gs / T;
+  const int64_t n = 64 * g + 16 * j + (l & 15);
+  Bp[idx] = n < N ? *reinterpret_cast<const uint32_t *>(B + n * row_bytes + 16 * s + 4 * (l >> 4))
+                  : 0u;
+}
+
+__global__ __launch_bounds__(256) void RelayoutSKernel(const float *__restrict__ S,
+                                                       const uint8_t *__restrict__ Z,
+                                                       const int32_t *__restrict__ col_exp,
+                                                       uint32_t *__restrict__ Sp, int64_t N,
+                                                       int64_t nb, int64_t zp_row_bytes,
+                                                       int log2_bs, int64_t T, int64_t words) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= words) return;
+  const int j = static_cast<int>(idx & 3);
+  const int c = static_cast<int>((idx >> 2) & 15);
+  const int64_t gs = idx >> 6;
+  const int64_t s = gs % T, g = gs / T;
+  const int64_t n = 64 * g + 16 * j + c;
+  const int64_t b = (32 * s) >> log2_bs;
+  uint32_t v = 8u << 16;  // rows past N: scale 0
+  if (n < N) {
+    const _Float16 h = static_cast<_Float16>(__builtin_amdgcn_ldexpf(S[n * nb + b], col_exp[n]));
+    const uint32_t z = Z != nullptr ? (Z[n * zp_row_bytes + (b >> 1)] >> (4 * (b & 1))) & 0xFu : 8u;
+    v = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h)) | (z << 16);
+  }
+  Sp[idx] = v;
+}
+
+bool PrefillSupportsShape(const WeightView &w) {
+  return w.Bp != nullptr && w.Sp != nullptr && (w.K % kBK) == 0 && w.block_size >= 32 &&
+         (w.N % 4) == 0 && w.N < (int64_t{1} << 22) && w.K <= (int64_t{1} << 24);
+}
+
+bool PrefillSupportsM(const WeightView &w, int64_t M) {
+  return M >= 1 && M <= (int64_t{1} << 30) && PrefillSupportsShape(w) &&
+         (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN) * kMaxSplits < (int64_t{1} << 31);
+}
+
+// The prefill kernel serves the automatic GEMM path when its 128 x 256 tiles
+// alone fill the CUs in whole waves (its last wave at least 85% full): then
+// it needs no split-K, and one workgroup per CU keeps every CU busy to the
+// end. Measured on MI355X (c4, c5 shapes): 10-17% faster than GemmKernel at
+// M = 2048 on c4, c5 o, gate+up and down; slower where split-K must supply
+// the workgroups (M = 512: 45 -> 68 us on c4) or a last wave is half empty
+// (c5 qkv at M = 2048, 1.5 waves: 146 -> 156 us), which GemmKernel keeps.
+bool UsePrefill(const WeightView &w, int64_t M) {
+  if (M < 65 || !PrefillSupportsM(w, M)) return false;
+  const int64_t tiles = (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN);
+  const int64_t cus = w.num_cus;
+  if (tiles < cus) return false;
+  const int64_t waves = (tiles + cus - 1) / cus;
+  return tiles * 100 >= waves * cus * 85;
+}
+
+size_t PrefillPartialBytes(const WeightView &w, int64_t M) {
+  return static_cast<size_t>(PrefillSplits(w, M) - 1) * static_cast<size_t>(M) * w.N * 4;
+}
+
 } // namespace
 
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M) {
-  return AImageBytes(w, M) + RowExpBytes(M) + PartialBytes(w, M, PickShape(w, M));
+  size_t partial = PartialBytes(w, M, PickShape(w, M));
+  if (PrefillSupportsM(w, M)) partial = std::max(partial, PrefillPartialBytes(w, M));
+  return AImageBytes(w, M) + RowExpBytes(M) + partial;
+}
+
+bool PrefillSupports(const WeightView &w, int64_t M) { return PrefillSupportsM(w, M); }
+
+
+size_t PrefillLayoutBytes(const WeightView &w, size_t *sp_bytes) {
+  const int64_t groups = (w.N + kPTN - 1) / kPTN * (kPTN / 64);
+  const int64_t steps = w.K / 32;
+  if (sp_bytes != nullptr) *sp_bytes = static_cast<size_t>(groups * steps * 256);
+  return static_cast<size_t>(groups * steps * 1024);
+}
+
+bool PrefillLayoutWanted(const WeightView &w) {
+  WeightView v = w;
+  v.Bp = v.Sp = reinterpret_cast<const uint8_t *>(16);  // the shape checks only
+  return PrefillSupportsShape(v) && (w.row_bytes % 16) == 0;
+}
+
+hipError_t LaunchPrefillRelayout(const WeightView &w, uint8_t *Bp, uint8_t *Sp, hipStream_t s) {
+  size_t sp_bytes = 0;
+  const size_t bp_bytes = PrefillLayoutBytes(w, &sp_bytes);
+  const int64_t T = w.K / 32;
+  const int64_t bw = static_cast<int64_t>(bp_bytes / 4), sw = static_cast<int64_t>(sp_bytes / 4);
+  hipLaunchKernelGGL(RelayoutBKernel, dim3(static_cast<unsigned>((bw + 255) / 256)), dim3(256), 0,
+                     s, w.B, reinterpret_cast<uint32_t *>(Bp), w.N, w.row_bytes, T, bw);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(RelayoutSKernel, dim3(static_cast<unsigned>((sw + 255) / 256)), dim3(256), 0,
+                     s, w.scales, w.zp, w.col_exp, reinterpret_cast<uint32_t *>(Sp), w.N, w.nb,
+                     w.zp_row_bytes, w.log2_bs, T, sw);
+  return hipGetLastError();
+}
+
+// ConvertA, the prefill kernel, and the split reduction when K is split.
+static hipError_t LaunchPrefillGemm(const WeightView &w, int64_t M, const float *A, float *Y,
+                                    void *work, hipStream_t s, float *H, const float *gamma,
+                                    float eps, const float *bias, int splits) {
+  uint4 *Ah = static_cast<uint4 *>(work);
+  int *row_exp = reinterpret_cast<int *>(static_cast<char *>(work) + AImageBytes(w, M));
+  float *partials = reinterpret_cast<float *>(static_cast<char *>(work) + AImageBytes(w, M) +
+                                              RowExpBytes(M));
+  hipError_t e = gamma != nullptr
+                     ? LaunchConvertA<kPTM, true>(w, M, A, Ah, row_exp, s, gamma, eps)
+                     : LaunchConvertA<kPTM, false>(w, M, A, Ah, row_exp, s, nullptr, 0.0f);
+  if (e != hipSuccess) return e;
+  // One split: the kernel's stores apply the gate/up activation or add the
+  // bias. Several: the ordered reduction does, after the partial sums.
+  float *Hk = splits == 1 ? H : nullptr;
+  const float *bk = splits == 1 ? bias : nullptr;
+  const bool zp = w.zp != nullptr, bs32 = w.block_size == 32;
+  if (zp)
+    e = bs32 ? LaunchPrefillT<true, true>(w, M, Ah, Y, partials, splits, s, Hk, row_exp, bk)
+             : LaunchPrefillT<true, false>(w, M, Ah, Y, partials, splits, s, Hk, row_exp, bk);
+  else
+    e = bs32 ? LaunchPrefillT<false, true>(w, M, Ah, Y, partials, splits, s, Hk, row_exp, bk)
+             : LaunchPrefillT<false, false>(w, M, Ah, Y, partials, splits, s, Hk, row_exp, bk);
+  if (e != hipSuccess || splits == 1) return e;
+  return DispatchReduce(splits - 1, Y, partials, M * w.N, s, H,
+                        std::make_integer_sequence<int, kMaxSplits - 1>{}, bias, w.N);
 }
 
 size_t GemmShapeWorkspaceBytes(const WeightView &w, int64_t M, int splits) {
@@ -743,9 +1226,23 @@ bool GemmSupports(const WeightView &w, int64_t M) {
          w.N <= (int64_t{1} << 30) && w.K <= (int64_t{1} << 24);
 }
 
+hipError_t LaunchPrefill(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                         hipStream_t s, float *H, const float *gamma, float eps, const float *bias,
+                         bool *bias_done) {
+  if (bias_done != nullptr) *bias_done = bias != nullptr;
+  return LaunchPrefillGemm(w, M, A, Y, work, s, H, gamma, eps, bias, PrefillSplits(w, M));
+}
+
 hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                            hipStream_t s, int bm, int splits, float *H, const float *gamma,
                            float eps) {
+  if (bm == kPrefillTileCode) {
+    if (!PrefillSupportsShape(w)) return hipErrorInvalidValue;
+    const int ktiles = static_cast<int>(w.K / kBK);
+    splits = std::max(1, std::min({splits, ktiles, kMaxSplits}));
+    const int per = (ktiles + splits - 1) / splits;
+    return LaunchPrefillGemm(w, M, A, Y, work, s, H, gamma, eps, nullptr, (ktiles + per - 1) / per);
+  }
   Shape sh = PickShape(w, M);
   if (bm > 0) sh = MakeShape(w, bm, splits > 0 ? splits : 1);
   switch (sh.bm) {
@@ -757,8 +1254,16 @@ hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float
 }
 
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                      hipStream_t s, float *H, const float *gamma, float eps) {
+                      hipStream_t s, float *H, const float *gamma, float eps, const float *bias,
+                      bool *bias_done) {
+  if (bias_done != nullptr) *bias_done = false;
+  if (UsePrefill(w, M)) {
+    if (bias_done != nullptr) *bias_done = bias != nullptr;
+    return LaunchPrefillGemm(w, M, A, Y, work, s, H, gamma, eps, bias, PrefillSplits(w, M));
+  }
   return LaunchGemmShape(w, M, A, Y, work, s, 0, 0, H, gamma, eps);
 }
+
+bool GemmUsesPrefill(const WeightView &w, int64_t M) { return UsePrefill(w, M); }
 
 } // namespace mnb

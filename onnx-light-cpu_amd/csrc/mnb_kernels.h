@@ -80,6 +80,8 @@ struct WeightView {
   const float *scales;    // [N, nb]
   const uint8_t *zp;      // [N, zp_row_bytes] packed nibbles, or nullptr (zp = 8)
   const int32_t *col_exp; // [N] RangeExponent(max_b |scales[n][b]|, kScaleExpTarget)
+  const uint8_t *Bp;      // the prefill kernel's fragment-ordered weights, or nullptr
+  const uint8_t *Sp;      // its per-step scale / zero-point words, or nullptr
   int64_t K;
   int64_t N;
   int64_t nb;             // ceil(K / bs)
@@ -140,14 +142,33 @@ hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, f
 // holds GemmWorkspaceBytes(w, M) bytes of device memory: A scaled per row by
 // a power of two and rounded to fp16, the rows' exponents, then the partial
 // sums of a split-K launch.
+// The prefill kernel (128 x 256 tiles over the plan's re-laid weights) serves
+// M >= 65 when the plan holds them; it adds `bias` (N floats) in its
+// epilogue and then sets *bias_done. Otherwise GemmKernel (BM x 128 tiles
+// over the original layout) serves.
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                       hipStream_t s, float *H = nullptr, const float *gamma = nullptr,
-                      float eps = 0.0f);
+                      float eps = 0.0f, const float *bias = nullptr, bool *bias_done = nullptr);
+bool GemmUsesPrefill(const WeightView &w, int64_t M);
+// The prefill kernel forced (any M >= 1 on a plan holding the re-laid
+// weights; split-K when its tiles alone do not fill the CUs); adds `bias`
+// in its epilogue and sets *bias_done.
+hipError_t LaunchPrefill(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                         hipStream_t s, float *H = nullptr, const float *gamma = nullptr,
+                         float eps = 0.0f, const float *bias = nullptr, bool *bias_done = nullptr);
+bool PrefillSupports(const WeightView &w, int64_t M);
+// The prefill kernel's weight layout: whether the plan's shape can use it,
+// its byte sizes (Bp returned, Sp through sp_bytes), and the plan-time
+// re-layout from B, scales, zero points and col_exp.
+bool PrefillLayoutWanted(const WeightView &w);
+size_t PrefillLayoutBytes(const WeightView &w, size_t *sp_bytes);
+hipError_t LaunchPrefillRelayout(const WeightView &w, uint8_t *Bp, uint8_t *Sp, hipStream_t s);
 bool GemmSupports(const WeightView &w, int64_t M);
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M);
-// Same with an explicit tile height (32, 64 or 128; 0 picks both) and split
-// count (1..16), for tuning; `work` then holds
-// GemmShapeWorkspaceBytes(w, M, splits) bytes.
+// Same with an explicit tile height (32, 64 or 128; 0 picks both;
+// kPrefillTileCode = the prefill kernel) and split count (1..16), for
+// tuning; `work` then holds GemmShapeWorkspaceBytes(w, M, splits) bytes.
+constexpr int kPrefillTileCode = 256;
 hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                            hipStream_t s, int bm, int splits, float *H = nullptr,
                            const float *gamma = nullptr, float eps = 0.0f);
