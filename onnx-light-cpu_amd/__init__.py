@@ -391,8 +391,15 @@ def host_library():
         H.olc_amd_run_node.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int, ctypes.c_int,
                                        ctypes.POINTER(ctypes.c_char_p), i64p, ctypes.c_int,
                                        ctypes.POINTER(vp), i32p, i32p, i32p, i64p, vp,
-                                       ctypes.c_int64, vp]
+                                       ctypes.c_int64, vp, ctypes.c_size_t, vp]
         H.olc_amd_run_node.restype = ctypes.c_int
+        H.olc_amd_kernel_create.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int,
+                                            ctypes.c_int, ctypes.POINTER(ctypes.c_char_p), i64p]
+        H.olc_amd_kernel_create.restype = vp
+        H.olc_amd_kernel_run.argtypes = [vp, ctypes.c_int, ctypes.POINTER(vp), i32p, i32p, i32p,
+                                         i64p, vp, ctypes.c_int64, vp, ctypes.c_size_t, vp]
+        H.olc_amd_kernel_run.restype = ctypes.c_int
+        H.olc_amd_kernel_destroy.argtypes = [vp]
         H.olc_amd_dequantize_linear_to_matmul_nbits.argtypes = [
             ctypes.c_int, ctypes.c_int64, ctypes.c_int64, vp, vp, ctypes.c_int, i64p, vp,
             ctypes.c_int, ctypes.c_int64, ctypes.c_int64, i64p, vp, ctypes.c_size_t, vp,
@@ -456,25 +463,76 @@ DEVICE_CPU, DEVICE_GPU = 1, 2
 DTYPE_FLOAT, DTYPE_UINT8 = 1, 2
 
 
-def run_node(domain, op_type, attrs, inputs, out, stream=None, device=DEVICE_GPU):
+def _attr_arrays(attrs):
+    names = (ctypes.c_char_p * max(1, len(attrs)))(*[k.encode() for k in attrs])
+    vals = (ctypes.c_int64 * max(1, len(attrs)))(*attrs.values())
+    return names, vals
+
+
+def _input_arrays(inputs):
+    n = len(inputs)
+    ptrs = (ctypes.c_void_p * max(1, n))(*[None if p is None else p for p, _, _, _ in inputs])
+    types = (ctypes.c_int32 * max(1, n))(*[t for _, t, _, _ in inputs])
+    devs = (ctypes.c_int32 * max(1, n))(*[d for _, _, d, _ in inputs])
+    ranks = (ctypes.c_int32 * max(1, n))(*[len(s) for _, _, _, s in inputs])
+    flat = [d for _, _, _, s in inputs for d in s]
+    dims = (ctypes.c_int64 * max(1, len(flat)))(*flat)
+    return n, ptrs, types, devs, ranks, dims
+
+
+def run_node(domain, op_type, attrs, inputs, out, stream=None, device=DEVICE_GPU,
+             workspace=None):
     """Runs one node through the dispatch table, as onnx-light's RunNode would.
 
     inputs: list of (pointer or None, dtype, device, shape) tuples; out: a
-    contiguous float32 torch tensor receiving Y.
+    contiguous float32 torch tensor receiving Y; workspace: a device torch
+    tensor the run may use as scratch (RuntimeContext's workspace allocator),
+    or None.
     """
     H = host_library()
-    names = (ctypes.c_char_p * len(attrs))(*[k.encode() for k in attrs])
-    vals = (ctypes.c_int64 * len(attrs))(*attrs.values())
-    n = len(inputs)
-    ptrs = (ctypes.c_void_p * n)(*[None if p is None else p for p, _, _, _ in inputs])
-    types = (ctypes.c_int32 * n)(*[t for _, t, _, _ in inputs])
-    devs = (ctypes.c_int32 * n)(*[d for _, _, d, _ in inputs])
-    ranks = (ctypes.c_int32 * n)(*[len(s) for _, _, _, s in inputs])
-    flat = [d for _, _, _, s in inputs for d in s]
-    dims = (ctypes.c_int64 * max(1, len(flat)))(*flat)
+    names, vals = _attr_arrays(attrs)
+    n, ptrs, types, devs, ranks, dims = _input_arrays(inputs)
     s = None if stream is None else ctypes.c_void_p(stream)
-    _host_check(H.olc_amd_run_node(domain.encode(), op_type.encode(), device, len(attrs), names,
-                                   vals, n, ptrs, types, devs, ranks, dims,
-                                   None if out is None else ctypes.c_void_p(out.data_ptr()),
-                                   0 if out is None else out.numel(), s))
+    _host_check(H.olc_amd_run_node(
+        domain.encode(), op_type.encode(), device, len(attrs), names, vals, n, ptrs, types, devs,
+        ranks, dims, None if out is None else ctypes.c_void_p(out.data_ptr()),
+        0 if out is None else out.numel(),
+        None if workspace is None else ctypes.c_void_p(workspace.data_ptr()),
+        0 if workspace is None else workspace.numel() * workspace.element_size(), s))
     return out
+
+
+class NodeKernel:
+    """One kernel object from the dispatch table, kept across runs the way a
+    session keeps a node's kernel; runs may come from several threads at once,
+    each with its own stream, output and workspace."""
+
+    def __init__(self, domain, op_type, attrs, device=DEVICE_GPU):
+        H = host_library()
+        names, vals = _attr_arrays(attrs)
+        self._h = H.olc_amd_kernel_create(domain.encode(), op_type.encode(), device, len(attrs),
+                                          names, vals)
+        if not self._h:
+            raise ValueError(H.olc_amd_last_error().decode())
+
+    def run(self, inputs, out, stream=None, workspace=None):
+        H = host_library()
+        n, ptrs, types, devs, ranks, dims = _input_arrays(inputs)
+        s = None if stream is None else ctypes.c_void_p(stream)
+        _host_check(H.olc_amd_kernel_run(
+            ctypes.c_void_p(self._h), n, ptrs, types, devs, ranks, dims,
+            ctypes.c_void_p(out.data_ptr()), out.numel(),
+            None if workspace is None else ctypes.c_void_p(workspace.data_ptr()),
+            0 if workspace is None else workspace.numel() * workspace.element_size(), s))
+        return out
+
+    def close(self):
+        if self._h:
+            host_library().olc_amd_kernel_destroy(ctypes.c_void_p(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -67,6 +67,17 @@ TensorView &RuntimeContext::MakeOutputTensor(size_t i, DataType type, std::vecto
   return out;
 }
 
+void *RuntimeContext::Workspace(size_t bytes) {
+  if (bytes == 0) return nullptr;
+  if (!allocate_workspace)
+    throw std::invalid_argument("onnx_light_cpu_amd::RuntimeContext: no workspace allocator (" +
+                                std::to_string(bytes) + " bytes needed)");
+  void *p = allocate_workspace(bytes);
+  if (p == nullptr)
+    throw std::runtime_error("onnx_light_cpu_amd::RuntimeContext: workspace allocation failed");
+  return p;
+}
+
 KernelRegistrationScope::KernelRegistrationScope(std::vector<KernelRegistration> *inventory) {
   if (CurrentScope() == nullptr) {
     CurrentScope() = this;

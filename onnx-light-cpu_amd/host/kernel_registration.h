@@ -59,8 +59,9 @@ struct NodeAttributes {
   }
 };
 
-// Per-run context: optional inputs, outputs, the stream and an output
-// allocator supplied by the caller (onnx-light's rt->MakeOutputTensor role).
+// Per-run context: optional inputs, outputs, the stream, an output allocator
+// (onnx-light's rt->MakeOutputTensor role) and a workspace allocator, all
+// supplied by the caller for this one run.
 class RuntimeContext {
 public:
   using Allocator = std::function<void *(size_t bytes)>;
@@ -69,6 +70,10 @@ public:
   std::vector<TensorView> outputs;
   void *stream = nullptr;
   Allocator allocate_output;
+  // Device scratch for this run only, 16-byte aligned, usable in stream
+  // order on `stream` until the run's work completes (a session's arena or a
+  // caller buffer). Kernels never allocate device memory themselves.
+  Allocator allocate_workspace;
 
   const TensorView *GetInput(size_t i) const {
     return i < inputs.size() && inputs[i].has_value() ? &*inputs[i] : nullptr;
@@ -76,6 +81,9 @@ public:
   // Allocates output i with `shape` through allocate_output, or checks a
   // preset output buffer of that shape.
   TensorView &MakeOutputTensor(size_t i, DataType type, std::vector<int64_t> shape);
+  // `bytes` of workspace through allocate_workspace (nullptr for 0 bytes);
+  // throws std::invalid_argument when there is no workspace allocator.
+  void *Workspace(size_t bytes);
 };
 
 class KernelBase {

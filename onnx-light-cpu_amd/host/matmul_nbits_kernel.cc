@@ -49,34 +49,17 @@ MatMulNBitsKernel::MatMulNBitsKernel(const NodeAttributes &attrs) {
 }
 
 MatMulNBitsKernel::~MatMulNBitsKernel() {
-  if (plan_ != nullptr) mnb_plan_destroy(plan_);
-  if (work_ != nullptr) (void)hipFree(work_);
+  for (auto &kv : plans_) mnb_plan_destroy(kv.second);
 }
 
-void *MatMulNBitsKernel::Workspace(int64_t M) {
-  size_t need = 0;
-  CheckStatus(mnb_workspace_bytes(plan_, M, &need), "mnb_workspace_bytes");
-  if (need == 0) return nullptr;
-  std::lock_guard<std::mutex> lock(mu_);
-  if (need > work_bytes_) {
-    if (work_ != nullptr) (void)hipFree(work_);
-    work_ = nullptr;
-    work_bytes_ = 0;
-    if (hipMalloc(&work_, need) != hipSuccess) Fail("workspace allocation failed");
-    work_bytes_ = need;
-  }
-  return work_;
-}
-
-void MatMulNBitsKernel::EnsurePlan(const TensorView &b, const TensorView &scales,
-                                   const TensorView *zero_points) {
-  std::lock_guard<std::mutex> lock(mu_);
+const mnb_plan *MatMulNBitsKernel::Plan(const TensorView &b, const TensorView &scales,
+                                        const TensorView *zero_points) {
   const void *z = zero_points ? zero_points->data : nullptr;
-  if (plan_ != nullptr && plan_b_ == b.data && plan_s_ == scales.data && plan_z_ == z) return;
-  if (plan_ != nullptr) {
-    mnb_plan_destroy(plan_);
-    plan_ = nullptr;
-  }
+  const auto key = std::make_tuple(static_cast<const void *>(b.data),
+                                   static_cast<const void *>(scales.data), z);
+  std::lock_guard<std::mutex> lock(mu_);
+  auto it = plans_.find(key);
+  if (it != plans_.end()) return it->second;
   mnb_desc d = desc_;
   d.has_zero_points = zero_points != nullptr;
   mnb_plan *p = nullptr;
@@ -91,15 +74,20 @@ void MatMulNBitsKernel::EnsurePlan(const TensorView &b, const TensorView &scales
                          static_cast<const uint8_t *>(z), &p);
   }
   CheckStatus(st, "plan creation");
-  plan_ = p;
-  plan_b_ = b.data;
-  plan_s_ = scales.data;
-  plan_z_ = z;
+  plans_.emplace(key, p);
+  return p;
 }
 
-void MatMulNBitsKernel::operator()(const TensorView &a, const TensorView &b,
-                                   const TensorView &scales, const TensorView *zero_points,
-                                   TensorView &y, void *stream, const TensorView *bias) {
+size_t MatMulNBitsKernel::WorkspaceBytes(const TensorView &b, const TensorView &scales,
+                                         const TensorView *zero_points, int64_t M) {
+  size_t need = 0;
+  CheckStatus(mnb_workspace_bytes(Plan(b, scales, zero_points), M, &need), "mnb_workspace_bytes");
+  return need;
+}
+
+void MatMulNBitsKernel::Validate(const TensorView &a, const TensorView &b,
+                                 const TensorView &scales, const TensorView *zero_points,
+                                 const TensorView *bias) const {
   const int64_t K = desc_.K, N = desc_.N, bs = desc_.block_size;
   const int64_t nb = (K + bs - 1) / bs;
   if (a.type != DataType::kFloat) Fail("input A must be float");
@@ -121,12 +109,19 @@ void MatMulNBitsKernel::operator()(const TensorView &a, const TensorView &b,
   if (bias && bias->type != DataType::kFloat) Fail("input bias must be float");
   if (bias && bias->numel() != N) Fail("bias must have N=" + std::to_string(N) + " elements");
   if (bias && bias->device != Device::kGPU) Fail("bias must be in device memory");
-  EnsurePlan(b, scales, zero_points);
+}
+
+void MatMulNBitsKernel::operator()(const TensorView &a, const TensorView &b,
+                                   const TensorView &scales, const TensorView *zero_points,
+                                   TensorView &y, void *stream, void *workspace,
+                                   size_t workspace_bytes, const TensorView *bias) {
+  Validate(a, b, scales, zero_points, bias);
+  const int64_t K = desc_.K;
+  const mnb_plan *plan = Plan(b, scales, zero_points);
   const int64_t M = a.numel() / K;
-  void *work = Workspace(M);
-  CheckStatus(mnb_run_ex(plan_, M, static_cast<const float *>(a.data),
+  CheckStatus(mnb_run_ex(plan, M, static_cast<const float *>(a.data),
                          bias ? static_cast<const float *>(bias->data) : nullptr,
-                         static_cast<float *>(y.data), work, work_bytes_, stream, 0),
+                         static_cast<float *>(y.data), workspace, workspace_bytes, stream, 0),
               "mnb_run_ex");
 }
 
@@ -144,8 +139,12 @@ void MatMulNBitsKernel::Run(RuntimeContext &rt) {
   std::vector<int64_t> shape = a->shape;
   if (shape.empty()) Fail("A must have rank >= 1");
   shape.back() = desc_.N;
+  Validate(*a, *b, *scales, zp, bias);
   TensorView &y = rt.MakeOutputTensor(0, DataType::kFloat, shape);
-  (*this)(*a, *b, *scales, zp, y, rt.stream, bias);
+  const int64_t M = a->numel() / desc_.K;
+  const size_t need = WorkspaceBytes(*b, *scales, zp, M);
+  void *work = rt.Workspace(need);
+  (*this)(*a, *b, *scales, zp, y, rt.stream, work, need, bias);
 }
 
 void RegisterMatMulNBitsKernel() {

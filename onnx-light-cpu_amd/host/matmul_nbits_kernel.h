@@ -11,7 +11,9 @@
 #include "kernel_registration.h"
 #include "mnb.h"
 
+#include <map>
 #include <mutex>
+#include <tuple>
 
 namespace onnx_light_cpu_amd {
 
@@ -24,31 +26,41 @@ public:
   explicit MatMulNBitsKernel(const NodeAttributes &attrs);
   ~MatMulNBitsKernel() override;
 
+  // Reentrant: runs on one kernel object may overlap in time from several
+  // host threads (distinct streams, outputs and workspaces).
   void Run(RuntimeContext &rt) override;
 
   // Y = A * W^T (+ bias) for device tensors. B/scales/zero_points are the
-  // node's constant initializers: the device plan is prepared on first use
-  // and reused while the same buffers are passed. bias (input 5) is fp32 [N]
-  // in device memory, or null.
+  // node's constant initializers: the device plan for a set of constant
+  // buffers is prepared once (on first use, under a lock) and kept, read-only,
+  // until the kernel object is destroyed. bias (input 5) is fp32 [N] in
+  // device memory, or null. The workspace (size: WorkspaceBytes) comes from
+  // the caller; this call allocates no device memory.
   void operator()(const TensorView &a, const TensorView &b, const TensorView &scales,
-                  const TensorView *zero_points, TensorView &y, void *stream,
-                  const TensorView *bias = nullptr);
+                  const TensorView *zero_points, TensorView &y, void *stream, void *workspace,
+                  size_t workspace_bytes, const TensorView *bias = nullptr);
+
+  // Workspace bytes a run of M rows needs with these constants (prepares the
+  // plan if needed).
+  size_t WorkspaceBytes(const TensorView &b, const TensorView &scales,
+                        const TensorView *zero_points, int64_t M);
 
   const mnb_desc &desc() const { return desc_; }
 
 private:
-  void EnsurePlan(const TensorView &b, const TensorView &scales, const TensorView *zero_points);
+  // Input types, shapes and placement against the node's attributes; throws
+  // before any device call.
+  void Validate(const TensorView &a, const TensorView &b, const TensorView &scales,
+                const TensorView *zero_points, const TensorView *bias) const;
 
-  void *Workspace(int64_t M);
+  // The plan of these constant buffers, created once and never destroyed
+  // before the kernel object (a run on another thread may be using it).
+  const mnb_plan *Plan(const TensorView &b, const TensorView &scales,
+                       const TensorView *zero_points);
 
   mnb_desc desc_{};
   std::mutex mu_;
-  void *work_ = nullptr;   // device workspace of the prefill path, grown on demand
-  size_t work_bytes_ = 0;
-  mnb_plan *plan_ = nullptr;
-  const void *plan_b_ = nullptr;
-  const void *plan_s_ = nullptr;
-  const void *plan_z_ = nullptr;
+  std::map<std::tuple<const void *, const void *, const void *>, mnb_plan *> plans_;
 };
 
 } // namespace onnx_light_cpu_amd

@@ -114,50 +114,121 @@ size_t olc_amd_dispatch_keys(char *buf, size_t cap) {
 
 void olc_amd_clear_dispatch_table(void) { ClearDispatchTable(); }
 
-// Runs one node through the dispatch table. Inputs are given as parallel
-// arrays; a NULL input pointer means the optional input is absent. dims holds
-// every input's dimensions back to back. The output is a caller-provided
-// device buffer of output_numel floats.
+} // extern "C"
+
+namespace {
+
+// The RuntimeContext of one run from the C arrays: inputs given as parallel
+// arrays (a NULL input pointer means the optional input is absent; dims holds
+// every input's dimensions back to back), a caller-provided device output of
+// output_numel floats, and a caller-provided device workspace that the
+// context hands out when it is large enough.
+RuntimeContext MakeContext(int n_inputs, void *const *input_ptrs, const int32_t *input_types,
+                           const int32_t *input_devices, const int32_t *input_ranks,
+                           const int64_t *dims, void *output, int64_t output_numel,
+                           void *workspace, size_t workspace_bytes, void *stream) {
+  RuntimeContext rt;
+  rt.stream = stream;
+  const int64_t *d = dims;
+  for (int i = 0; i < n_inputs; ++i) {
+    if (input_ptrs[i] == nullptr) {
+      rt.inputs.emplace_back(std::nullopt);
+      d += input_ranks[i];
+      continue;
+    }
+    TensorView t;
+    t.data = input_ptrs[i];
+    t.type = static_cast<DataType>(input_types[i]);
+    t.device = static_cast<Device>(input_devices[i]);
+    t.shape.assign(d, d + input_ranks[i]);
+    d += input_ranks[i];
+    rt.inputs.emplace_back(std::move(t));
+  }
+  TensorView y;
+  y.data = output;
+  y.type = DataType::kFloat;
+  y.shape = {output_numel};
+  rt.outputs.push_back(y);
+  rt.allocate_workspace = [workspace, workspace_bytes](size_t bytes) -> void * {
+    if (bytes > workspace_bytes)
+      throw std::invalid_argument("onnx_light_cpu_amd::RunNode: workspace of " +
+                                  std::to_string(workspace_bytes) + " bytes, " +
+                                  std::to_string(bytes) + " needed");
+    return workspace;
+  };
+  return rt;
+}
+
+NodeAttributes MakeAttributes(int n_attrs, const char *const *attr_names,
+                              const int64_t *attr_values) {
+  NodeAttributes attrs;
+  for (int i = 0; i < n_attrs; ++i) attrs.ints[attr_names[i]] = attr_values[i];
+  return attrs;
+}
+
+NodeKernelFn Lookup(const char *domain, const char *op_type, int device) {
+  NodeKernelFn fn = LookupKernel(domain ? domain : "", op_type ? op_type : "",
+                                 static_cast<Device>(device));
+  if (!fn)
+    throw std::invalid_argument("onnx_light_cpu_amd::RunNode: no kernel for '" +
+                                NormaliseDomain(domain ? domain : "") + ":" +
+                                (op_type ? op_type : "") + "'");
+  return fn;
+}
+
+} // namespace
+
+extern "C" {
+
+// Runs one node through the dispatch table (a kernel object created for this
+// run). The workspace is a caller device buffer of workspace_bytes (NULL/0
+// when the run needs none).
 int olc_amd_run_node(const char *domain, const char *op_type, int device, int n_attrs,
                      const char *const *attr_names, const int64_t *attr_values, int n_inputs,
                      void *const *input_ptrs, const int32_t *input_types,
                      const int32_t *input_devices, const int32_t *input_ranks,
-                     const int64_t *dims, void *output, int64_t output_numel, void *stream) {
+                     const int64_t *dims, void *output, int64_t output_numel, void *workspace,
+                     size_t workspace_bytes, void *stream) {
   return Guard([&] {
-    NodeKernelFn fn = LookupKernel(domain ? domain : "", op_type ? op_type : "",
-                                   static_cast<Device>(device));
-    if (!fn)
-      throw std::invalid_argument("onnx_light_cpu_amd::RunNode: no kernel for '" +
-                                  NormaliseDomain(domain ? domain : "") + ":" +
-                                  (op_type ? op_type : "") + "'");
-    NodeAttributes attrs;
-    for (int i = 0; i < n_attrs; ++i) attrs.ints[attr_names[i]] = attr_values[i];
-    RuntimeContext rt;
-    rt.stream = stream;
-    const int64_t *d = dims;
-    for (int i = 0; i < n_inputs; ++i) {
-      if (input_ptrs[i] == nullptr) {
-        rt.inputs.emplace_back(std::nullopt);
-        d += input_ranks[i];
-        continue;
-      }
-      TensorView t;
-      t.data = input_ptrs[i];
-      t.type = static_cast<DataType>(input_types[i]);
-      t.device = static_cast<Device>(input_devices[i]);
-      t.shape.assign(d, d + input_ranks[i]);
-      d += input_ranks[i];
-      rt.inputs.emplace_back(std::move(t));
-    }
-    TensorView y;
-    y.data = output;
-    y.type = DataType::kFloat;
-    y.shape = {output_numel};
-    rt.outputs.push_back(y);
-    std::unique_ptr<KernelBase> kernel = fn(attrs, rt);
+    NodeKernelFn fn = Lookup(domain, op_type, device);
+    RuntimeContext rt = MakeContext(n_inputs, input_ptrs, input_types, input_devices,
+                                    input_ranks, dims, output, output_numel, workspace,
+                                    workspace_bytes, stream);
+    std::unique_ptr<KernelBase> kernel = fn(MakeAttributes(n_attrs, attr_names, attr_values), rt);
     kernel->Run(rt);
   });
 }
+
+// One kernel object kept across runs, as a session keeps a node's kernel:
+// created from the dispatch table once, run any number of times (also from
+// several threads at once, each with its own stream, output and workspace),
+// destroyed once. Returns NULL on failure (message in olc_amd_last_error).
+void *olc_amd_kernel_create(const char *domain, const char *op_type, int device, int n_attrs,
+                            const char *const *attr_names, const int64_t *attr_values) {
+  KernelBase *out = nullptr;
+  const int rc = Guard([&] {
+    NodeKernelFn fn = Lookup(domain, op_type, device);
+    RuntimeContext rt;
+    out = fn(MakeAttributes(n_attrs, attr_names, attr_values), rt).release();
+  });
+  return rc == 0 ? out : nullptr;
+}
+
+int olc_amd_kernel_run(void *kernel, int n_inputs, void *const *input_ptrs,
+                       const int32_t *input_types, const int32_t *input_devices,
+                       const int32_t *input_ranks, const int64_t *dims, void *output,
+                       int64_t output_numel, void *workspace, size_t workspace_bytes,
+                       void *stream) {
+  return Guard([&] {
+    if (kernel == nullptr) throw std::invalid_argument("onnx_light_cpu_amd::RunNode: null kernel");
+    RuntimeContext rt = MakeContext(n_inputs, input_ptrs, input_types, input_devices,
+                                    input_ranks, dims, output, output_numel, workspace,
+                                    workspace_bytes, stream);
+    static_cast<KernelBase *>(kernel)->Run(rt);
+  });
+}
+
+void olc_amd_kernel_destroy(void *kernel) { delete static_cast<KernelBase *>(kernel); }
 
 // DequantizeLinearToMatMulNBits for the Python mirror: x is INT4 (x_type 22)
 // or UINT4 (21) [K, N], x_scale fp32 with scale_rank dims, x_zero_point of

@@ -1,7 +1,8 @@
 """The operator adapter end to end on the GPU: a MatMulNBits node dispatched
 through the registration table (MatMulNBitsKernel::Run -> C ABI -> HIP) gives
-the same bits as the direct C ABI call, records its usage, and keeps working
-when the constant inputs change."""
+the same bits as the direct C ABI call, records its usage, and takes its
+workspace from the runtime's allocator (a run that needs one fails without
+it)."""
 import numpy as np
 import pytest
 
@@ -32,11 +33,17 @@ def test_node_matches_direct_call(pkg, orc, cuda, K, N, bs, zp, M):
     pkg.clear_used_kernel_names()
     y_node = torch.empty(M, N, device=cuda)
     attrs = {"K": K, "N": N, "bits": 4, "block_size": bs, "accuracy_level": 0}
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare_device(dB, dS, dZ)
+    work = torch.empty(max(1, op.workspace_bytes(M)), dtype=torch.uint8, device=cuda)
     pkg.run_node("com.microsoft", "MatMulNBits", attrs, _node_inputs(pkg, dA, dB, dS, dZ), y_node,
-                 stream=torch.cuda.current_stream().cuda_stream)
+                 stream=torch.cuda.current_stream().cuda_stream, workspace=work)
     torch.cuda.synchronize()
     assert pkg.used_kernel_names() == ["onnx_light_cpu_amd::MatMulNBitsKernel"]
-    op = pkg.MatMulNBits(K, N, 4, bs).prepare_device(dB, dS, dZ)
+    if op.workspace_bytes(M) > 0:
+        # the runtime's workspace allocator must supply the scratch; the kernel allocates none
+        with pytest.raises(ValueError, match="workspace of 0 bytes"):
+            pkg.run_node("com.microsoft", "MatMulNBits", attrs, _node_inputs(pkg, dA, dB, dS, dZ),
+                         y_node, stream=torch.cuda.current_stream().cuda_stream)
     y_direct = op(dA)
     torch.cuda.synchronize()
     assert torch.equal(y_node.cpu(), y_direct.cpu())

@@ -89,9 +89,10 @@ def test_bias_through_the_adapter(pkg, cuda):
     pkg.register_kernels()
     y_node = torch.empty(M, N, device=cuda)
     attrs = {"K": K, "N": N, "bits": 4, "block_size": bs}
-    pkg.run_node("com.microsoft", "MatMulNBits", attrs, inputs, y_node,
-                 stream=torch.cuda.current_stream().cuda_stream)
     op = pkg.MatMulNBits(K, N, 4, bs).prepare_device(dB, dS, dZ)
+    work = torch.empty(max(1, op.workspace_bytes(M)), dtype=torch.uint8, device=cuda)
+    pkg.run_node("com.microsoft", "MatMulNBits", attrs, inputs, y_node,
+                 stream=torch.cuda.current_stream().cuda_stream, workspace=work)
     y_direct = op(dA, bias=bias)
     torch.cuda.synchronize()
     assert torch.equal(y_node.cpu(), y_direct.cpu())
