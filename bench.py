@@ -133,20 +133,6 @@ def copy_leg(torch, dev, steps, warmup, stream):
             "GBps": 2 * n / (ms * 1e-3) / 1e9, "wall_s": wall}
 
 
-def decode_kernel(M, p):
-    """Kernel mnb_run's decode path launches for M rows of projection p when
-    the shape qualifies (K a multiple of 512, block_size >= 32, a workspace
-    given; true for c1..c3): the exact-product MFMA kernel and its ordered
-    partial-sum pass from M = 5, or from M = 4 when N >= 3K and M = 3 when
-    N >= 6K (the library's measured crossover); fp32-FMA kernels below."""
-    first_mfma = 3 if p.N >= 6 * p.K else (4 if p.N >= 3 * p.K else 5)
-    if M == 1:
-        return "GemvM1Kernel"
-    if M < first_mfma:
-        return "GemvSmallMKernel"
-    return "GemvMfmaKernel + SumPartialsKernel"
-
-
 def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
     """One decode shape over >= 1 GiB of rotated weight copies."""
     rot = max(2, -(-ROTATION_BYTES // p.weight_bytes()))
@@ -157,6 +143,7 @@ def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
     A = (torch.randn((M, p.K), device=dev, generator=g) * p.a_sigma).contiguous()
     Y = torch.empty((M, p.N), device=dev)
     path = ops[0].select_path(M)
+    kernel = ops[0].kernel_name(M)
 
     def launches():
         for op in ops:
@@ -171,7 +158,7 @@ def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
     torch.cuda.empty_cache()
     return {
         "K": p.K, "N": p.N, "M": M, "block_size": p.block_size,
-        "zero_points": p.has_zero_points, "path": path, "kernel": decode_kernel(M, p),
+        "zero_points": p.has_zero_points, "path": path, "kernel": kernel,
         "rotation_copies": rot,
         "us_per_launch": per_launch_us, "bytes_per_launch": nbytes,
         "GBps": nbytes / (per_launch_us * 1e-6) / 1e9, "ms_per_step": ms, "wall_s": wall,

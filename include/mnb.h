@@ -194,6 +194,39 @@ int mnb_run_no_alloc(const mnb_plan *plan, int64_t M, const float *dA, float *dY
  * automatic GEMM path reports 2 whichever GEMM kernel serves). */
 int mnb_select_path(const mnb_plan *plan, int64_t M, int *path);
 
+/* Kernels a run can launch, for mnb_kernel_name and mnb_run_kernel. */
+#define MNB_KERNEL_GEMV_M1 1      /* GemvM1Kernel: M = 1, fp32 mixed FMA */
+#define MNB_KERNEL_GEMV_SMALL_M 2 /* GemvSmallMKernel: 2 <= M <= 16, fp32 FMA */
+#define MNB_KERNEL_GEMV_MFMA 3    /* GemvMfmaKernel: 2 <= M <= 16, exact-product MFMA, original layout */
+#define MNB_KERNEL_DECODE_FRAG 4  /* DecodeFragKernel: 2 <= M <= 16, exact-product MFMA, fragment-ordered copy */
+#define MNB_KERNEL_GEMM 5         /* GemmKernel: fp16 MFMA, BM x 128 tiles, original layout */
+#define MNB_KERNEL_PREFILL 6      /* PrefillKernel: fp16 MFMA, 128 x 256 tiles, fragment-ordered copy */
+#define MNB_KERNEL_GEMV 7         /* GemvKernel: fp32 FMA fallback, M <= 16 */
+#define MNB_KERNEL_GENERIC 8      /* GenericKernel: any shape, one wavefront per output */
+
+/* Name of the main kernel mnb_run launches for M rows given workspace_bytes
+ * of workspace ("GemvM1Kernel", "DecodeFragKernel", "PrefillKernel", ...;
+ * "" for M == 0 or a bad plan). Static storage. The counterpart of the
+ * reference's record of the kernels a run dispatched to
+ * (onnx_light_cpu/_register.py:157-170, used_kernel_names), answered before
+ * the run. */
+const char *mnb_kernel_name(const mnb_plan *plan, int64_t M, size_t workspace_bytes);
+
+/* Tuning and cross-checks: one run of M rows with the named kernel (one of
+ * MNB_KERNEL_*) and launch shape p0, p1 (0 picks each): GEMV_M1 (band rows,
+ * rows per wavefront), GEMV_SMALL_M (tokens per launch, wavefronts per
+ * workgroup), GEMV_MFMA (16-row blocks per item, workgroups per CU),
+ * DECODE_FRAG (wavefronts per workgroup, 256-k units per wavefront), GEMM
+ * (tile height 32, 64 or 128; K splits), PREFILL (K splits); GEMV and
+ * GENERIC take none. Plain (not gate/up) plans, no bias; MNB_ERR_UNSUPPORTED
+ * when the kernel cannot serve the plan or M, MNB_ERR_WORKSPACE below
+ * mnb_kernel_workspace_bytes. No counterpart in the reference, whose
+ * kernels are chosen inside the plan. */
+int mnb_kernel_workspace_bytes(const mnb_plan *plan, int64_t M, int kernel, int p0, int p1,
+                               size_t *bytes);
+int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
+                   size_t workspace_bytes, void *stream, int kernel, int p0, int p1);
+
 /* Text for a status code (static storage). */
 const char *mnb_status_str(int status);
 

@@ -35,6 +35,9 @@ STATUS = {
     8: "MNB_ERR_ALLOC",
 }
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GENERIC, PATH_EXACT, PATH_PREFILL = 0, 1, 2, 3, 4, 5
+# MNB_KERNEL_* of include/mnb.h (mnb_run_kernel)
+(KERNEL_GEMV_M1, KERNEL_GEMV_SMALL_M, KERNEL_GEMV_MFMA, KERNEL_DECODE_FRAG, KERNEL_GEMM,
+ KERNEL_PREFILL, KERNEL_GEMV, KERNEL_GENERIC) = range(1, 9)
 
 
 class MnbDesc(ctypes.Structure):
@@ -76,11 +79,18 @@ def library():
         L.mnb_last_error.restype = ctypes.c_char_p
         L.mnb_weight_bytes.argtypes = [ctypes.POINTER(MnbDesc), ctypes.POINTER(sz)]
         L.mnb_version.restype = ctypes.c_char_p
+        L.mnb_kernel_name.argtypes = [vp, i64, sz]
+        L.mnb_kernel_name.restype = ctypes.c_char_p
+        L.mnb_kernel_workspace_bytes.argtypes = [vp, i64, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_int, ctypes.POINTER(sz)]
+        L.mnb_run_kernel.argtypes = [vp, i64, vp, vp, vp, sz, vp, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int]
         for name in ("mnb_plan_create", "mnb_plan_create_device", "mnb_plan_destroy",
                      "mnb_workspace_bytes", "mnb_run", "mnb_run_path", "mnb_select_path",
                      "mnb_weight_bytes", "mnb_run_ex", "mnb_qdq_repack",
                      "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes",
-                     "mnb_run_rmsnorm", "mnb_run_no_alloc"):
+                     "mnb_run_rmsnorm", "mnb_run_no_alloc", "mnb_kernel_workspace_bytes",
+                     "mnb_run_kernel"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib
@@ -136,6 +146,7 @@ class MatMulNBits:
         self._plan = ctypes.c_void_p()
         self._keep = ()
         self._work = None
+        self._kwork = None
 
     # -- constants ---------------------------------------------------------
     def prepare(self, B, scales, zero_points=None):
@@ -257,6 +268,35 @@ class MatMulNBits:
                                          _dev_ptr(out), _dev_ptr(self._work), self._work.numel(),
                                          ctypes.c_void_p(s.cuda_stream)),
                "run_rmsnorm")
+        return out
+
+    def kernel_name(self, M: int, workspace_bytes=None) -> str:
+        """The main kernel a run of M rows launches, with workspace_bytes of
+        workspace (default: what workspace_bytes(M) asks for)."""
+        n = self.workspace_bytes(M) if workspace_bytes is None else workspace_bytes
+        return library().mnb_kernel_name(self._plan, M, n).decode()
+
+    def run_kernel(self, A, kernel: int, p0: int = 0, p1: int = 0, out=None, stream=None):
+        """One run with a chosen kernel and launch shape (mnb_run_kernel: tuning
+        and cross-checks; plain plans, no bias)."""
+        import torch
+        A2 = A.reshape(-1, self.desc.K).contiguous()
+        M = A2.shape[0]
+        if out is None:
+            out = torch.empty(M, self.desc.N, device=A.device, dtype=torch.float32)
+        n = ctypes.c_size_t()
+        _check(library().mnb_kernel_workspace_bytes(self._plan, M, kernel, p0, p1,
+                                                    ctypes.byref(n)), "kernel workspace")
+        work = None
+        if n.value > 0:
+            if self._kwork is None or self._kwork.numel() < n.value or self._kwork.device != A.device:
+                self._kwork = torch.empty(n.value, dtype=torch.uint8, device=A.device)
+            work = self._kwork
+        s = stream if stream is not None else torch.cuda.current_stream(A.device)
+        _check(library().mnb_run_kernel(self._plan, M, _dev_ptr(A2), _dev_ptr(out), _dev_ptr(work),
+                                        0 if work is None else work.numel(),
+                                        ctypes.c_void_p(s.cuda_stream), kernel, p0, p1),
+               "run_kernel")
         return out
 
     def workspace_bytes(self, M: int) -> int:

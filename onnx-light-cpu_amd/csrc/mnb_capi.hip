@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -29,6 +30,8 @@ struct mnb_plan {
   int32_t *dColExp;  // always plan-owned: per weight row power-of-two scale exponent
   uint8_t *dBp;      // plan-owned prefill layout of the weights (nullptr: shape not served)
   uint8_t *dSp;
+  float *dSd;        // plan-owned decode layout of the block scales (nullptr: not served)
+  uint32_t *dZd;     // and of the zero points (nullptr without zero points)
 };
 
 namespace {
@@ -103,6 +106,8 @@ void FillView(mnb_plan *p) {
   p->view.col_exp = p->dColExp;
   p->view.Bp = p->dBp;
   p->view.Sp = p->dSp;
+  p->view.Sd = p->dSd;
+  p->view.Zd = p->dZd;
   p->view.K = p->desc.K;
   p->view.N = p->desc.N;
   p->view.nb = nb;
@@ -122,6 +127,10 @@ void FreePlanMemory(mnb_plan *p) {
   if (p->dColExp) (void)hipFree(p->dColExp);
   if (p->dBp) (void)hipFree(p->dBp);
   if (p->dSp) (void)hipFree(p->dSp);
+  if (p->dSd) (void)hipFree(p->dSd);
+  if (p->dZd) (void)hipFree(p->dZd);
+  p->dSd = nullptr;
+  p->dZd = nullptr;
   p->dB = nullptr;
   p->dS = nullptr;
   p->dZ = nullptr;
@@ -166,6 +175,25 @@ int DerivePlanConstants(mnb_plan *p) {
       return MNB_ERR_HIP;
     }
     FillView(p);
+    // The small-M decode kernel reads the same fragment-ordered weights with
+    // fp32 block scales and zero points re-laid per 64-row group.
+    if (mnb::DecodeFragLayoutWanted(p->view)) {
+      size_t zd_bytes = 0;
+      const size_t sd_bytes = mnb::DecodeFragScaleBytes(p->view, &zd_bytes);
+      e = hipMalloc(reinterpret_cast<void **>(&p->dSd), sd_bytes);
+      if (e == hipSuccess && zd_bytes > 0) e = hipMalloc(reinterpret_cast<void **>(&p->dZd), zd_bytes);
+      if (e != hipSuccess) {
+        SetLastError("hipMalloc", e);
+        return MNB_ERR_ALLOC;
+      }
+      e = mnb::LaunchDecodeFragRelayout(p->view, p->dSd, p->dZd, nullptr);
+      if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+      if (e != hipSuccess) {
+        SetLastError("decode re-layout", e);
+        return MNB_ERR_HIP;
+      }
+      FillView(p);
+    }
   }
   return MNB_OK;
 }
@@ -478,8 +506,10 @@ int mnb_plan_destroy(mnb_plan *plan) {
   return MNB_OK;
 }
 
-// Rows from which the decode path multiplies on MFMA (when the caller passes
-// the workspace): below it the fp32-FMA kernels are faster, their cost
+// Rows from which the decode path multiplies on the original-layout MFMA
+// kernel (GemvMfmaKernel), for plans without the fragment-ordered weight copy
+// (N % 4 != 0 or N >= 2^22; when the caller passes the workspace): below it
+// the fp32-FMA kernels are faster, their cost
 // growing by about one M = 1 pass per token while the MFMA kernel's barely
 // changes with M. Where the MFMA kernel starts ahead depends on the shape: it
 // splits K into 512-k ranges, so wide, short weights (N large against K) give
@@ -499,6 +529,31 @@ static bool UsesMfmaDecode(const mnb_plan *plan, int64_t M) {
   return M >= MfmaDecodeMinRows(plan->view) && M <= 16 && mnb::GemvMfmaSupports(plan->view, M);
 }
 
+// Rows from which plans holding the fragment-ordered weights (and their
+// decode scales) take DecodeFragKernel, when the caller passes its
+// workspace; the fp32-FMA kernels serve fewer. DecodeFragKernel's cost barely
+// changes with M (its pre-pass and, for long K, its partial-sum pass add a
+// fixed few us), the FMA kernel's grows by about one M = 1 pass per token.
+// Measured on MI355X (c1-c5 shapes, HIP-graph replay, us, FMA against
+// DecodeFragKernel): M = 2 c2 13.4 / 14.4, c5 gate+up 23.3 / 22.7, the others
+// 5.3-12.7 against 10.0-18.7; M = 4 c2 20.2 / 13.6, gate+up 32.5 / 22.3, c1
+// 7.3 / 10.3, c5 qkv 10.9 / 11.8, c3 18.2 / 18.4; from M = 5 it is ahead
+// of both the FMA and the original-layout MFMA kernel everywhere except c5
+// qkv (5-7% behind the latter).
+static int64_t FragDecodeMinRows(const mnb::WeightView &w) {
+  if (w.N >= 6 * w.K) return 2;
+  if (w.N >= 3 * w.K) return 3;
+  return 5;
+}
+
+static bool UsesFragDecode(const mnb_plan *plan, int64_t M) {
+  return M >= FragDecodeMinRows(plan->view) && mnb::DecodeFragSupports(plan->view, M);
+}
+
+// The decode kernel path 1 launches for M rows with `work_bytes` of workspace
+// at `work` (M <= 16).
+enum DecodeKernel { kDecM1, kDecFrag, kDecMfma, kDecSmallM, kDecGemv };
+
 // Rows per launch of the exact route (path 4): the decode kernels' limit.
 constexpr int64_t kExactGroupRows = 16;
 
@@ -506,6 +561,20 @@ static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
   return need == 0 ||
          (work != nullptr && bytes >= need && (reinterpret_cast<uintptr_t>(work) % 16) == 0);
 }
+
+// Without the kernel's workspace, M >= 2 falls back to the fp32-FMA kernels.
+static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void *work,
+                                     size_t work_bytes) {
+  if (M == 1 && mnb::GemvM1Supports(plan->view)) return kDecM1;
+  if (UsesFragDecode(plan, M) &&
+      HasWorkspace(work, work_bytes, mnb::DecodeFragWorkspaceBytes(plan->view, M)))
+    return kDecFrag;
+  if (!mnb::DecodeFragSupports(plan->view, M) && UsesMfmaDecode(plan, M) &&
+      HasWorkspace(work, work_bytes, mnb::GemvMfmaWorkspaceBytes(plan->view, M)))
+    return kDecMfma;
+  return mnb::GemvSmallMSupports(plan->view, M) ? kDecSmallM : kDecGemv;
+}
+
 
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
   if (plan == nullptr || bytes == nullptr) return MNB_ERR_NULL_POINTER;
@@ -519,7 +588,10 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
   size_t need = 0;
   if (M > 0 && mnb::GemmSupports(plan->view, M)) need = mnb::GemmWorkspaceBytes(plan->view, M);
   const int64_t md = std::min<int64_t>(M, kExactGroupRows);
-  if (UsesMfmaDecode(plan, md)) need = std::max(need, mnb::GemvMfmaWorkspaceBytes(plan->view, md));
+  if (UsesFragDecode(plan, md))
+    need = std::max(need, mnb::DecodeFragWorkspaceBytes(plan->view, md));
+  else if (!mnb::DecodeFragSupports(plan->view, md) && UsesMfmaDecode(plan, md))
+    need = std::max(need, mnb::GemvMfmaWorkspaceBytes(plan->view, md));
   *bytes = need + GateUpScratchBytes(plan, M);
   return MNB_OK;
 }
@@ -616,7 +688,8 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   bool fused = false, bias_done = false;
   switch (path) {
   case 1:
-    if (M == 1 && mnb::GemvM1Supports(plan->view)) {
+    switch (PickDecodeKernel(plan, M, work, work_bytes)) {
+    case kDecM1:
       e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0, H, gamma, eps);
       fused = true;
       if (e == hipErrorInvalidValue && H != nullptr) {
@@ -624,14 +697,17 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
         e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0, nullptr, gamma, eps);
         fused = false;
       }
-    } else if (UsesMfmaDecode(plan, M) &&
-               HasWorkspace(work, work_bytes, mnb::GemvMfmaWorkspaceBytes(plan->view, M))) {
+      break;
+    case kDecFrag:
+      e = mnb::LaunchDecodeFrag(plan->view, M, dA, Ys, work, s, H);
+      fused = true;
+      break;
+    case kDecMfma:
       e = mnb::LaunchGemvMfma(plan->view, M, dA, Ys, work, s, H);
       fused = true;
-    } else if (mnb::GemvSmallMSupports(plan->view, M)) {
-      e = mnb::LaunchGemvSmallM(plan->view, M, dA, Ys, s);
-    } else {
-      e = mnb::LaunchGemv(plan->view, M, dA, Ys, s);
+      break;
+    case kDecSmallM: e = mnb::LaunchGemvSmallM(plan->view, M, dA, Ys, s); break;
+    default: e = mnb::LaunchGemv(plan->view, M, dA, Ys, s); break;
     }
     break;
   case 2:
@@ -717,6 +793,124 @@ int mnb_run_path(const mnb_plan *plan, int64_t M, const float *dA, float *dY, vo
 int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
             size_t workspace_bytes, void *stream) {
   return mnb_run_ex(plan, M, dA, nullptr, dY, dWorkspace, workspace_bytes, stream, 0);
+}
+
+const char *mnb_kernel_name(const mnb_plan *plan, int64_t M, size_t workspace_bytes) {
+  if (plan == nullptr || M <= 0 || M > (int64_t{1} << 30)) return "";
+  // The workspace's address only matters through its alignment here.
+  const void *work = workspace_bytes > 0 ? reinterpret_cast<const void *>(uintptr_t{256}) : nullptr;
+  size_t work_bytes = workspace_bytes;
+  const size_t scratch = GateUpScratchBytes(plan, M);
+  if (scratch > 0) {
+    if (workspace_bytes < scratch) return "";
+    work_bytes -= scratch;
+  }
+  switch (SelectPath(plan, M, reinterpret_cast<const float *>(uintptr_t{256}))) {
+  case 1:
+    switch (PickDecodeKernel(plan, M, work, work_bytes)) {
+    case kDecM1: return "GemvM1Kernel";
+    case kDecFrag: return "DecodeFragKernel";
+    case kDecMfma: return "GemvMfmaKernel";
+    case kDecSmallM: return "GemvSmallMKernel";
+    default: return "GemvKernel";
+    }
+  case 2: return mnb::GemmUsesPrefill(plan->view, M) ? "PrefillKernel" : "GemmKernel";
+  case 4: return "exact groups of 16 rows";
+  default: return "GenericKernel";
+  }
+}
+
+int mnb_kernel_workspace_bytes(const mnb_plan *plan, int64_t M, int kernel, int p0, int p1,
+                               size_t *bytes) {
+  if (plan == nullptr || bytes == nullptr) return MNB_ERR_NULL_POINTER;
+  if (M < 1 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
+  const mnb::WeightView &w = plan->view;
+  switch (kernel) {
+  case MNB_KERNEL_GEMV_MFMA:
+    *bytes = mnb::GemvMfmaWorkspaceBytes(w, M);
+    return MNB_OK;
+  case MNB_KERNEL_DECODE_FRAG:
+    *bytes = mnb::DecodeFragWorkspaceBytes(w, M, p0, p1);
+    return MNB_OK;
+  case MNB_KERNEL_GEMM:
+    *bytes = p0 > 0 ? mnb::GemmShapeWorkspaceBytes(w, M, std::max(1, p1))
+                    : mnb::GemmWorkspaceBytes(w, M);
+    return MNB_OK;
+  case MNB_KERNEL_PREFILL:
+    *bytes = mnb::GemmShapeWorkspaceBytes(w, M, std::max(1, p0));
+    if (p0 <= 0) *bytes = std::max(*bytes, mnb::GemmWorkspaceBytes(w, M));
+    return MNB_OK;
+  case MNB_KERNEL_GEMV_M1:
+  case MNB_KERNEL_GEMV_SMALL_M:
+  case MNB_KERNEL_GEMV:
+  case MNB_KERNEL_GENERIC:
+    *bytes = 0;
+    return MNB_OK;
+  default: return MNB_ERR_UNSUPPORTED;
+  }
+}
+
+int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
+                   size_t workspace_bytes, void *stream, int kernel, int p0, int p1) {
+  if (plan == nullptr) return MNB_ERR_NULL_POINTER;
+  if (M < 1 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
+  if (dA == nullptr || dY == nullptr) return MNB_ERR_NULL_POINTER;
+  if (plan->gate_up || p0 < 0 || p1 < 0) return MNB_ERR_UNSUPPORTED;
+  auto one_of = [](int v, std::initializer_list<int> ok) {
+    return std::find(ok.begin(), ok.end(), v) != ok.end();
+  };
+  bool shape_ok = true;
+  switch (kernel) {
+  case MNB_KERNEL_GEMV_M1: shape_ok = p0 <= 1024 && one_of(p1, {0, 1, 2, 4, 8}); break;
+  case MNB_KERNEL_GEMV_SMALL_M: shape_ok = p0 <= 8 && one_of(p1, {0, 4, 8}); break;
+  case MNB_KERNEL_GEMV_MFMA: shape_ok = p0 <= 2 && p1 <= 8; break;
+  case MNB_KERNEL_DECODE_FRAG: shape_ok = one_of(p0, {0, 1, 2, 4, 8}) && p1 <= 2; break;
+  case MNB_KERNEL_GEMM: shape_ok = one_of(p0, {0, 32, 64, 128}) && p1 <= 16; break;
+  case MNB_KERNEL_PREFILL: shape_ok = p0 <= 16 && p1 == 0; break;
+  default: shape_ok = p0 == 0 && p1 == 0; break;
+  }
+  if (!shape_ok) return MNB_ERR_UNSUPPORTED;
+  size_t need = 0;
+  int st = mnb_kernel_workspace_bytes(plan, M, kernel, p0, p1, &need);
+  if (st != MNB_OK) return st;
+  if (!HasWorkspace(dWorkspace, workspace_bytes, need)) return MNB_ERR_WORKSPACE;
+  const mnb::WeightView &w = plan->view;
+  const bool a_aligned = (reinterpret_cast<uintptr_t>(dA) % 16) == 0;
+  bool ok = false;
+  switch (kernel) {
+  case MNB_KERNEL_GEMV_M1: ok = M == 1 && a_aligned && mnb::GemvM1Supports(w); break;
+  case MNB_KERNEL_GEMV_SMALL_M: ok = M >= 2 && a_aligned && mnb::GemvSmallMSupports(w, M); break;
+  case MNB_KERNEL_GEMV_MFMA: ok = a_aligned && mnb::GemvMfmaSupports(w, M); break;
+  case MNB_KERNEL_DECODE_FRAG: ok = a_aligned && mnb::DecodeFragSupports(w, M); break;
+  case MNB_KERNEL_GEMM: ok = a_aligned && mnb::GemmSupports(w, M); break;
+  case MNB_KERNEL_PREFILL: ok = a_aligned && mnb::PrefillSupports(w, M); break;
+  case MNB_KERNEL_GEMV: ok = M <= 16 && a_aligned && mnb::GemvSupports(w, M); break;
+  case MNB_KERNEL_GENERIC: ok = true; break;
+  default: ok = false; break;
+  }
+  if (!ok) return MNB_ERR_UNSUPPORTED;
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur != plan->device) return MNB_ERR_NO_DEVICE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = hipSuccess;
+  switch (kernel) {
+  case MNB_KERNEL_GEMV_M1: e = mnb::LaunchGemvM1(w, dA, dY, s, p0, p1); break;
+  case MNB_KERNEL_GEMV_SMALL_M: e = mnb::LaunchGemvSmallMShape(w, M, dA, dY, s, p0, p1, 0); break;
+  case MNB_KERNEL_GEMV_MFMA: e = mnb::LaunchGemvMfmaShape(w, M, dA, dY, dWorkspace, s, p0, p1); break;
+  case MNB_KERNEL_DECODE_FRAG: e = mnb::LaunchDecodeFrag(w, M, dA, dY, dWorkspace, s, nullptr, p0, p1); break;
+  case MNB_KERNEL_GEMM: e = mnb::LaunchGemmShape(w, M, dA, dY, dWorkspace, s, p0, std::max(1, p1)); break;
+  case MNB_KERNEL_PREFILL:
+    e = p0 > 0 ? mnb::LaunchGemmShape(w, M, dA, dY, dWorkspace, s, mnb::kPrefillTileCode, p0)
+               : mnb::LaunchPrefill(w, M, dA, dY, dWorkspace, s);
+    break;
+  case MNB_KERNEL_GEMV: e = mnb::LaunchGemv(w, M, dA, dY, s); break;
+  default: e = mnb::LaunchGeneric(w, M, dA, dY, s); break;
+  }
+  if (e != hipSuccess) {
+    SetLastError("kernel launch", e);
+    return e == hipErrorInvalidValue ? MNB_ERR_UNSUPPORTED : MNB_ERR_HIP;
+  }
+  return MNB_OK;
 }
 
 int mnb_run_no_alloc(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *stream) {

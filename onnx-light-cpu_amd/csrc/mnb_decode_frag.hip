@@ -1,0 +1,462 @@
+// Decode GEMV for 2 <= M <= 16 activation rows on fp16 MFMA with 22-bit
+// activations and fp32 sums, streaming the plan's fragment-ordered weights.
+//
+// Role in the reference: the roadmap's `int4_gemv` / `int4_small_m` decode
+// side (docs/next_steps/2026/2026_08_qwen3_inference.rst:208-221: each
+// weight byte streamed once, unpacked blocks reused across the batch rows);
+// the fp32 semantics are those of the reference engine's skinny-M product
+// (onnx_light_cpu/impl/math/gemm_kernel.cc:1208-1258): q - zp is exact, each
+// activation keeps 22 significant bits (relative error at most 2^-22, against
+// fp32's 2^-24 rounding of each product) and the products are summed in fp32.
+//
+// Two kernels per call:
+//
+// 1. SplitActKernel (one workgroup per unit of 256 k) scales each token's
+//    values in the unit by a power of two 2^e (largest magnitude in
+//    [2^14, 2^15); exact) and splits every scaled value into two fp16 terms,
+//    a 2^e ~ a0 + a1 with a0 = fp16(a 2^e) and a1 = fp16(a 2^e - a0) (the
+//    difference is exact in fp32; 2 x 11 significand bits, so |a 2^e - a0 -
+//    a1| <= 2^-22 |a 2^e|, and below 2^-39 of the unit's largest magnitude
+//    for values under fp16's normal range), written to the workspace as the
+//    MFMA operand image [unit][step][term][lane] (16 bytes per lane: token
+//    lane & 15, 8 k of quarter lane >> 4, in the weight decode's
+//    [0,4,1,5,2,6,3,7] order) plus e per (unit, token). Tokens past M are
+//    zero.
+//
+// 2. DecodeFragKernel. The plan's prefill weight copy Bp holds, for each
+//    group g of 64 weight rows and 32-k step s, a 1 KiB record whose lane l
+//    holds the packed words of rows 64 g + 16 j + (l & 15), j = 0..3, at
+//    k = 32 s + 8 (l >> 4): the MFMA B operands of four 16-row slices. A
+//    unit (8 steps) of one group is therefore 8 KiB of contiguous weights,
+//    read with 16-byte loads that cover 1 KiB per wavefront instruction
+//    (measured on MI355X: such records stream the c2 and c3 weights in
+//    6.1 us against 7.9-8.6 us for 64-byte pieces of 16 rows). A third
+//    activation term (exact products) cost 15-25% more time on c1-c3 at
+//    M = 16 for no gain under the decode bound.
+//    - A workgroup of WPG wavefronts owns one group and a run of
+//      WPG * U consecutive units; wavefront w multiplies U of them. Per step
+//      it decodes the record's four words (q - zp exact in fp16, exponent
+//      constants), reads the two activation terms of the step (from L2:
+//      the image is shared by every group) and issues 2 x 4
+//      v_mfma_f32_16x16x32_f16 into one fp32 tile per slice; at each block's
+//      end the tile is multiplied by the rows' fp32 block scales into the
+//      unit's sum, at each unit's end the unit's sum is scaled by 2^-e
+//      (exact) into the wavefront's sum.
+//    - The wavefronts' sums meet in LDS and are added in wavefront order;
+//      a run that does not cover K writes a partial sum, added in run order
+//      by the ordered partial-sum pass. Results do not depend on scheduling.
+//    - Weights, activation terms, block scales and zero points stream
+//      through a rolling window of WIN steps in registers: multiply the
+//      oldest, issue the one WIN further on. Every load is unconditional and
+//      in bounds (rows past N are zero in the re-laid copies).
+//    The MFMA takes the activations as its A operand (rows = tokens) and the
+//    weights as its B operand (columns = weight rows): lane l's value v is
+//    token 4 (l >> 4) + v of weight row 16 j + (l & 15), so a lane's block
+//    scale is its own row's.
+#include "mnb_decode_common.h"
+
+#include <algorithm>
+
+namespace mnb {
+namespace df {
+
+using namespace dec;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kUnitK = 256;            // k per unit: one activation exponent per token
+constexpr int kUnitSteps = kUnitK / 32;
+constexpr int kTok = 16;               // tokens per MFMA tile (M padded)
+constexpr int kMaxWaves = 8;
+constexpr int kTerms = 2;              // fp16 terms per activation
+constexpr int kStepBytes = kTerms * 1024;  // image bytes per 32-k step
+
+__device__ __forceinline__ uint32_t PkAddF16(uint32_t a, uint32_t b) {
+  const half2v r = __builtin_bit_cast(half2v, a) + __builtin_bit_cast(half2v, b);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// 8 nibbles (k order) of one word -> q - zp as fp16 in [0,4,1,5,2,6,3,7]
+// order, exact: (w & 0x000F000F) | 0x6400.. is the fp16 pair 1024 + q of
+// nibbles 0 | 4 (ulp 1 at 1024), (w & 0x00F000F0) | 0x5400.. the pair 64 + q
+// of nibbles 1 | 5 (ulp 1/16 at 64); the same of w >> 8 gives nibbles 2 | 6
+// and 3 | 7. neg_lo / neg_hi are the fp16 pairs -(1024 + zp) / -(64 + zp).
+// The masks sit in VGPRs (v_and_or_b32 takes no literal on gfx9).
+struct Masks {
+  uint32_t lo, hi, e1024, e64;
+};
+__device__ __forceinline__ Masks MakeMasks() {
+  Masks c{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u};
+  __asm__ volatile("" : "+v"(c.lo), "+v"(c.hi), "+v"(c.e1024), "+v"(c.e64));
+  return c;
+}
+__device__ __forceinline__ half8 DecodeQ(uint32_t w, uint32_t neg_lo, uint32_t neg_hi,
+                                         const Masks &c) {
+  const uint32_t w8 = w >> 8;
+  const uint4 r = make_uint4(PkAddF16((w & c.lo) | c.e1024, neg_lo),
+                             PkAddF16((w & c.hi) | c.e64, neg_hi),
+                             PkAddF16((w8 & c.lo) | c.e1024, neg_lo),
+                             PkAddF16((w8 & c.hi) | c.e64, neg_hi));
+  return __builtin_bit_cast(half8, r);
+}
+
+// One workgroup (128 threads) per unit u: thread (t, ch) takes the 32 values
+// k = 256 u + 32 ch .. + 31 of token t. Writes img[((u * 8 + ch) * kTerms +
+// term) * 64 + 16 quarter + t] and exps[u * 16 + t].
+__global__ __launch_bounds__(128) void SplitActKernel(const float *__restrict__ A,
+                                                      uint4 *__restrict__ img,
+                                                      int *__restrict__ exps, int M, int K) {
+  const int u = blockIdx.x;
+  const int t = threadIdx.x >> 3, ch = threadIdx.x & 7;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, M * K * 4, 0x00020000);
+  // tokens past M read past the end of the buffer: zeros
+  const int vo = t < M ? (t * K + kUnitK * u + 32 * ch) * 4 : M * K * 4;
+  floatx4 av[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    av[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo + 16 * i, 0, 0));
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) amax = fmaxf(amax, fabsf(av[i][c]));
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  // The largest magnitude times 2^e in [2^14, 2^15); ldexp is exact for
+  // every e this gives (|e| <= 163), subnormal inputs included. A zero, inf
+  // or NaN maximum gives e = 0 (inf and NaN then propagate).
+  const int e = RangeExponent(amax, 14);
+  if (ch == 0) exps[u * kTok + t] = e;
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {  // 8 values k = 32 ch + 8 qd .. + 7
+    half8 h[kTerms];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int o = (i & 3) * 2 + (i >> 2);  // k order [0,4,1,5,2,6,3,7]
+      const float x = ldexpf(av[2 * qd + (i >> 2)][i & 3], e);
+      const _Float16 h0 = static_cast<_Float16>(x);
+      h[0][o] = h0;
+      h[1][o] = static_cast<_Float16>(__builtin_isfinite(x) ? x - static_cast<float>(h0) : 0.f);
+    }
+#pragma unroll
+    for (int term = 0; term < kTerms; ++term)
+      img[((u * kUnitSteps + ch) * kTerms + term) * 64 + 16 * qd + t] = __builtin_bit_cast(uint4, h[term]);
+  }
+}
+
+// Group g of 64 weight rows, run `seg` of WPG * U units. SPB = 32-k steps
+// per quantization block within a unit (bs / 32, at most 8).
+template <bool HAS_ZP, int SPB, int U, int WIN>
+__global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
+    const uint8_t *__restrict__ Bp, const float *__restrict__ Sd, const uint32_t *__restrict__ Zd,
+    const uint4 *__restrict__ img, const int *__restrict__ exps, float *__restrict__ Y,
+    float *__restrict__ partials, float *__restrict__ H, int M, int N, int K, int nb, int log2_bs,
+    int segs, int wpg) {
+  __shared__ float red[kMaxWaves * 16 * 64];  // 32 KiB: [wave][slice * 4 + v][lane]
+  constexpr int kSteps = U * kUnitSteps;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int c = lane & 15, qd = lane >> 4;
+  const int g = static_cast<int>(blockIdx.x) / segs;
+  const int seg = static_cast<int>(blockIdx.x) - g * segs;
+  const int T = K / 32;
+  const int u0 = (seg * wpg + wave) * U;  // first unit of this wavefront
+  const int s0 = u0 * kUnitSteps;         // first step
+
+  // Per-group bases (wave-uniform), per-lane offsets below 2^31.
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(Bp + static_cast<size_t>(g) * T * 1024), 0, T * 1024, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ri =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4 *>(img), 0, T * kStepBytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(Sd + static_cast<size_t>(g) * nb * 64), 0, nb * 256, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t *>(HAS_ZP ? Zd + static_cast<size_t>(g) * nb * 16 : Zd), 0,
+      HAS_ZP ? nb * 64 : 0, 0x00020000);
+
+  // Each unit's token exponents: lane quarter qd holds tokens 4 qd .. 4 qd + 3.
+  int4 ue[U];
+#pragma unroll
+  for (int uu = 0; uu < U; ++uu)
+    ue[uu] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          __builtin_amdgcn_make_buffer_rsrc(const_cast<int *>(exps), 0,
+                                                                            (T / kUnitSteps) * 64, 0x00020000),
+                                          (u0 + uu) * 64 + 16 * qd, 0, 0));
+
+  struct Slot {
+    u32x4 w, a0, a1;
+    floatx4 s;
+    uint32_t z;
+  };
+  Slot ring[WIN];
+  auto issue = [&](int i) __attribute__((always_inline)) {
+    Slot &sl = ring[i % WIN];
+    const int s = s0 + i;
+    sl.w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, s * 1024 + 16 * lane, 0,
+                                                                           kNonTemporal));
+    sl.a0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ri, s * kStepBytes + 16 * lane, 0, 0));
+    sl.a1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ri, s * kStepBytes + 1024 + 16 * lane, 0, 0));
+    if (i % SPB == 0) {
+      const int blk = (s * 32) >> log2_bs;
+      sl.s = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, blk * 256 + 16 * c, 0, 0));
+      if constexpr (HAS_ZP) sl.z = __builtin_amdgcn_raw_buffer_load_b32(rz, blk * 64 + 4 * c, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < WIN && i < kSteps; ++i) issue(i);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const Masks mk = MakeMasks();
+  floatx4 acc[4], racc[4], tmp[4];
+  floatx4 bsc = floatx4{0.f, 0.f, 0.f, 0.f};
+  uint32_t neg_lo[4], neg_hi[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    neg_lo[j] = 0xE408E408u;  // fp16 -(1024 + 8)
+    neg_hi[j] = 0xD480D480u;  // fp16 -(64 + 8)
+  }
+  auto step = [&](int i) __attribute__((always_inline)) {
+    Slot &sl = ring[i % WIN];
+    // Pins the step's arithmetic here: left free, the compiler hoists work
+    // on later steps' registers into this one and waits for their loads.
+    __asm__ volatile("" : "+v"(sl.w), "+v"(sl.a0), "+v"(sl.a1));
+    if (i % kUnitSteps == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) racc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (i % SPB == 0) {
+      bsc = sl.s;
+      if constexpr (HAS_ZP) {
+        const uint32_t z = sl.z;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // byte j is the zero point of row 16 j + c: fp16 -(1024 + zp) =
+          // 0xE400 | zp, -(64 + zp) = 0xD400 | zp << 4
+          const uint32_t zz = ((z >> (8 * j)) & 0xFu) * 0x10001u;
+          neg_lo[j] = zz | 0xE400E400u;
+          neg_hi[j] = (zz << 4) | 0xD400D400u;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tmp[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    half8 q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q[j] = DecodeQ(sl.w[j], neg_lo[j], neg_hi[j], mk);
+    const half8 a0 = __builtin_bit_cast(half8, sl.a0);
+    const half8 a1 = __builtin_bit_cast(half8, sl.a1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tmp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, q[j], tmp[j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tmp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, q[j], tmp[j], 0, 0, 0);
+    if ((i + 1) % SPB == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) racc[j][v] = fmaf(bsc[j], tmp[j][v], racc[j][v]);
+    }
+    if ((i + 1) % kUnitSteps == 0) {
+      const int4 e4 = ue[i / kUnitSteps];
+      const int ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[j][v] += __builtin_amdgcn_ldexpf(racc[j][v], -ev[v]);
+    }
+  };
+  // Straight-line code (no loop, no branch around a load) keeps the
+  // compiler's waits exact; the scheduling barriers keep each load where it
+  // is issued.
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {
+    step(i);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + WIN < kSteps) issue(i + WIN);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // The wavefronts' sums meet in LDS; wavefront w then finishes the (slice,
+  // token) pairs x = w, w + wpg, ...: added in wavefront order.
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[(wave * 16 + j * 4 + v) * 64 + lane] = acc[j][v];
+  __syncthreads();
+  float *out = seg == 0 ? Y : partials + static_cast<size_t>(seg - 1) * M * N;
+  const int y_end = M * N * 4;
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(out, 0, y_end, 0x00020000);
+  for (int x = wave; x < 16; x += wpg) {
+    float sum = red[x * 64 + lane];
+    for (int w = 1; w < wpg; ++w) sum += red[(w * 16 + x) * 64 + lane];
+    const int j = x >> 2, v = x & 3;
+    const int n = 64 * g + 16 * j + c;
+    const int tok = 4 * qd + v;
+    if (H != nullptr) {
+      // gate/up pairs (rows 2 n', 2 n' + 1 in lanes c, c ^ 1; N even)
+      const float other = PairSwap(sum);
+      const int half_n = N >> 1;
+      if ((c & 1) == 0 && tok < M && n < N) H[tok * half_n + (n >> 1)] = SiluMul(sum, other);
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), ry,
+                                            tok < M && n < N ? (tok * N + n) * 4 : y_end, 0, 0);
+    }
+  }
+}
+
+// Plan-time re-layout of the block scales and zero points for the kernel
+// above: for group g (64 rows) and block b, Sd[g][b][c][j] is the fp32 scale
+// of row 64 g + 16 j + c (0 past N) and byte j of Zd[g][b][c] its zero point
+// (8 when absent or past N).
+__global__ __launch_bounds__(256) void RelayoutDecodeScalesKernel(
+    const float *__restrict__ S, const uint8_t *__restrict__ Z, float *__restrict__ Sd,
+    uint32_t *__restrict__ Zd, int64_t N, int64_t nb, int64_t zp_row_bytes, int64_t items) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // (g, b, c)
+  if (idx >= items) return;
+  const int c = static_cast<int>(idx & 15);
+  const int64_t gb = idx >> 4;
+  const int64_t b = gb % nb, g = gb / nb;
+  float4 s;
+  uint32_t z = 0;
+  float *sv = reinterpret_cast<float *>(&s);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t n = 64 * g + 16 * j + c;
+    sv[j] = n < N ? S[n * nb + b] : 0.0f;
+    const uint32_t zj =
+        n < N && Z != nullptr ? (Z[n * zp_row_bytes + (b >> 1)] >> (4 * (b & 1))) & 0xFu : 8u;
+    z |= zj << (8 * j);
+  }
+  reinterpret_cast<float4 *>(Sd)[idx] = s;
+  if (Zd != nullptr) Zd[idx] = z;
+}
+
+struct Shape {
+  int wpg, units_per_wave, segs;
+};
+
+// Runs per group (segs), wavefronts per workgroup (wpg) and units per
+// wavefront (U), segs * wpg * U = K / 256: the fewest runs (partial sums)
+// whose workgroups still cover 85% of the CUs, then U = 2 before U = 1 and
+// the largest wpg of at least 4 (else any). Measured on MI355X at M = 16
+// (kernel alone): c2 one run of 8 x 2 units 10.5 us (two runs of 4 x 2:
+// 10.7); c1 four runs of 4 x 1 5.7 us (two runs of 4 x 2: 7.1); c3 seven
+// runs of 4 x 2 12.6 us (fourteen of 4 x 1: 12.9).
+inline Shape PickShape(const WeightView &w, int wpg_req, int u_req) {
+  const int64_t groups = (w.N + 63) / 64;
+  const int units = static_cast<int>(w.K / kUnitK);
+  Shape sh{1, 1, units};
+  if (wpg_req > 0 || u_req > 0) {
+    sh.units_per_wave = u_req > 0 ? u_req : 1;
+    sh.wpg = wpg_req > 0 ? wpg_req : 1;
+    sh.segs = units / (sh.units_per_wave * sh.wpg);
+    return sh;
+  }
+  for (int segs = 1; segs <= units; ++segs) {
+    if (units % segs != 0) continue;
+    const int per = units / segs;  // units per workgroup
+    if (segs < units && groups * segs * 100 < static_cast<int64_t>(w.num_cus) * 85) continue;
+    for (int min_wpg : {4, 1})
+      for (int U : {2, 1})
+        for (int wpg : {8, 4, 2, 1})
+          if (wpg >= min_wpg && wpg * U == per) return Shape{wpg, U, segs};
+  }
+  return sh;
+}
+
+inline size_t ImageBytes(const WeightView &w) { return static_cast<size_t>(w.K / 32) * kStepBytes; }
+inline size_t ExpBytes(const WeightView &w) {
+  return (static_cast<size_t>(w.K / kUnitK) * kTok * 4 + 255) / 256 * 256;
+}
+
+template <bool HAS_ZP, int SPB, int U>
+hipError_t LaunchMain(const WeightView &w, int64_t M, const uint4 *img, const int *exps, float *Y,
+                      float *P, float *H, const Shape &sh, hipStream_t s) {
+  const int64_t groups = (w.N + 63) / 64;
+  constexpr int kWin = 4;
+  hipLaunchKernelGGL((DecodeFragKernel<HAS_ZP, SPB, U, kWin>),
+                     dim3(static_cast<unsigned>(groups * sh.segs)), dim3(64 * sh.wpg), 0, s, w.Bp,
+                     w.Sd, w.Zd, img, exps, Y, P, H, static_cast<int>(M), static_cast<int>(w.N),
+                     static_cast<int>(w.K), static_cast<int>(w.nb), w.log2_bs, sh.segs, sh.wpg);
+  return hipGetLastError();
+}
+
+template <bool HAS_ZP, int SPB>
+hipError_t LaunchU(const WeightView &w, int64_t M, const uint4 *img, const int *exps, float *Y,
+                   float *P, float *H, const Shape &sh, hipStream_t s) {
+  return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2>(w, M, img, exps, Y, P, H, sh, s)
+                                : LaunchMain<HAS_ZP, SPB, 1>(w, M, img, exps, Y, P, H, sh, s);
+}
+
+template <bool HAS_ZP>
+hipError_t LaunchZp(const WeightView &w, int64_t M, const uint4 *img, const int *exps, float *Y,
+                    float *P, float *H, const Shape &sh, hipStream_t s) {
+  switch (std::min(w.block_size / 32, kUnitSteps)) {
+  case 1: return LaunchU<HAS_ZP, 1>(w, M, img, exps, Y, P, H, sh, s);
+  case 2: return LaunchU<HAS_ZP, 2>(w, M, img, exps, Y, P, H, sh, s);
+  case 4: return LaunchU<HAS_ZP, 4>(w, M, img, exps, Y, P, H, sh, s);
+  default: return LaunchU<HAS_ZP, 8>(w, M, img, exps, Y, P, H, sh, s);
+  }
+}
+
+} // namespace df
+
+bool DecodeFragLayoutWanted(const WeightView &w) {
+  return (w.K % df::kUnitK) == 0 && w.block_size >= 32 &&
+         (w.block_size & (w.block_size - 1)) == 0 && w.K <= (int64_t{1} << 24) &&
+         w.N < (int64_t{1} << 22) && w.nb * 256 < (int64_t{1} << 31);
+}
+
+size_t DecodeFragScaleBytes(const WeightView &w, size_t *zd_bytes) {
+  const int64_t items = (w.N + 63) / 64 * w.nb * 16;
+  if (zd_bytes != nullptr) *zd_bytes = w.zp != nullptr ? static_cast<size_t>(items) * 4 : 0;
+  return static_cast<size_t>(items) * 16;
+}
+
+hipError_t LaunchDecodeFragRelayout(const WeightView &w, float *Sd, uint32_t *Zd, hipStream_t s) {
+  const int64_t items = (w.N + 63) / 64 * w.nb * 16;
+  hipLaunchKernelGGL(df::RelayoutDecodeScalesKernel, dim3(static_cast<unsigned>((items + 255) / 256)),
+                     dim3(256), 0, s, w.scales, w.zp, Sd, Zd, w.N, w.nb, w.zp_row_bytes, items);
+  return hipGetLastError();
+}
+
+bool DecodeFragSupports(const WeightView &w, int64_t M) {
+  return M >= 2 && M <= 16 && w.Bp != nullptr && w.Sd != nullptr &&
+         (w.zp == nullptr || w.Zd != nullptr) && DecodeFragLayoutWanted(w) &&
+         M * w.K * 4 + 4096 < (int64_t{1} << 31) && M * w.N * 4 < (int64_t{1} << 31) &&
+         (w.K / 32) * df::kStepBytes < (int64_t{1} << 31);
+}
+
+size_t DecodeFragWorkspaceBytes(const WeightView &w, int64_t M, int wpg, int units_per_wave) {
+  const df::Shape sh = df::PickShape(w, wpg, units_per_wave);
+  return df::ImageBytes(w) + df::ExpBytes(w) +
+         static_cast<size_t>(std::max(sh.segs, 1) - 1) * static_cast<size_t>(M) * w.N * 4;
+}
+
+hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                            hipStream_t s, float *H, int wpg, int units_per_wave) {
+  const df::Shape sh = df::PickShape(w, wpg, units_per_wave);
+  const int units = static_cast<int>(w.K / df::kUnitK);
+  if (sh.wpg < 1 || sh.wpg > df::kMaxWaves || sh.segs < 1 ||
+      sh.segs * sh.wpg * sh.units_per_wave != units || (sh.units_per_wave != 1 && sh.units_per_wave != 2))
+    return hipErrorInvalidValue;
+  uint4 *img = static_cast<uint4 *>(work);
+  int *exps = reinterpret_cast<int *>(static_cast<char *>(work) + df::ImageBytes(w));
+  float *P = reinterpret_cast<float *>(static_cast<char *>(work) + df::ImageBytes(w) + df::ExpBytes(w));
+  hipLaunchKernelGGL(df::SplitActKernel, dim3(static_cast<unsigned>(units)), dim3(128), 0, s, A, img,
+                     exps, static_cast<int>(M), static_cast<int>(w.K));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // One run per group: the kernel writes Y (or H) itself.
+  float *Hk = sh.segs == 1 ? H : nullptr;
+  e = w.zp != nullptr ? df::LaunchZp<true>(w, M, img, exps, Y, P, Hk, sh, s)
+                      : df::LaunchZp<false>(w, M, img, exps, Y, P, Hk, sh, s);
+  if (e != hipSuccess || sh.segs == 1) return e;
+  return LaunchSumPartials(Y, P, M * w.N, sh.segs - 1, H, s);
+}
+
+} // namespace mnb

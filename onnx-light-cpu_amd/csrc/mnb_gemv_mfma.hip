@@ -543,19 +543,23 @@ hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, f
   default: e = mf::LaunchBsc<4>(w, M, A, Y, P, sh, s); break;
   }
   if (e != hipSuccess) return e;
-  const int64_t mn = M * w.N;
   // One 512-k range: Y is complete, only the gate/up activation is left.
   if (sh.splits == 1) return H != nullptr ? LaunchSiluMul(Y, H, M, w.N, s) : hipSuccess;
+  return LaunchSumPartials(Y, P, M * w.N, sh.splits - 1, H, s);
+}
+
+hipError_t LaunchSumPartials(float *Y, const float *P, int64_t mn, int parts, float *H,
+                             hipStream_t s) {
   const bool vec = (mn % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(P) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(H) % 8) == 0;
   if (vec)
     hipLaunchKernelGGL(mf::SumPartialsKernel<true>,
                        dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s, Y, P,
-                       mn, sh.splits - 1, H);
+                       mn, parts, H);
   else
     hipLaunchKernelGGL(mf::SumPartialsKernel<false>, dim3(static_cast<unsigned>((mn + 255) / 256)),
-                       dim3(256), 0, s, Y, P, mn, sh.splits - 1, H);
+                       dim3(256), 0, s, Y, P, mn, parts, H);
   return hipGetLastError();
 }
 

@@ -82,6 +82,8 @@ struct WeightView {
   const int32_t *col_exp; // [N] RangeExponent(max_b |scales[n][b]|, kScaleExpTarget)
   const uint8_t *Bp;      // the prefill kernel's fragment-ordered weights, or nullptr
   const uint8_t *Sp;      // its per-step scale / zero-point words, or nullptr
+  const float *Sd;        // DecodeFragKernel's block scales per 64-row group, or nullptr
+  const uint32_t *Zd;     // its zero points per 64-row group, or nullptr
   int64_t K;
   int64_t N;
   int64_t nb;             // ceil(K / bs)
@@ -137,6 +139,28 @@ size_t GemvMfmaWorkspaceBytes(const WeightView &w, int64_t M);
 hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, float *Y,
                                void *work, hipStream_t s, int rows_per_wave, int wgs_per_cu,
                                float *H = nullptr);
+
+// Decode GEMV for 2 <= M <= 16 on fp16 MFMA with exact products over the
+// plan's fragment-ordered weights (Bp) and re-laid block scales / zero points
+// (Sd, Zd); K % 256 == 0, power-of-two block_size >= 32. `work` holds
+// DecodeFragWorkspaceBytes(w, M, 0, 0) bytes: the split activation image, the
+// per-unit exponents and the partial sums of runs 1.. (one pre-pass kernel,
+// the main kernel, and the ordered partial-sum pass when K is split over
+// several workgroups). wpg (wavefronts per workgroup: 1, 2, 4 or 8) and
+// units_per_wave (1 or 2; a unit is 256 k): 0 picks.
+bool DecodeFragLayoutWanted(const WeightView &w);
+size_t DecodeFragScaleBytes(const WeightView &w, size_t *zd_bytes);
+hipError_t LaunchDecodeFragRelayout(const WeightView &w, float *Sd, uint32_t *Zd, hipStream_t s);
+bool DecodeFragSupports(const WeightView &w, int64_t M);
+size_t DecodeFragWorkspaceBytes(const WeightView &w, int64_t M, int wpg = 0,
+                                int units_per_wave = 0);
+hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                            hipStream_t s, float *H = nullptr, int wpg = 0,
+                            int units_per_wave = 0);
+// Y += P[0] + ... + P[parts - 1] over mn elements, in that order (then the
+// gate/up activation into H when H is not null).
+hipError_t LaunchSumPartials(float *Y, const float *P, int64_t mn, int parts, float *H,
+                             hipStream_t s);
 
 // Prefill GEMM on fp16 MFMA, any M, K % 64 == 0, block_size >= 32. `work`
 // holds GemmWorkspaceBytes(w, M) bytes of device memory: A scaled per row by

@@ -1,8 +1,11 @@
-"""GPU parity of the MFMA decode GEMV (5 <= M <= 16, K a multiple of 512).
+"""GPU parity of the two MFMA decode GEMV kernels (2 <= M <= 16).
 
-The kernel splits every activation into three fp16 terms after a
-power-of-two scaling per (token, 512-k range), multiplies them by the exact
-fp16 values of q - zp on the matrix cores and sums in fp32. It is held to the
+DecodeFragKernel (plans holding the fragment-ordered weight copy: N % 4 == 0,
+K % 256 == 0) splits every activation into two fp16 terms after a
+power-of-two scaling per (token, 256-k unit): 22 significant bits. The
+original-layout GemvMfmaKernel (the other plans, K % 512 == 0) splits into
+three terms per 512-k range: exact products. Both multiply by the exact fp16
+values of q - zp on the matrix cores and sum in fp32. Both are held to the
 decode tolerance, max|y - y64| / max|y64| <= 1e-5 against the fp64 oracle,
 and cross-checked against the fp32-FMA decode kernel, which the same call
 runs when no workspace is passed.
@@ -44,13 +47,19 @@ def _run_path1(pkg, cuda, op, A, with_workspace):
     return Y.cpu().numpy()
 
 
+def _expected_kernel(N):
+    return "DecodeFragKernel" if N % 4 == 0 else "GemvMfmaKernel"
+
+
 @pytest.mark.parametrize("K,N,bs,zp", [
-    (1024, 250, 32, True),     # 32-k blocks: each group transposed, four scales per group
-    (1536, 333, 64, False),    # 64-k blocks, no zero points, ragged N, 3 ranges
-    (2048, 200, 128, True),    # one block per 128-k group
-    (1024, 77, 256, False),    # a block spans two groups
-    (4608, 130, 128, True),    # 9 ranges: partial sums of 8 added in order
-    (3072, 96, 1024, True),    # a block spans two ranges
+    (1024, 250, 32, True),     # original layout: 32-k blocks, each group transposed
+    (1536, 333, 64, False),    # original layout: 64-k blocks, no zero points, 3 ranges
+    (2048, 200, 128, True),    # fragment copy: one block per 4 steps, ragged last group
+    (1024, 77, 256, False),    # original layout: a block spans two groups
+    (4608, 130, 128, True),    # original layout: 9 ranges, partial sums added in order
+    (3072, 96, 1024, True),    # fragment copy: a block spans four units
+    (1024, 64, 32, True),      # fragment copy: one scale per step, one group
+    (768, 1028, 64, False),    # fragment copy: 3 units, 17 groups
 ])
 @pytest.mark.parametrize("M", [5, 8, 16])
 def test_mfma_decode_vs_oracle_and_fma(pkg, orc, cuda, K, N, bs, zp, M):
@@ -59,8 +68,9 @@ def test_mfma_decode_vs_oracle_and_fma(pkg, orc, cuda, K, N, bs, zp, M):
     op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
     assert op.select_path(M) == pkg.PATH_GEMV
     print(f"case mfma-decode K={K} N={N} bs={bs} zp={zp} M={M} "
-          f"workspace={op.workspace_bytes(M)}", flush=True)
-    assert op.workspace_bytes(M) >= (K // 512 - 1) * M * N * 4
+          f"workspace={op.workspace_bytes(M)} kernel={op.kernel_name(M)}", flush=True)
+    assert op.kernel_name(M) == _expected_kernel(N)
+    assert op.kernel_name(M, 0) in ("GemvSmallMKernel", "GemvKernel")
     y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
     y_mfma = _run_path1(pkg, cuda, op, A, True)
     y_fma = _run_path1(pkg, cuda, op, A, False)
@@ -136,22 +146,30 @@ def test_mfma_decode_workspace_reuse_and_fallback(pkg, orc, cuda):
 
 
 @pytest.mark.parametrize("K,N,M,mfma", [
-    (1024, 3072, 4, True),    # N >= 3K: MFMA from M = 4
-    (1024, 3072, 3, False),
-    (1024, 6144, 3, True),    # N >= 6K: MFMA from M = 3
+    (1024, 3072, 3, True),    # N >= 3K: DecodeFragKernel from M = 3
+    (1024, 3072, 2, False),
+    (1024, 6144, 2, True),    # N >= 6K: DecodeFragKernel from M = 2
     (2048, 2048, 4, False),   # square: FMA up to M = 4
+    (2048, 2048, 5, True),
+    (1024, 3074, 4, True),    # no fragment copy (N % 4 != 0): GemvMfmaKernel from M = 4
+    (1024, 3074, 3, False),
 ])
 def test_decode_crossover_by_shape(pkg, orc, cuda, K, N, M, mfma):
-    """The automatic decode path takes the MFMA kernel from M = 4 when N >= 3K
-    and from M = 3 when N >= 6K (FMA below): it is then bit-identical to the
-    MFMA run (workspace given) or to the FMA run (no workspace), and both are
-    within the decode bound of the fp64 oracle."""
+    """The automatic decode path takes DecodeFragKernel from M = 3 when
+    N >= 3K, from M = 2 when N >= 6K and from M = 5 otherwise (plans without
+    the fragment copy: GemvMfmaKernel from M = 4 when N >= 3K, M = 3 when
+    N >= 6K, else 5), the FMA kernels below: it is then bit-identical to the
+    MFMA run (workspace given) or to the FMA run (no workspace), both within
+    the decode bound of the fp64 oracle, and mnb_kernel_name names it."""
     import torch
     bs = 128
     B, S, Z = _weights(pkg, K, N, bs, True, seed=K + N + M)
     A = pkg.workloads.make_activations(M, K, 1.0, seed=M + 3)
     op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
-    print(f"case decode-crossover K={K} N={N} M={M} expect_mfma={mfma}", flush=True)
+    name = op.kernel_name(M)
+    print(f"case decode-crossover K={K} N={N} M={M} expect_mfma={mfma} kernel={name}",
+          flush=True)
+    assert name == (_expected_kernel(N) if mfma else "GemvSmallMKernel")
     y_ws = _run_path1(pkg, cuda, op, A, True)
     y_fma = _run_path1(pkg, cuda, op, A, False)
     y_auto = op(torch.from_numpy(A).to(cuda)).cpu().numpy()
@@ -161,4 +179,39 @@ def test_decode_crossover_by_shape(pkg, orc, cuda, K, N, M, mfma):
     np.testing.assert_array_equal(y_auto, y_ws)
     # with the workspace the MFMA kernel's summation order differs from FMA's
     assert (not np.array_equal(y_ws, y_fma)) == mfma
+    op.release()
+
+
+@pytest.mark.parametrize("K,N,bs", [(4096, 448, 128), (3584, 256, 32), (2048, 1024, 64)])
+def test_decode_frag_every_launch_shape(pkg, orc, cuda, K, N, bs):
+    """DecodeFragKernel for every valid (wavefronts per workgroup, units per
+    wavefront) split of K, forced through mnb_run_kernel: each within the
+    decode bound of the fp64 oracle and bit-reproducible; invalid splits are
+    rejected before any launch."""
+    import torch
+    M = 16
+    B, S, Z = _weights(pkg, K, N, bs, True, seed=K + bs)
+    A = pkg.workloads.make_activations(M, K, 1.0, seed=K + 1)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
+    dA = torch.from_numpy(A).to(cuda)
+    units = K // 256
+    ran = 0
+    for wpg in (1, 2, 4, 8):
+        for U in (1, 2):
+            valid = units % (wpg * U) == 0
+            print(f"case decode-frag-shape K={K} N={N} bs={bs} wpg={wpg} U={U} valid={valid}",
+                  flush=True)
+            if not valid:
+                with pytest.raises(ValueError, match="unsupported"):
+                    op.run_kernel(dA, pkg.KERNEL_DECODE_FRAG, wpg, U)
+                continue
+            y1 = op.run_kernel(dA, pkg.KERNEL_DECODE_FRAG, wpg, U).cpu().numpy()
+            y2 = op.run_kernel(dA, pkg.KERNEL_DECODE_FRAG, wpg, U).cpu().numpy()
+            np.testing.assert_array_equal(y1, y2)
+            err = orc.normwise_max_error(y1, y64)
+            print(f"  normwise error {err:.2e}")
+            assert err <= GEMV_TOL
+            ran += 1
+    assert ran >= 3
     op.release()

@@ -306,18 +306,36 @@ def test_c5_layer_projections(pkg, orc, cuda, proj, M):
         assert np.isfinite(Y).all()
 
 
-@pytest.mark.parametrize("K,N,bs,M", [
-    (16384, 200, 64, 1),    # the M = 1 kernel's largest K (8 chunks per lane)
-    (16416, 130, 32, 1),    # one chunk past it: another decode kernel serves M = 1
-    (32768, 96, 128, 8),    # the MFMA decode's largest K (64 ranges of 512)
-    (33280, 96, 128, 8),    # one range past it: the fp32-FMA kernel serves it
+@pytest.mark.parametrize("K,N,bs,M,kernel", [
+    (16384, 200, 64, 1, "GemvM1Kernel"),      # the M = 1 kernel's largest K (8 chunks per lane)
+    (16416, 130, 32, 1, "GemvKernel"),        # one chunk past it: the fp32-FMA fallback serves M = 1
+    (32768, 94, 128, 8, "GemvMfmaKernel"),    # the original-layout MFMA decode's largest K (64 ranges)
+    (33280, 94, 128, 8, "GemvSmallMKernel"),  # one range past it: the fp32-FMA kernel serves it
+    (33280, 96, 128, 8, "DecodeFragKernel"),  # the fragment-copy kernel has no such limit
 ])
-def test_decode_at_the_kernels_k_limits(pkg, orc, cuda, K, N, bs, M):
-    """At and just past each decode kernel's largest K the path stays correct
-    (the dispatcher switches kernels instead of overflowing a limit)."""
+def test_decode_at_the_kernels_k_limits(pkg, orc, cuda, K, N, bs, M, kernel):
+    """At and just past each decode kernel's largest K the dispatcher switches
+    kernels (named by mnb_kernel_name, checked against the run: the MFMA
+    kernels' results differ from the FMA kernel's summation, the FMA kernels'
+    equal the no-workspace run bit for bit) and the result stays within the
+    decode bound."""
+    import torch
     p, B, S, Z = _case(pkg, K, N, bs, True, seed=K % 1000 + N)
     A = pkg.workloads.make_activations(M, K, 1.0, seed=M + 5)
-    Y, path = _run(pkg, cuda, K, N, bs, B, S, Z, A)
-    assert path == pkg.PATH_GEMV
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    name = op.kernel_name(M)
+    print(f"case k-limit K={K} N={N} bs={bs} M={M} kernel={name}", flush=True)
+    assert name == kernel
+    assert op.select_path(M) == pkg.PATH_GEMV
+    dA = torch.from_numpy(A).to(cuda)
+    Y = op(dA).cpu().numpy()
     y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
     assert orc.normwise_max_error(Y, y64) <= GEMV_TOL
+    if M == 1:
+        forced = op.run_kernel(dA, pkg.KERNEL_GEMV_M1).cpu().numpy() if kernel == "GemvM1Kernel" \
+            else op.run_kernel(dA, pkg.KERNEL_GEMV).cpu().numpy()
+        np.testing.assert_array_equal(Y, forced)
+    else:
+        fma = op.run_kernel(dA, pkg.KERNEL_GEMV_SMALL_M).cpu().numpy()
+        assert np.array_equal(Y, fma) == (kernel == "GemvSmallMKernel")
+    op.release()
