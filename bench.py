@@ -56,8 +56,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline sampling budget over its four modes (0 disables)")
     ap.add_argument("--only", default="",
-                    help="comma list of legs: decode,gemm,sweep,c5,gate_up,rmsnorm,cpu,copy "
-                         "(default: all but copy)")
+                    help="comma list of legs: decode,ceiling,gemm,sweep,c5,gate_up,rmsnorm,plan,"
+                         "cpu,copy (default: all but copy)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step directly instead of replaying a HIP graph "
                          "(for counter collection, which serialises dispatches)")
@@ -131,6 +131,93 @@ def copy_leg(torch, dev, steps, warmup, stream):
     ms, wall = time_graph(torch, launches, steps, warmup, stream)
     return {"bytes_read": n, "bytes_written": n, "us_per_launch": ms * 1e3,
             "GBps": 2 * n / (ms * 1e-3) / 1e9, "wall_s": wall}
+
+
+def stream_ceiling_leg(torch, pkg, dev, nbytes, steps, warmup, stream):
+    """The HBM read ceiling for one launch of nbytes: mnb_stream_read (loads
+    only, 16 KiB contiguous records per wavefront) over as many rotated
+    buffers as the headline leg, one launch each, graph-replayed."""
+    import ctypes
+    rot = max(2, -(-ROTATION_BYTES // nbytes))
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(i & 0xFF) for i in range(rot)]
+    out = torch.empty(2048, dtype=torch.int32, device=dev)  # MNB_STREAM_OUT_WORDS
+    L = pkg.library()
+
+    def launches():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for b in bufs:
+            rc = L.mnb_stream_read(ctypes.c_void_p(b.data_ptr()), nbytes,
+                                   ctypes.c_void_p(out.data_ptr()), out.numel(), st)
+            if rc != 0:
+                raise RuntimeError(f"mnb_stream_read: status {rc}")
+
+    ms, _ = time_graph(torch, launches, steps, warmup, stream)
+    us = ms * 1e3 / rot
+    del bufs
+    torch.cuda.empty_cache()
+    return {"kernel": "StreamReadKernel (mnb_stream_read)", "bytes_per_launch": nbytes,
+            "rotation_copies": rot, "us_per_launch": us, "GBps": nbytes / (us * 1e-6) / 1e9,
+            "frac_of_peak": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
+def fp16_gemm_reference(torch, dev, p, M, steps, warmup, stream):
+    """Vendor dense fp16 GEMM on the same shape (torch.matmul -> hipBLASLt),
+    fp16 A and fp16 weights already dequantized: no 4-bit decode and no fp32
+    input conversion, i.e. a reference for what the fp16 matrix cores reach on
+    this shape through the vendor library."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    A = torch.randn((M, p.K), device=dev, generator=g).to(torch.float16)
+    Wt = torch.randn((p.N, p.K), device=dev, generator=g).to(torch.float16)
+    Y = torch.empty((M, p.N), device=dev, dtype=torch.float16)
+
+    def launches():
+        torch.matmul(A, Wt.t(), out=Y)
+
+    ms, _ = time_graph(torch, launches, steps, warmup, stream)
+    tflops = p.flops(M) / (ms * 1e-3) / 1e12
+    return {"what": "torch.matmul fp16 x fp16 -> fp16 (hipBLASLt), dense weights",
+            "us_per_launch": ms * 1e3, "TFLOPs": tflops, "frac_fp16_peak": tflops / FP16_PEAK_TFLOPS}
+
+
+def plan_create_leg(torch, pkg, dev):
+    """First-use packing time: mnb_plan_create per c5 projection (host upload of
+    B, scales and zero points, the per-row scale exponents, and the re-laid
+    copies for the prefill and small-M decode kernels), mnb_plan_create_device
+    on weights already in HBM (the derived copies only), and the gate/up plan
+    (host interleave of the two weights, then the above). Wall time per plan,
+    synchronous."""
+    W = pkg.workloads
+    out = []
+    for p in W.CONFIGS["c5"].projections:
+        B, S, Z = W.make_weights(p, 5)
+        dB, dS = torch.from_numpy(B).to(dev), torch.from_numpy(S).to(dev)
+        dZ = torch.from_numpy(Z).to(dev) if Z is not None else None
+        torch.cuda.synchronize()
+        r = {"projection": p.name, "K": p.K, "N": p.N, "weight_bytes": p.weight_bytes()}
+        for name, fn in (("host_ms", lambda: pkg.MatMulNBits(p.K, p.N, 4, p.block_size).prepare(B, S, Z)),
+                         ("device_ms", lambda: pkg.MatMulNBits(p.K, p.N, 4, p.block_size)
+                          .prepare_device(dB, dS, dZ))):
+            fn().release()  # warm
+            t0 = time.perf_counter()
+            op = fn()
+            torch.cuda.synchronize()
+            r[name] = (time.perf_counter() - t0) * 1e3
+            op.release()
+        out.append(r)
+    p = W.Projection("gate_up", 4096, 14336, 128, True)
+    Bg, Sg, Zg = W.make_weights(p, 6)
+    Bu, Su, Zu = W.make_weights(p, 7)
+    pkg.GateUpSiLU(p.K, p.N, 4, p.block_size).prepare(Bg, Sg, Zg, Bu, Su, Zu).release()
+    t0 = time.perf_counter()
+    op = pkg.GateUpSiLU(p.K, p.N, 4, p.block_size).prepare(Bg, Sg, Zg, Bu, Su, Zu)
+    torch.cuda.synchronize()
+    out.append({"projection": "gate_up plan (two 14336-row weights interleaved)", "K": p.K,
+                "N": 2 * p.N, "weight_bytes": 2 * p.weight_bytes(),
+                "host_ms": (time.perf_counter() - t0) * 1e3})
+    op.release()
+    torch.cuda.empty_cache()
+    return out
 
 
 def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
@@ -442,7 +529,7 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(device=dev)
     legs = (set(args.only.split(",")) if args.only
-            else {"decode", "gemm", "sweep", "c5", "gate_up", "rmsnorm", "cpu"})
+            else {"decode", "ceiling", "gemm", "sweep", "c5", "gate_up", "rmsnorm", "plan", "cpu"})
     W = pkg.workloads
 
     t_start = time.perf_counter()
@@ -459,10 +546,21 @@ def main():
         gemm = gemm_leg(torch, pkg, dev, p, 2048, args.steps, args.warmup, 13, stream)
         print(f"# gemm c4 M=2048: {gemm['us_per_launch']:.1f} us, {gemm['TFLOPs']:.1f} TFLOP/s",
               file=sys.stderr, flush=True)
+        gemm["reference_fp16_gemm"] = fp16_gemm_reference(torch, dev, p, 2048, args.steps,
+                                                          args.warmup, stream)
+        print(f"# reference: dense fp16 torch.matmul c4 shape: "
+              f"{gemm['reference_fp16_gemm']['us_per_launch']:.1f} us, "
+              f"{gemm['reference_fp16_gemm']['TFLOPs']:.1f} TFLOP/s", file=sys.stderr, flush=True)
     sweep = []
     if "sweep" in legs:
-        for cname, Ms in (("c1", (1,)), ("c2", (4, 16)), ("c3", (1, 2, 8, 16))):
-            p = W.CONFIGS[cname].projections[0]
+        # the configs, then one GPU's shard of c2 and c3 under 8-way tensor
+        # parallelism (c2 column-parallel: N / 8 weight rows; c3 row-parallel:
+        # K / 8 of each row)
+        tp8 = {"c2/tp8": W.Projection("c2/tp8", 4096, 14336 // 8, 128, True),
+               "c3/tp8": W.Projection("c3/tp8", 14336 // 8, 4096, 32, True, 0.5, 0.002, 0.01)}
+        for cname, Ms in (("c1", (1,)), ("c2", (4, 16)), ("c3", (1, 2, 8, 16)),
+                          ("c2/tp8", (1, 16)), ("c3/tp8", (1, 16))):
+            p = tp8[cname] if cname in tp8 else W.CONFIGS[cname].projections[0]
             for M in Ms:
                 r = decode_leg(torch, pkg, dev, p, M, max(3, args.steps // 4), 2, 17 + M, stream)
                 r["config"] = cname
@@ -492,6 +590,20 @@ def main():
             print(f"# RMSNorm + qkv M={r['M']}: fused {r['fused_us']:.1f} us, unfused "
                   f"{r['unfused_us']:.1f} us ({r['gain']:.2f}x), matmul alone "
                   f"{r['matmul_only_us']:.1f} us", file=sys.stderr, flush=True)
+    ceiling = None
+    if "ceiling" in legs and head is not None:
+        ceiling = stream_ceiling_leg(torch, pkg, dev, head["bytes_per_launch"], args.steps,
+                                     args.warmup, stream)
+        print(f"# read ceiling, {ceiling['bytes_per_launch']} B per launch: "
+              f"{ceiling['us_per_launch']:.2f} us, {ceiling['GBps']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+    plans = []
+    if "plan" in legs:
+        plans = plan_create_leg(torch, pkg, dev)
+        for r in plans:
+            print(f"# plan create {r['projection']}: host {r['host_ms']:.1f} ms"
+                  + (f", device {r['device_ms']:.1f} ms" if "device_ms" in r else ""),
+                  file=sys.stderr, flush=True)
     copy = None
     if "copy" in legs:
         copy = copy_leg(torch, dev, args.steps, args.warmup, stream)
@@ -512,6 +624,10 @@ def main():
                                 "copy-calibrated)",
                 "kernel": "GemvM1Kernel (c2 M=1)", "us_per_launch": head["us_per_launch"],
                 "bytes_per_launch": head["bytes_per_launch"]}
+        if ceiling is not None:
+            roof["ceiling"] = ceiling["frac_of_peak"]
+            roof["ceiling_GBps"] = ceiling["GBps"]
+            roof["frac_of_ceiling"] = head["GBps"] / ceiling["GBps"]
         workload = ("c2: MatMulNBits M=1 K=4096 N=14336 bits=4 block_size=128 zero_points; "
                     f"{head['rotation_copies']} rotated weight copies per step")
     else:
@@ -529,6 +645,8 @@ def main():
         "decode_sweep": sweep,
         "c5_layer_stack": c5,
         "gate_up_fusion": gate_up,
+        "read_ceiling": ceiling,
+        "plan_create": plans,
         "rmsnorm_fusion": rms,
         "copy_calibration": copy,
         "timing": "eager launches" if EAGER else "HIP graph replay",

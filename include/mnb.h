@@ -227,6 +227,18 @@ int mnb_kernel_workspace_bytes(const mnb_plan *plan, int64_t M, int kernel, int 
 int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
                    size_t workspace_bytes, void *stream, int kernel, int p0, int p1);
 
+/* Words of dOut that mnb_stream_read writes (one per wavefront). */
+#define MNB_STREAM_OUT_WORDS 2048u
+
+/* HBM read ceiling probe: one launch that streams `bytes` (< 2^31) of device
+ * memory at dSrc and nothing else (2048 wavefronts, each reading 16 KiB
+ * contiguous records with sixteen 16-byte loads in flight), folding them into
+ * dOut[0 .. MNB_STREAM_OUT_WORDS) so the loads are kept. A decode launch's
+ * roofline fraction is reported next to this probe's rate over the same
+ * bytes per launch. No counterpart in the reference. */
+int mnb_stream_read(const void *dSrc, size_t bytes, uint32_t *dOut, size_t out_words,
+                    void *stream);
+
 /* Text for a status code (static storage). */
 const char *mnb_status_str(int status);
 

@@ -21,7 +21,8 @@ def test_library_exports_every_header_function(pkg):
         "mnb_run", "mnb_run_path", "mnb_run_ex", "mnb_select_path", "mnb_status_str",
         "mnb_last_error", "mnb_weight_bytes", "mnb_version", "mnb_qdq_repack",
         "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes", "mnb_run_rmsnorm",
-        "mnb_run_no_alloc", "mnb_kernel_name", "mnb_kernel_workspace_bytes", "mnb_run_kernel"])
+        "mnb_run_no_alloc", "mnb_kernel_name", "mnb_kernel_workspace_bytes", "mnb_run_kernel",
+        "mnb_stream_read"])
     for name in names:
         assert hasattr(L, name), name
 
