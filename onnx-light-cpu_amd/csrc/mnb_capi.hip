@@ -711,13 +711,16 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
     }
     break;
   case 2:
-    // The GEMM's fused stores address H with 32-bit byte offsets.
-    fused = H != nullptr && M * plan->view.N * 2 < (int64_t{1} << 31);
+    // The GEMM's fused stores address H with 32-bit byte offsets: H's bytes
+    // and those of a whole tile of rows (up to 128) must stay below 2^31.
+    fused = H != nullptr && M * plan->view.N * 2 < (int64_t{1} << 31) &&
+            plan->view.N < (int64_t{1} << 22);
     e = mnb::LaunchGemm(plan->view, M, dA, Ys, work, s, fused ? H : nullptr, gamma, eps, dBias,
                         &bias_done);
     break;
   case 5:
-    fused = H != nullptr && M * plan->view.N * 2 < (int64_t{1} << 31);
+    fused = H != nullptr && M * plan->view.N * 2 < (int64_t{1} << 31) &&
+            plan->view.N < (int64_t{1} << 22);
     e = mnb::LaunchPrefill(plan->view, M, dA, Ys, work, s, fused ? H : nullptr, gamma, eps, dBias,
                            &bias_done);
     break;
@@ -820,11 +823,28 @@ const char *mnb_kernel_name(const mnb_plan *plan, int64_t M, size_t workspace_by
   }
 }
 
+// Whether `kernel` can serve M rows of the plan's weights (A's alignment is
+// checked by the caller that has it).
+static bool KernelServes(const mnb::WeightView &w, int64_t M, int kernel) {
+  switch (kernel) {
+  case MNB_KERNEL_GEMV_M1: return M == 1 && mnb::GemvM1Supports(w);
+  case MNB_KERNEL_GEMV_SMALL_M: return M >= 2 && mnb::GemvSmallMSupports(w, M);
+  case MNB_KERNEL_GEMV_MFMA: return mnb::GemvMfmaSupports(w, M);
+  case MNB_KERNEL_DECODE_FRAG: return mnb::DecodeFragSupports(w, M);
+  case MNB_KERNEL_GEMM: return mnb::GemmSupports(w, M);
+  case MNB_KERNEL_PREFILL: return mnb::PrefillSupports(w, M);
+  case MNB_KERNEL_GEMV: return M <= 16 && mnb::GemvSupports(w, M);
+  case MNB_KERNEL_GENERIC: return true;
+  default: return false;
+  }
+}
+
 int mnb_kernel_workspace_bytes(const mnb_plan *plan, int64_t M, int kernel, int p0, int p1,
                                size_t *bytes) {
   if (plan == nullptr || bytes == nullptr) return MNB_ERR_NULL_POINTER;
   if (M < 1 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
   const mnb::WeightView &w = plan->view;
+  if (plan->gate_up || !KernelServes(w, M, kernel)) return MNB_ERR_UNSUPPORTED;
   switch (kernel) {
   case MNB_KERNEL_GEMV_MFMA:
     *bytes = mnb::GemvMfmaWorkspaceBytes(w, M);
@@ -876,19 +896,7 @@ int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, 
   if (!HasWorkspace(dWorkspace, workspace_bytes, need)) return MNB_ERR_WORKSPACE;
   const mnb::WeightView &w = plan->view;
   const bool a_aligned = (reinterpret_cast<uintptr_t>(dA) % 16) == 0;
-  bool ok = false;
-  switch (kernel) {
-  case MNB_KERNEL_GEMV_M1: ok = M == 1 && a_aligned && mnb::GemvM1Supports(w); break;
-  case MNB_KERNEL_GEMV_SMALL_M: ok = M >= 2 && a_aligned && mnb::GemvSmallMSupports(w, M); break;
-  case MNB_KERNEL_GEMV_MFMA: ok = a_aligned && mnb::GemvMfmaSupports(w, M); break;
-  case MNB_KERNEL_DECODE_FRAG: ok = a_aligned && mnb::DecodeFragSupports(w, M); break;
-  case MNB_KERNEL_GEMM: ok = a_aligned && mnb::GemmSupports(w, M); break;
-  case MNB_KERNEL_PREFILL: ok = a_aligned && mnb::PrefillSupports(w, M); break;
-  case MNB_KERNEL_GEMV: ok = M <= 16 && a_aligned && mnb::GemvSupports(w, M); break;
-  case MNB_KERNEL_GENERIC: ok = true; break;
-  default: ok = false; break;
-  }
-  if (!ok) return MNB_ERR_UNSUPPORTED;
+  if (!a_aligned && kernel != MNB_KERNEL_GENERIC) return MNB_ERR_UNSUPPORTED;
   int cur = -1;
   if (hipGetDevice(&cur) != hipSuccess || cur != plan->device) return MNB_ERR_NO_DEVICE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);

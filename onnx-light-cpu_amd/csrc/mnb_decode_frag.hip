@@ -11,9 +11,10 @@
 //
 // Two kernels per call:
 //
-// 1. SplitActKernel (one workgroup per unit of 256 k) scales each token's
-//    values in the unit by a power of two 2^e (largest magnitude in
-//    [2^14, 2^15); exact) and splits every scaled value into two fp16 terms,
+// 1. SplitActKernel (one wavefront per unit of 256 k and pair of tokens)
+//    scales each token's values in the unit by a power of two 2^e (largest
+//    magnitude in [2^14, 2^15); exact) and splits every scaled value into two
+//    fp16 terms,
 //    a 2^e ~ a0 + a1 with a0 = fp16(a 2^e) and a1 = fp16(a 2^e - a0) (the
 //    difference is exact in fp32; 2 x 11 significand bits, so |a 2^e - a0 -
 //    a1| <= 2^-22 |a 2^e|, and below 2^-39 of the unit's largest magnitude
@@ -103,49 +104,48 @@ __device__ __forceinline__ half8 DecodeQ(uint32_t w, uint32_t neg_lo, uint32_t n
   return __builtin_bit_cast(half8, r);
 }
 
-// One workgroup (128 threads) per unit u: thread (t, ch) takes the 32 values
-// k = 256 u + 32 ch .. + 31 of token t. Writes img[((u * 8 + ch) * kTerms +
-// term) * 64 + 16 quarter + t] and exps[u * 16 + t].
-__global__ __launch_bounds__(128) void SplitActKernel(const float *__restrict__ A,
-                                                      uint4 *__restrict__ img,
-                                                      int *__restrict__ exps, int M, int K) {
-  const int u = blockIdx.x;
-  const int t = threadIdx.x >> 3, ch = threadIdx.x & 7;
+// One wavefront (a workgroup of 64 threads) per unit u and pair of tokens:
+// lane (t, ch) of workgroup (u, pair) takes the 8 values k = 256 u + 8 ch ..
+// + 7 of token t = 2 pair + (lane >> 5), so each token's unit spans 32 lanes
+// and its largest magnitude is a 5-step butterfly within them. Writes
+// img[((u * 8 + ch / 4) * kTerms + term) * 64 + 16 (ch % 4) + t] and
+// exps[u * 16 + t]. (One 128-thread workgroup per unit, each thread taking 32
+// values, kept 16 workgroups busy for about 4 us at M = 16.)
+__global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A,
+                                                     uint4 *__restrict__ img,
+                                                     int *__restrict__ exps, int M, int K) {
+  const int u = static_cast<int>(blockIdx.x) >> 3;
+  const int t = (static_cast<int>(blockIdx.x) & 7) * 2 + static_cast<int>(threadIdx.x >> 5);
+  const int ch = threadIdx.x & 31;
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, M * K * 4, 0x00020000);
   // tokens past M read past the end of the buffer: zeros
-  const int vo = t < M ? (t * K + kUnitK * u + 32 * ch) * 4 : M * K * 4;
-  floatx4 av[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    av[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo + 16 * i, 0, 0));
+  const int vo = t < M ? (t * K + kUnitK * u + 8 * ch) * 4 : M * K * 4;
+  const floatx4 v0 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo, 0, 0));
+  const floatx4 v1 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo + 16, 0, 0));
   float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int c = 0; c < 4; ++c) amax = fmaxf(amax, fmaxf(fabsf(v0[c]), fabsf(v1[c])));
 #pragma unroll
-    for (int c = 0; c < 4; ++c) amax = fmaxf(amax, fabsf(av[i][c]));
-#pragma unroll
-  for (int o = 4; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
   // The largest magnitude times 2^e in [2^14, 2^15); ldexp is exact for
   // every e this gives (|e| <= 163), subnormal inputs included. A zero, inf
   // or NaN maximum gives e = 0 (inf and NaN then propagate).
   const int e = RangeExponent(amax, 14);
   if (ch == 0) exps[u * kTok + t] = e;
+  half8 h[kTerms];
 #pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {  // 8 values k = 32 ch + 8 qd .. + 7
-    half8 h[kTerms];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int o = (i & 3) * 2 + (i >> 2);  // k order [0,4,1,5,2,6,3,7]
-      const float x = ldexpf(av[2 * qd + (i >> 2)][i & 3], e);
-      const _Float16 h0 = static_cast<_Float16>(x);
-      h[0][o] = h0;
-      h[1][o] = static_cast<_Float16>(__builtin_isfinite(x) ? x - static_cast<float>(h0) : 0.f);
-    }
-#pragma unroll
-    for (int term = 0; term < kTerms; ++term)
-      img[((u * kUnitSteps + ch) * kTerms + term) * 64 + 16 * qd + t] = __builtin_bit_cast(uint4, h[term]);
+  for (int i = 0; i < 8; ++i) {
+    const int o = (i & 3) * 2 + (i >> 2);  // k order [0,4,1,5,2,6,3,7]
+    const float x = ldexpf(i < 4 ? v0[i] : v1[i - 4], e);
+    const _Float16 h0 = static_cast<_Float16>(x);
+    h[0][o] = h0;
+    h[1][o] = static_cast<_Float16>(__builtin_isfinite(x) ? x - static_cast<float>(h0) : 0.f);
   }
+#pragma unroll
+  for (int term = 0; term < kTerms; ++term)
+    img[((u * kUnitSteps + (ch >> 2)) * kTerms + term) * 64 + 16 * (ch & 3) + t] =
+        __builtin_bit_cast(uint4, h[term]);
 }
 
 // Group g of 64 weight rows, run `seg` of WPG * U units. SPB = 32-k steps
@@ -447,7 +447,7 @@ hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, floa
   uint4 *img = static_cast<uint4 *>(work);
   int *exps = reinterpret_cast<int *>(static_cast<char *>(work) + df::ImageBytes(w));
   float *P = reinterpret_cast<float *>(static_cast<char *>(work) + df::ImageBytes(w) + df::ExpBytes(w));
-  hipLaunchKernelGGL(df::SplitActKernel, dim3(static_cast<unsigned>(units)), dim3(128), 0, s, A, img,
+  hipLaunchKernelGGL(df::SplitActKernel, dim3(static_cast<unsigned>(units * 8)), dim3(64), 0, s, A, img,
                      exps, static_cast<int>(M), static_cast<int>(w.K));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
