@@ -817,7 +817,10 @@ const char *mnb_kernel_name(const mnb_plan *plan, int64_t M, size_t workspace_by
     case kDecSmallM: return "GemvSmallMKernel";
     default: return "GemvKernel";
     }
-  case 2: return mnb::GemmUsesPrefill(plan->view, M) ? "PrefillKernel" : "GemmKernel";
+  case 2:
+    return mnb::GemmUsesStream(plan->view, M)    ? "StreamKernel"
+           : mnb::GemmUsesPrefill(plan->view, M) ? "PrefillKernel"
+                                                 : "GemmKernel";
   case 4: return "exact groups of 16 rows";
   default: return "GenericKernel";
   }
@@ -833,6 +836,7 @@ static bool KernelServes(const mnb::WeightView &w, int64_t M, int kernel) {
   case MNB_KERNEL_DECODE_FRAG: return mnb::DecodeFragSupports(w, M);
   case MNB_KERNEL_GEMM: return mnb::GemmSupports(w, M);
   case MNB_KERNEL_PREFILL: return mnb::PrefillSupports(w, M);
+  case MNB_KERNEL_STREAM: return mnb::StreamSupports(w, M);
   case MNB_KERNEL_GEMV: return M <= 16 && mnb::GemvSupports(w, M);
   case MNB_KERNEL_GENERIC: return true;
   default: return false;
@@ -859,6 +863,9 @@ int mnb_kernel_workspace_bytes(const mnb_plan *plan, int64_t M, int kernel, int 
   case MNB_KERNEL_PREFILL:
     *bytes = mnb::GemmShapeWorkspaceBytes(w, M, std::max(1, p0));
     if (p0 <= 0) *bytes = std::max(*bytes, mnb::GemmWorkspaceBytes(w, M));
+    return MNB_OK;
+  case MNB_KERNEL_STREAM:
+    *bytes = mnb::StreamWorkspaceBytes(w, M, p0, p1);
     return MNB_OK;
   case MNB_KERNEL_GEMV_M1:
   case MNB_KERNEL_GEMV_SMALL_M:
@@ -887,6 +894,7 @@ int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, 
   case MNB_KERNEL_DECODE_FRAG: shape_ok = one_of(p0, {0, 1, 2, 4, 8}) && p1 <= 2; break;
   case MNB_KERNEL_GEMM: shape_ok = one_of(p0, {0, 32, 64, 128}) && p1 <= 16; break;
   case MNB_KERNEL_PREFILL: shape_ok = p0 <= 16 && p1 == 0; break;
+  case MNB_KERNEL_STREAM: shape_ok = p0 <= 16 && one_of(p1, {0, 4, 8, 16}) && (p0 == 0) == (p1 == 0); break;
   default: shape_ok = p0 == 0 && p1 == 0; break;
   }
   if (!shape_ok) return MNB_ERR_UNSUPPORTED;
@@ -910,6 +918,9 @@ int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, 
   case MNB_KERNEL_PREFILL:
     e = p0 > 0 ? mnb::LaunchGemmShape(w, M, dA, dY, dWorkspace, s, mnb::kPrefillTileCode, p0)
                : mnb::LaunchPrefill(w, M, dA, dY, dWorkspace, s);
+    break;
+  case MNB_KERNEL_STREAM:
+    e = mnb::LaunchStream(w, M, dA, dY, dWorkspace, s, nullptr, nullptr, 0.0f, nullptr, p0, p1);
     break;
   case MNB_KERNEL_GEMV: e = mnb::LaunchGemv(w, M, dA, dY, s); break;
   default: e = mnb::LaunchGeneric(w, M, dA, dY, s); break;

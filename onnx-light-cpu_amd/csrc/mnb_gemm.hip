@@ -1048,6 +1048,234 @@ PrefillKernel(const uint4 *__restrict__ Ah, const uint8_t *__restrict__ Bp,
     body(std::integral_constant<int, 1>{});
 }
 
+// ---------------------------------------------------------------------------
+// Small-M prefill (17 <= M <= 64) streaming the fragment-ordered weights
+// (StreamKernel). With so few rows a 128 x 256 tile holds mostly padding and
+// the GEMM is bound by reading the weights once, so the grid is laid out
+// like the decode kernels': one workgroup per (group g of 64 weight rows, K
+// segment), WPG wavefronts each taking SPW consecutive 32-k steps of the
+// segment. Per step a wavefront loads the group's 1 KiB weight record and
+// 256-byte scale record (the PrefillKernel layouts), dequantizes the four
+// words exactly as PrefillKernel does (DequantWord on the fp16 scale times
+// 2^e_n), reads TG activation fragments of the fp16 image ConvertAKernel
+// wrote (BM = 64 tiling, rows scaled by 2^f_m, rows past M zero) and issues
+// 4 TG v_mfma_f32_16x16x32_f16 into TG x 4 fp32 tiles. The operands are
+// those of the prefill GEMM, so the product is the same up to the order of
+// the fp32 sums. Loads stream through a rolling window of WIN steps in
+// registers (multiply the oldest, issue the one WIN further on), with no
+// branch around any load. The wavefronts' tiles meet in LDS and are added
+// in wavefront order; segment 0 writes Y (adding the bias or applying the
+// gate/up activation when K is not split), segment s > 0 its partial sum,
+// added in segment order by SplitReduceKernel.
+constexpr int kSGroupRows = 64;
+
+template <bool HAS_ZP, int TG, int SPW, int WIN>
+__global__ __launch_bounds__(512) void StreamKernel(
+    const uint4 *__restrict__ Ah, const uint8_t *__restrict__ Bp, const uint8_t *__restrict__ Sp,
+    float *__restrict__ Y, float *__restrict__ partials, float *__restrict__ H,
+    const int *__restrict__ row_exp, const int *__restrict__ col_exp,
+    const float *__restrict__ bias, int M, int N, int K, int segs, int wpg) {
+  extern __shared__ floatx4 sred[];  // [wave][tg * 4 + j][lane]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int g = static_cast<int>(blockIdx.x) / segs;
+  const int seg = static_cast<int>(blockIdx.x) - g * segs;
+  const int T = K / 32;
+  const int s0 = (seg * wpg + wave) * SPW;  // first step of this wavefront
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(Bp + static_cast<size_t>(g) * T * 1024), 0, T * 1024, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(Sp + static_cast<size_t>(g) * T * 256), 0, T * 256, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint4 *>(Ah), 0, (K / kBK) * AUnits<kSGroupRows>() * 16, 0x00020000);
+  // Lane l's activation fragment tg of step s: row 16 tg + (l & 15), unit
+  // 4 (s & 1) + (l >> 4) of k-tile s / 2 (the PrefillKernel operand order).
+  int aoff[TG][2];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) aoff[tg][h] = Swz(16 * tg + (lane & 15), 4 * h + (lane >> 4)) * 16;
+
+  typedef uint32_t u32x4e __attribute__((ext_vector_type(4)));
+  struct Slot {
+    u32x4e w, sz;
+    half8 a[TG];
+  };
+  Slot ring[WIN];
+  auto issue = [&](int i) __attribute__((always_inline)) {
+    Slot &sl = ring[i % WIN];
+    const int s = s0 + i;
+    sl.w = __builtin_bit_cast(u32x4e, __builtin_amdgcn_raw_buffer_load_b128(rb, s * 1024 + 16 * lane, 0, 2));
+    sl.sz = __builtin_bit_cast(u32x4e, __builtin_amdgcn_raw_buffer_load_b128(rs, s * 256 + 16 * (lane & 15), 0, 0));
+    const int kt = s >> 1;
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg)
+      sl.a[tg] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
+                                               ra, kt * (AUnits<kSGroupRows>() * 16) + aoff[tg][s & 1], 0, 0));
+  };
+#pragma unroll
+  for (int i = 0; i < WIN && i < SPW; ++i) issue(i);
+  // The epilogue's exponents and bias for the fragments x = wave, wave + wpg,
+  // ... this wavefront finishes (at most 4: wpg >= 4), loaded behind the
+  // first weights so their latency hides under the main loop.
+  constexpr int kMaxItems = (TG * 4 + 3) / 4;
+  int er[kMaxItems];
+  int4 ec[kMaxItems];
+  float4 bv[kMaxItems];
+#pragma unroll
+  for (int it = 0; it < kMaxItems; ++it) {
+    const int x = min(wave + it * wpg, TG * 4 - 1);
+    const int m = min(16 * (x >> 2) + (lane & 15), M - 1);
+    const int nc = min(kSGroupRows * g + 16 * (x & 3) + 4 * (lane >> 4), N - 4);
+    er[it] = row_exp[m];
+    ec[it] = *reinterpret_cast<const int4 *>(col_exp + nc);
+    bv[it] = bias != nullptr ? make_float4(bias[nc], bias[nc + 1], bias[nc + 2], bias[nc + 3])
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  const DequantConsts dq = MakeDequantConsts();
+  floatx4 acc[TG][4];
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[tg][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    Slot &sl = ring[i % WIN];
+    __asm__ volatile("" : "+v"(sl.w), "+v"(sl.sz));
+    const uint32_t wv[4] = {sl.w[0], sl.w[1], sl.w[2], sl.w[3]};
+    const uint32_t zv[4] = {sl.sz[0], sl.sz[1], sl.sz[2], sl.sz[3]};
+    half8 bf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      bf[j] = __builtin_bit_cast(half8, DequantWord(wv[j], RowFromSz<HAS_ZP>(zv[j]), dq));
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[tg][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], sl.a[tg], acc[tg][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + WIN < SPW) issue(i + WIN);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // The wavefronts' tiles meet in LDS; wavefront w then finishes the
+  // fragments x = (tg, j) = w, w + wpg, ..., adding the wavefronts' tiles in
+  // wavefront order. Lane l holds row 16 tg + (l & 15) and the 4 columns
+  // 64 g + 16 j + 4 (l >> 4) .. + 3.
+#pragma unroll
+  for (int tg = 0; tg < TG; ++tg)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sred[(wave * TG * 4 + tg * 4 + j) * 64 + lane] = acc[tg][j];
+  __syncthreads();
+  float *out = seg == 0 ? Y : partials + static_cast<size_t>(seg - 1) * M * N;
+#pragma unroll
+  for (int it = 0; it < kMaxItems; ++it) {
+    const int x = wave + it * wpg;
+    if (x >= TG * 4) break;
+    floatx4 sum = sred[x * 64 + lane];
+    for (int w = 1; w < wpg; ++w) sum += sred[(w * TG * 4 + x) * 64 + lane];
+    const int tg = x >> 2, j = x & 3;
+    const int m = 16 * tg + (lane & 15);
+    const int n = kSGroupRows * g + 16 * j + 4 * (lane >> 4);
+    const int ecv[4] = {ec[it].x, ec[it].y, ec[it].z, ec[it].w};
+    floatx4 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = __builtin_amdgcn_ldexpf(sum[q], -(er[it] + ecv[q]));
+    const bool ok = m < M && n < N;
+    if (H != nullptr) {
+      // gate/up pairs (columns n, n + 1 and n + 2, n + 3): H columns n / 2, n / 2 + 1
+      const int half_n = N >> 1;
+      const auto hr = __builtin_amdgcn_make_buffer_rsrc(H, 0, M * half_n * 4, 0x00020000);
+      typedef unsigned int u32x2 __attribute__((vector_size(8)));
+      const u32x2 hv = {__float_as_uint(SiluMul(v[0], v[1])), __float_as_uint(SiluMul(v[2], v[3]))};
+      __builtin_amdgcn_raw_buffer_store_b64(hv, hr, ok ? (m * half_n + (n >> 1)) * 4 : M * half_n * 4, 0, 0);
+    } else {
+      if (bias != nullptr) {
+        v[0] += bv[it].x;
+        v[1] += bv[it].y;
+        v[2] += bv[it].z;
+        v[3] += bv[it].w;
+      }
+      const auto yr = __builtin_amdgcn_make_buffer_rsrc(out, 0, M * N * 4, 0x00020000);
+      typedef unsigned int u32x4 __attribute__((vector_size(16)));
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), yr,
+                                             ok ? (m * N + n) * 4 : M * N * 4, 0, 0);
+    }
+  }
+}
+
+struct StreamShape {
+  int segs, wpg, spw;
+};
+
+// K segments, wavefronts per workgroup and steps per wavefront (segs * wpg *
+// spw = K / 32): the fewest segments whose workgroups cover 85% of the CUs
+// (else the most that leave a workgroup at least 16 steps), then 8
+// wavefronts before 4 and the longest spw in {16, 8, 4}.
+inline StreamShape PickStreamShape(const WeightView &w, int segs_req, int spw_req) {
+  const int64_t groups = (w.N + kSGroupRows - 1) / kSGroupRows;
+  const int T = static_cast<int>(w.K / 32);
+  if (segs_req > 0 && spw_req > 0) {
+    const int per = segs_req * spw_req;
+    return StreamShape{segs_req, T % per == 0 ? T / per : 0, spw_req};
+  }
+  auto fit = [](int per) {
+    for (int wpg : {8, 4})
+      for (int spw : {16, 8, 4})
+        if (wpg * spw == per) return StreamShape{0, wpg, spw};
+    return StreamShape{0, 0, 0};
+  };
+  StreamShape best{0, 0, 0};
+  for (int segs = 1; segs <= kMaxSplits; ++segs) {
+    if (T % segs != 0) continue;
+    StreamShape sh = fit(T / segs);
+    if (sh.wpg == 0) continue;
+    sh.segs = segs;
+    best = sh;
+    if (groups * segs * 100 >= static_cast<int64_t>(w.num_cus) * 85) break;
+  }
+  return best;
+}
+
+template <bool HAS_ZP, int TG, int SPW>
+hipError_t LaunchStreamT(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, float *P,
+                         float *H, const int *row_exp, const float *bias, const StreamShape &sh,
+                         hipStream_t s) {
+  const int64_t groups = (w.N + kSGroupRows - 1) / kSGroupRows;
+  const size_t lds = static_cast<size_t>(sh.wpg) * TG * 4 * 64 * 16;
+  hipLaunchKernelGGL((StreamKernel<HAS_ZP, TG, SPW, 4>), dim3(static_cast<unsigned>(groups * sh.segs)),
+                     dim3(64 * sh.wpg), lds, s, Ah, w.Bp, w.Sp, Y, P, H, row_exp, w.col_exp, bias,
+                     static_cast<int>(M), static_cast<int>(w.N), static_cast<int>(w.K), sh.segs,
+                     sh.wpg);
+  return hipGetLastError();
+}
+
+template <bool HAS_ZP, int TG>
+hipError_t LaunchStreamTG(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, float *P,
+                          float *H, const int *row_exp, const float *bias, const StreamShape &sh,
+                          hipStream_t s) {
+  switch (sh.spw) {
+  case 4: return LaunchStreamT<HAS_ZP, TG, 4>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
+  case 8: return LaunchStreamT<HAS_ZP, TG, 8>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
+  case 16: return LaunchStreamT<HAS_ZP, TG, 16>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+template <bool HAS_ZP>
+hipError_t LaunchStreamZp(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, float *P,
+                          float *H, const int *row_exp, const float *bias, const StreamShape &sh,
+                          hipStream_t s) {
+  switch ((M + 15) / 16) {
+  case 2: return LaunchStreamTG<HAS_ZP, 2>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
+  case 3: return LaunchStreamTG<HAS_ZP, 3>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
+  case 4: return LaunchStreamTG<HAS_ZP, 4>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
+  default: return hipErrorInvalidValue;
+  }
+}
+
 // Splits of a prefill launch: enough workgroups for one per CU when the
 // tiles alone do not fill the chip, each split at least 8 k-tiles long.
 inline int PrefillSplits(const WeightView &w, int64_t M) {
@@ -1141,12 +1369,56 @@ size_t PrefillPartialBytes(const WeightView &w, int64_t M) {
   return static_cast<size_t>(PrefillSplits(w, M) - 1) * static_cast<size_t>(M) * w.N * 4;
 }
 
+bool StreamSupportsM(const WeightView &w, int64_t M) {
+  return M >= 17 && M <= 64 && PrefillSupportsShape(w) && w.K <= (int64_t{1} << 23) &&
+         PickStreamShape(w, 0, 0).segs > 0;
+}
+
+size_t StreamPartialBytes(const WeightView &w, int64_t M, int segs) {
+  return static_cast<size_t>(std::max(segs, 1) - 1) * static_cast<size_t>(M) * w.N * 4;
+}
+
 } // namespace
 
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M) {
   size_t partial = PartialBytes(w, M, PickShape(w, M));
   if (PrefillSupportsM(w, M)) partial = std::max(partial, PrefillPartialBytes(w, M));
+  if (StreamSupportsM(w, M))
+    partial = std::max(partial, StreamPartialBytes(w, M, PickStreamShape(w, 0, 0).segs));
   return AImageBytes(w, M) + RowExpBytes(M) + partial;
+}
+
+bool StreamSupports(const WeightView &w, int64_t M) { return StreamSupportsM(w, M); }
+
+size_t StreamWorkspaceBytes(const WeightView &w, int64_t M, int segs, int spw) {
+  const StreamShape sh = PickStreamShape(w, segs, spw);
+  return AImageBytes(w, M) + RowExpBytes(M) + StreamPartialBytes(w, M, sh.segs);
+}
+
+// ConvertA (64-row tiling), the streaming kernel, and the ordered reduction
+// of the segments' partial sums when K is split.
+hipError_t LaunchStream(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                        hipStream_t s, float *H, const float *gamma, float eps, const float *bias,
+                        int segs, int spw) {
+  const StreamShape sh = PickStreamShape(w, segs, spw);
+  if (!StreamSupportsM(w, M) || sh.segs < 1 || sh.wpg < 1 || sh.wpg > 8 || sh.segs > kMaxSplits ||
+      sh.segs * sh.wpg * sh.spw != w.K / 32)
+    return hipErrorInvalidValue;
+  uint4 *Ah = static_cast<uint4 *>(work);
+  int *row_exp = reinterpret_cast<int *>(static_cast<char *>(work) + AImageBytes(w, M));
+  float *P = reinterpret_cast<float *>(static_cast<char *>(work) + AImageBytes(w, M) +
+                                       RowExpBytes(M));
+  hipError_t e = gamma != nullptr
+                     ? LaunchConvertA<kSGroupRows, true>(w, M, A, Ah, row_exp, s, gamma, eps)
+                     : LaunchConvertA<kSGroupRows, false>(w, M, A, Ah, row_exp, s, nullptr, 0.0f);
+  if (e != hipSuccess) return e;
+  float *Hk = sh.segs == 1 ? H : nullptr;
+  const float *bk = sh.segs == 1 ? bias : nullptr;
+  e = w.zp != nullptr ? LaunchStreamZp<true>(w, M, Ah, Y, P, Hk, row_exp, bk, sh, s)
+                      : LaunchStreamZp<false>(w, M, Ah, Y, P, Hk, row_exp, bk, sh, s);
+  if (e != hipSuccess || sh.segs == 1) return e;
+  return DispatchReduce(sh.segs - 1, Y, P, M * w.N, s, H,
+                        std::make_integer_sequence<int, kMaxSplits - 1>{}, bias, w.N);
 }
 
 bool PrefillSupports(const WeightView &w, int64_t M) { return PrefillSupportsM(w, M); }
@@ -1254,6 +1526,10 @@ hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, 
                       hipStream_t s, float *H, const float *gamma, float eps, const float *bias,
                       bool *bias_done) {
   if (bias_done != nullptr) *bias_done = false;
+  if (StreamSupportsM(w, M)) {
+    if (bias_done != nullptr) *bias_done = bias != nullptr;
+    return LaunchStream(w, M, A, Y, work, s, H, gamma, eps, bias, 0, 0);
+  }
   if (UsePrefill(w, M)) {
     if (bias_done != nullptr) *bias_done = bias != nullptr;
     return LaunchPrefillGemm(w, M, A, Y, work, s, H, gamma, eps, bias, PrefillSplits(w, M));
@@ -1262,5 +1538,7 @@ hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, 
 }
 
 bool GemmUsesPrefill(const WeightView &w, int64_t M) { return UsePrefill(w, M); }
+
+bool GemmUsesStream(const WeightView &w, int64_t M) { return StreamSupportsM(w, M); }
 
 } // namespace mnb

@@ -166,14 +166,15 @@ hipError_t LaunchSumPartials(float *Y, const float *P, int64_t mn, int parts, fl
 // holds GemmWorkspaceBytes(w, M) bytes of device memory: A scaled per row by
 // a power of two and rounded to fp16, the rows' exponents, then the partial
 // sums of a split-K launch.
-// The prefill kernel (128 x 256 tiles over the plan's re-laid weights) serves
-// M >= 65 when the plan holds them; it adds `bias` (N floats) in its
-// epilogue and then sets *bias_done. Otherwise GemmKernel (BM x 128 tiles
-// over the original layout) serves.
+// On a plan holding the re-laid weights, StreamKernel serves 17 <= M <= 64
+// and the prefill kernel (128 x 256 tiles) M >= 65 where its tiles fill the
+// CUs; both add `bias` (N floats) themselves and then set *bias_done.
+// Otherwise GemmKernel (BM x 128 tiles over the original layout) serves.
 hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                       hipStream_t s, float *H = nullptr, const float *gamma = nullptr,
                       float eps = 0.0f, const float *bias = nullptr, bool *bias_done = nullptr);
 bool GemmUsesPrefill(const WeightView &w, int64_t M);
+bool GemmUsesStream(const WeightView &w, int64_t M);
 // The prefill kernel forced (any M >= 1 on a plan holding the re-laid
 // weights; split-K when its tiles alone do not fill the CUs); adds `bias`
 // in its epilogue and sets *bias_done.
@@ -181,6 +182,17 @@ hipError_t LaunchPrefill(const WeightView &w, int64_t M, const float *A, float *
                          hipStream_t s, float *H = nullptr, const float *gamma = nullptr,
                          float eps = 0.0f, const float *bias = nullptr, bool *bias_done = nullptr);
 bool PrefillSupports(const WeightView &w, int64_t M);
+// Small-M prefill (17 <= M <= 64) streaming the prefill kernel's re-laid
+// weights once: ConvertA, StreamKernel over (64-row group, K segment)
+// workgroups, and the ordered reduction of the segments when K is split.
+// segs / spw (K segments, 32-k steps per wavefront) pick the shape, 0 for
+// the default; `work` holds StreamWorkspaceBytes(w, M, segs, spw) bytes.
+// Adds `bias` itself.
+bool StreamSupports(const WeightView &w, int64_t M);
+size_t StreamWorkspaceBytes(const WeightView &w, int64_t M, int segs, int spw);
+hipError_t LaunchStream(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                        hipStream_t s, float *H, const float *gamma, float eps, const float *bias,
+                        int segs, int spw);
 // The prefill kernel's weight layout: whether the plan's shape can use it,
 // its byte sizes (Bp returned, Sp through sp_bytes), and the plan-time
 // re-layout from B, scales, zero points and col_exp.
