@@ -690,8 +690,9 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   case 1:
     switch (PickDecodeKernel(plan, M, work, work_bytes)) {
     case kDecM1:
-      e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0, H, gamma, eps);
+      e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0, H, gamma, eps, dBias);
       fused = true;
+      bias_done = dBias != nullptr;
       if (e == hipErrorInvalidValue && H != nullptr) {
         // no shape with paired rows for this plan: plain launch, then the pass
         e = mnb::LaunchGemvM1(plan->view, dA, Ys, s, 0, 0, nullptr, gamma, eps);
@@ -699,8 +700,9 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
       }
       break;
     case kDecFrag:
-      e = mnb::LaunchDecodeFrag(plan->view, M, dA, Ys, work, s, H);
+      e = mnb::LaunchDecodeFrag(plan->view, M, dA, Ys, work, s, H, 0, 0, dBias);
       fused = true;
+      bias_done = dBias != nullptr;
       break;
     case kDecMfma:
       e = mnb::LaunchGemvMfma(plan->view, M, dA, Ys, work, s, H);
@@ -891,7 +893,7 @@ int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, 
   case MNB_KERNEL_GEMV_M1: shape_ok = p0 <= 1024 && one_of(p1, {0, 1, 2, 4, 8}); break;
   case MNB_KERNEL_GEMV_SMALL_M: shape_ok = p0 <= 8 && one_of(p1, {0, 4, 8}); break;
   case MNB_KERNEL_GEMV_MFMA: shape_ok = p0 <= 2 && p1 <= 8; break;
-  case MNB_KERNEL_DECODE_FRAG: shape_ok = one_of(p0, {0, 1, 2, 4, 8}) && p1 <= 2; break;
+  case MNB_KERNEL_DECODE_FRAG: shape_ok = p0 <= 8 && p1 <= 2; break;
   case MNB_KERNEL_GEMM: shape_ok = one_of(p0, {0, 32, 64, 128}) && p1 <= 16; break;
   case MNB_KERNEL_PREFILL: shape_ok = p0 <= 16 && p1 == 0; break;
   case MNB_KERNEL_STREAM: shape_ok = p0 <= 16 && one_of(p1, {0, 4, 8, 16}) && (p0 == 0) == (p1 == 0); break;

@@ -154,8 +154,8 @@ template <bool HAS_ZP, int SPB, int U, int WIN>
 __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
     const uint8_t *__restrict__ Bp, const float *__restrict__ Sd, const uint32_t *__restrict__ Zd,
     const uint4 *__restrict__ img, const int *__restrict__ exps, float *__restrict__ Y,
-    float *__restrict__ partials, float *__restrict__ H, int M, int N, int K, int nb, int log2_bs,
-    int segs, int wpg) {
+    float *__restrict__ partials, float *__restrict__ H, const float *__restrict__ bias, int M,
+    int N, int K, int nb, int log2_bs, int segs, int wpg) {
   __shared__ float red[kMaxWaves * 16 * 64];  // 32 KiB: [wave][slice * 4 + v][lane]
   constexpr int kSteps = U * kUnitSteps;
   const int lane = threadIdx.x & 63;
@@ -302,6 +302,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
       const int half_n = N >> 1;
       if ((c & 1) == 0 && tok < M && n < N) H[tok * half_n + (n >> 1)] = SiluMul(sum, other);
     } else {
+      if (bias != nullptr) sum += bias[min(n, N - 1)];  // one run: the bias input is added here
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), ry,
                                             tok < M && n < N ? (tok * N + n) * 4 : y_end, 0, 0);
     }
@@ -375,31 +376,31 @@ inline size_t ExpBytes(const WeightView &w) {
 
 template <bool HAS_ZP, int SPB, int U>
 hipError_t LaunchMain(const WeightView &w, int64_t M, const uint4 *img, const int *exps, float *Y,
-                      float *P, float *H, const Shape &sh, hipStream_t s) {
+                      float *P, float *H, const float *bias, const Shape &sh, hipStream_t s) {
   const int64_t groups = (w.N + 63) / 64;
   constexpr int kWin = 4;
   hipLaunchKernelGGL((DecodeFragKernel<HAS_ZP, SPB, U, kWin>),
                      dim3(static_cast<unsigned>(groups * sh.segs)), dim3(64 * sh.wpg), 0, s, w.Bp,
-                     w.Sd, w.Zd, img, exps, Y, P, H, static_cast<int>(M), static_cast<int>(w.N),
+                     w.Sd, w.Zd, img, exps, Y, P, H, bias, static_cast<int>(M), static_cast<int>(w.N),
                      static_cast<int>(w.K), static_cast<int>(w.nb), w.log2_bs, sh.segs, sh.wpg);
   return hipGetLastError();
 }
 
 template <bool HAS_ZP, int SPB>
 hipError_t LaunchU(const WeightView &w, int64_t M, const uint4 *img, const int *exps, float *Y,
-                   float *P, float *H, const Shape &sh, hipStream_t s) {
-  return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2>(w, M, img, exps, Y, P, H, sh, s)
-                                : LaunchMain<HAS_ZP, SPB, 1>(w, M, img, exps, Y, P, H, sh, s);
+                   float *P, float *H, const float *bias, const Shape &sh, hipStream_t s) {
+  return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2>(w, M, img, exps, Y, P, H, bias, sh, s)
+                                : LaunchMain<HAS_ZP, SPB, 1>(w, M, img, exps, Y, P, H, bias, sh, s);
 }
 
 template <bool HAS_ZP>
 hipError_t LaunchZp(const WeightView &w, int64_t M, const uint4 *img, const int *exps, float *Y,
-                    float *P, float *H, const Shape &sh, hipStream_t s) {
+                    float *P, float *H, const float *bias, const Shape &sh, hipStream_t s) {
   switch (std::min(w.block_size / 32, kUnitSteps)) {
-  case 1: return LaunchU<HAS_ZP, 1>(w, M, img, exps, Y, P, H, sh, s);
-  case 2: return LaunchU<HAS_ZP, 2>(w, M, img, exps, Y, P, H, sh, s);
-  case 4: return LaunchU<HAS_ZP, 4>(w, M, img, exps, Y, P, H, sh, s);
-  default: return LaunchU<HAS_ZP, 8>(w, M, img, exps, Y, P, H, sh, s);
+  case 1: return LaunchU<HAS_ZP, 1>(w, M, img, exps, Y, P, H, bias, sh, s);
+  case 2: return LaunchU<HAS_ZP, 2>(w, M, img, exps, Y, P, H, bias, sh, s);
+  case 4: return LaunchU<HAS_ZP, 4>(w, M, img, exps, Y, P, H, bias, sh, s);
+  default: return LaunchU<HAS_ZP, 8>(w, M, img, exps, Y, P, H, bias, sh, s);
   }
 }
 
@@ -438,7 +439,8 @@ size_t DecodeFragWorkspaceBytes(const WeightView &w, int64_t M, int wpg, int uni
 }
 
 hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
-                            hipStream_t s, float *H, int wpg, int units_per_wave) {
+                            hipStream_t s, float *H, int wpg, int units_per_wave,
+                            const float *bias) {
   const df::Shape sh = df::PickShape(w, wpg, units_per_wave);
   const int units = static_cast<int>(w.K / df::kUnitK);
   if (sh.wpg < 1 || sh.wpg > df::kMaxWaves || sh.segs < 1 ||
@@ -451,12 +453,13 @@ hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, floa
                      exps, static_cast<int>(M), static_cast<int>(w.K));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // One run per group: the kernel writes Y (or H) itself.
+  // One run per group: the kernel writes Y (or H) itself and adds the bias.
   float *Hk = sh.segs == 1 ? H : nullptr;
-  e = w.zp != nullptr ? df::LaunchZp<true>(w, M, img, exps, Y, P, Hk, sh, s)
-                      : df::LaunchZp<false>(w, M, img, exps, Y, P, Hk, sh, s);
+  const float *bk = sh.segs == 1 ? bias : nullptr;
+  e = w.zp != nullptr ? df::LaunchZp<true>(w, M, img, exps, Y, P, Hk, bk, sh, s)
+                      : df::LaunchZp<false>(w, M, img, exps, Y, P, Hk, bk, sh, s);
   if (e != hipSuccess || sh.segs == 1) return e;
-  return LaunchSumPartials(Y, P, M * w.N, sh.segs - 1, H, s);
+  return LaunchSumPartials(Y, P, M * w.N, sh.segs - 1, H, s, bias, w.N);
 }
 
 } // namespace mnb

@@ -155,7 +155,8 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
                                                      int chunk_shift, int row_bytes,
                                                      int zp_row_bytes, int G,
                                                      float *__restrict__ H,
-                                                     const float *__restrict__ gamma, float eps) {
+                                                     const float *__restrict__ gamma, float eps,
+                                                     const float *__restrict__ bias) {
   extern __shared__ float4 lds4[];
   const int nchunks = K >> 5;
   const int tid = threadIdx.x, nthreads = blockDim.x;
@@ -356,6 +357,7 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
     if (lane < R && (lane & 1) == 0 && wr0 + lane < rows)
       H[(row0 + wr0 + lane) >> 1] = SiluMul(mine, other);
   } else if (lane < R && wr0 + lane < rows) {
+    if (bias != nullptr) mine += bias[row0 + wr0 + lane];  // MatMulNBits input 5
     Y[row0 + wr0 + lane] = mine;
   }
 }
@@ -424,7 +426,7 @@ inline Shape PickShape(const WeightView &w, int cpl, int G, int R) {
 
 template <int CPL, int R, bool HAS_ZP>
 hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s, const Shape &sh,
-                   float *H, const float *gamma, float eps) {
+                   float *H, const float *gamma, float eps, const float *bias) {
   const bool full = (w.K / 32) == 64 * CPL;
   const bool quads = (w.nb % 4) == 0;
   const dim3 grid(static_cast<unsigned>(sh.grid)), block(static_cast<unsigned>(sh.waves * 64));
@@ -434,10 +436,10 @@ hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s,
 #define MNB_M1_LAUNCH(FULLV, PWV)                                                                  \
   if (gamma != nullptr)                                                                            \
     hipLaunchKernelGGL((GemvM1Kernel<CPL, R, FULLV, HAS_ZP, PWV, true>), grid, block, sh.lds, s,  \
-                       A, w.B, w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G, H, gamma, eps);    \
+                       A, w.B, w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G, H, gamma, eps, bias);\
   else                                                                                             \
     hipLaunchKernelGGL((GemvM1Kernel<CPL, R, FULLV, HAS_ZP, PWV, false>), grid, block, sh.lds, s, \
-                       A, w.B, w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G, H, gamma, eps)
+                       A, w.B, w.scales, w.zp, Y, K, N, nb, cs, rb, zb, sh.G, H, gamma, eps, bias)
   if (full) {
     if (quads) MNB_M1_LAUNCH(true, 4);
     else MNB_M1_LAUNCH(true, 1);
@@ -451,7 +453,7 @@ hipError_t LaunchT(const WeightView &w, const float *A, float *Y, hipStream_t s,
 
 template <int CPL, bool HAS_ZP>
 hipError_t LaunchC(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R,
-                   float *H, const float *gamma, float eps) {
+                   float *H, const float *gamma, float eps, const float *bias) {
   Shape sh = PickShape(w, CPL, G, R);
   if (H != nullptr && (sh.R < 2 || (sh.G & 1) != 0)) {
     // Gate/up epilogue: an even number of rows per wavefront and per band.
@@ -464,13 +466,13 @@ hipError_t LaunchC(const WeightView &w, const float *A, float *Y, hipStream_t s,
   if (sh.waves < 1 || sh.waves > kMaxWaves || sh.lds > 160 * 1024 || sh.R > kRMax)
     return hipErrorInvalidValue;
   switch (sh.R) {
-  case 1: return LaunchT<CPL, 1, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps);
-  case 2: return LaunchT<CPL, 2, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps);
+  case 1: return LaunchT<CPL, 1, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps, bias);
+  case 2: return LaunchT<CPL, 2, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps, bias);
   case 4:
-    if constexpr (kRMax >= 4) return LaunchT<CPL, 4, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps);
+    if constexpr (kRMax >= 4) return LaunchT<CPL, 4, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps, bias);
     return hipErrorInvalidValue;
   case 8:
-    if constexpr (kRMax >= 8) return LaunchT<CPL, 8, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps);
+    if constexpr (kRMax >= 8) return LaunchT<CPL, 8, HAS_ZP>(w, A, Y, s, sh, H, gamma, eps, bias);
     return hipErrorInvalidValue;
   default: return hipErrorInvalidValue;
   }
@@ -478,16 +480,16 @@ hipError_t LaunchC(const WeightView &w, const float *A, float *Y, hipStream_t s,
 
 template <bool HAS_ZP>
 hipError_t LaunchZ(const WeightView &w, const float *A, float *Y, hipStream_t s, int G, int R,
-                   float *H, const float *gamma, float eps) {
+                   float *H, const float *gamma, float eps, const float *bias) {
   switch ((w.K / 32 + 63) / 64) {
-  case 1: return LaunchC<1, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
-  case 2: return LaunchC<2, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
-  case 3: return LaunchC<3, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
-  case 4: return LaunchC<4, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
-  case 5: return LaunchC<5, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
-  case 6: return LaunchC<6, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
-  case 7: return LaunchC<7, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
-  default: return LaunchC<8, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps);
+  case 1: return LaunchC<1, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps, bias);
+  case 2: return LaunchC<2, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps, bias);
+  case 3: return LaunchC<3, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps, bias);
+  case 4: return LaunchC<4, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps, bias);
+  case 5: return LaunchC<5, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps, bias);
+  case 6: return LaunchC<6, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps, bias);
+  case 7: return LaunchC<7, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps, bias);
+  default: return LaunchC<8, HAS_ZP>(w, A, Y, s, G, R, H, gamma, eps, bias);
   }
 }
 
@@ -508,9 +510,9 @@ bool GemvM1Supports(const WeightView &w) {
 
 hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
                         int band_rows, int rows_per_wave, float *H, const float *gamma,
-                        float eps) {
-  return w.zp ? m1::LaunchZ<true>(w, A, Y, s, band_rows, rows_per_wave, H, gamma, eps)
-              : m1::LaunchZ<false>(w, A, Y, s, band_rows, rows_per_wave, H, gamma, eps);
+                        float eps, const float *bias) {
+  return w.zp ? m1::LaunchZ<true>(w, A, Y, s, band_rows, rows_per_wave, H, gamma, eps, bias)
+              : m1::LaunchZ<false>(w, A, Y, s, band_rows, rows_per_wave, H, gamma, eps, bias);
 }
 
 } // namespace mnb

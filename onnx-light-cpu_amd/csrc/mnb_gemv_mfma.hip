@@ -409,7 +409,9 @@ __global__ __launch_bounds__(64 * kWaves) void GemvMfmaKernel(
 template <bool VEC>
 __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
                                                          const float *__restrict__ P, int64_t mn,
-                                                         int parts, float *__restrict__ H) {
+                                                         int parts, float *__restrict__ H,
+                                                         const float *__restrict__ bias,
+                                                         int64_t N) {
   constexpr int kBatch = 16;
   if constexpr (VEC) {
     const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
@@ -424,6 +426,10 @@ __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
 #pragma unroll
       for (int q = 0; q < kBatch; ++q)
         if (p + q < parts) y += v[q];
+    }
+    if (bias != nullptr) {  // after the sum, as a separate bias pass; N % 4 == 0 here
+      const int64_t n = i % N;
+      y += floatx4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
     }
     if (H != nullptr) {
       // gate/up pairs (N even, so a pair never straddles rows)
@@ -444,6 +450,7 @@ __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
       for (int q = 0; q < kBatch; ++q)
         if (p + q < parts) y += v[q];
     }
+    if (bias != nullptr) y += bias[i % N];
     if (H != nullptr) {
       // mn is even: lanes i and i ^ 1 are both in range, in the same wavefront
       const float other = PairSwap(y);
@@ -549,17 +556,17 @@ hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, f
 }
 
 hipError_t LaunchSumPartials(float *Y, const float *P, int64_t mn, int parts, float *H,
-                             hipStream_t s) {
+                             hipStream_t s, const float *bias, int64_t N) {
   const bool vec = (mn % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(P) % 16) == 0 &&
-                   (reinterpret_cast<uintptr_t>(H) % 8) == 0;
+                   (reinterpret_cast<uintptr_t>(H) % 8) == 0 && (bias == nullptr || N % 4 == 0);
   if (vec)
     hipLaunchKernelGGL(mf::SumPartialsKernel<true>,
                        dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0, s, Y, P,
-                       mn, parts, H);
+                       mn, parts, H, bias, N);
   else
     hipLaunchKernelGGL(mf::SumPartialsKernel<false>, dim3(static_cast<unsigned>((mn + 255) / 256)),
-                       dim3(256), 0, s, Y, P, mn, parts, H);
+                       dim3(256), 0, s, Y, P, mn, parts, H, bias, N);
   return hipGetLastError();
 }
 

@@ -121,9 +121,12 @@ hipError_t LaunchGemvSmallMShape(const WeightView &w, int64_t M, const float *A,
 // RMSNorm input (M = 1 GEMV, GEMM): with gamma (K floats, 16-byte aligned)
 // the launch multiplies RMSNorm(A) = A / sqrt(mean_k(A^2) + eps) * gamma
 // instead of A; both compute the rows' mean squares themselves.
+// bias (N floats, MatMulNBits input 5, not with H) is added to each row's sum
+// before its store.
 hipError_t LaunchGemvM1(const WeightView &w, const float *A, float *Y, hipStream_t s,
                         int band_rows, int rows_per_wave, float *H = nullptr,
-                        const float *gamma = nullptr, float eps = 0.0f);
+                        const float *gamma = nullptr, float eps = 0.0f,
+                        const float *bias = nullptr);
 bool GemvM1Supports(const WeightView &w);
 
 // Decode GEMV for 2 <= M <= 16 on fp16 MFMA with exact products (each
@@ -146,8 +149,9 @@ hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, f
 // DecodeFragWorkspaceBytes(w, M, 0, 0) bytes: the split activation image, the
 // per-unit exponents and the partial sums of runs 1.. (one pre-pass kernel,
 // the main kernel, and the ordered partial-sum pass when K is split over
-// several workgroups). wpg (wavefronts per workgroup: 1, 2, 4 or 8) and
-// units_per_wave (1 or 2; a unit is 256 k): 0 picks.
+// several workgroups). wpg (wavefronts per workgroup, 1 to 8) and
+// units_per_wave (1 or 2; a unit is 256 k): 0 picks. bias (N floats, not
+// with H) is added by the main kernel's stores or the partial-sum pass.
 bool DecodeFragLayoutWanted(const WeightView &w);
 size_t DecodeFragScaleBytes(const WeightView &w, size_t *zd_bytes);
 hipError_t LaunchDecodeFragRelayout(const WeightView &w, float *Sd, uint32_t *Zd, hipStream_t s);
@@ -156,11 +160,11 @@ size_t DecodeFragWorkspaceBytes(const WeightView &w, int64_t M, int wpg = 0,
                                 int units_per_wave = 0);
 hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                             hipStream_t s, float *H = nullptr, int wpg = 0,
-                            int units_per_wave = 0);
+                            int units_per_wave = 0, const float *bias = nullptr);
 // Y += P[0] + ... + P[parts - 1] over mn elements, in that order (then the
 // gate/up activation into H when H is not null).
 hipError_t LaunchSumPartials(float *Y, const float *P, int64_t mn, int parts, float *H,
-                             hipStream_t s);
+                             hipStream_t s, const float *bias = nullptr, int64_t N = 1);
 
 // Prefill GEMM on fp16 MFMA, any M, K % 64 == 0, block_size >= 32. `work`
 // holds GemmWorkspaceBytes(w, M) bytes of device memory: A scaled per row by
