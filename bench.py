@@ -41,11 +41,11 @@ ROTATION_BYTES = 1 << 30
 
 # HBM bytes per launch of the headline kernel (GemvM1Kernel on c2 M=1), from
 # two rocprofv3 --pmc passes over `bench.py --only decode,gemm,sweep,copy
-# --eager --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15526.5 KiB and
+# --eager --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15525.7 KiB and
 # WRITE_SIZE 80.0 KiB per dispatch, each scaled by what the same counter reads
-# for the copy leg's 512 MiB device copy (FETCH_SIZE 262156.8 KiB -> x1.99990,
+# for the copy leg's 512 MiB device copy (FETCH_SIZE 262155.5 KiB -> x1.99992,
 # WRITE_SIZE 524288.0 KiB -> x1.00000). Re-measure when the kernel changes.
-GEMV_M1_C2_TRAFFIC_BYTES = round((15526.5 * (524288.0 / 262156.8) + 80.0) * 1024)
+GEMV_M1_C2_TRAFFIC_BYTES = round((15525.7 * (524288.0 / 262155.5) + 80.0) * 1024)
 
 
 def parse_args():
@@ -573,6 +573,17 @@ def main():
         print(f"# reference: dense fp16 torch.matmul c4 shape: "
               f"{gemm['reference_fp16_gemm']['us_per_launch']:.1f} us, "
               f"{gemm['reference_fp16_gemm']['TFLOPs']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+        # the small-M end of the GEMM path (17 <= M <= 64: the weight-streaming
+        # kernel) on the c4 and c2 weights, over >= 1 GiB of rotated copies
+        gemm["small_m"] = []
+        for cname, M in (("c4", 32), ("c4", 64), ("c2", 32)):
+            q = W.CONFIGS[cname].projections[0]
+            r = decode_leg(torch, pkg, dev, q, M, max(3, args.steps // 4), 2, 19 + M, stream)
+            gemm["small_m"].append({"config": cname, "M": M, "kernel": r["kernel"],
+                                    "us_per_launch": r["us_per_launch"], "GBps": r["GBps"],
+                                    "TFLOPs": q.flops(M) / (r["us_per_launch"] * 1e-6) / 1e12})
+            print(f"# small-M gemm {cname} M={M}: {r['us_per_launch']:.2f} us, {r['GBps']:.0f} GB/s",
+                  file=sys.stderr, flush=True)
     sweep = []
     if "sweep" in legs:
         # the configs, then one GPU's shard of c2 and c3 under 8-way tensor
