@@ -345,8 +345,9 @@ struct Shape {
 // whose workgroups still cover 85% of the CUs, then U = 2 before U = 1 and
 // the largest wpg of at least 4 (else any). Measured on MI355X at M = 16
 // (kernel alone): c2 one run of 8 x 2 units 10.5 us (two runs of 4 x 2:
-// 10.7); c1 four runs of 4 x 1 5.7 us (two runs of 4 x 2: 7.1); c3 seven
-// runs of 4 x 2 12.6 us (fourteen of 4 x 1: 12.9).
+// 10.7); c1 four runs of 4 x 1 5.7 us (two runs of 4 x 2: 7.1); c3 (56
+// units) four runs of 7 x 2, one workgroup per CU, 17.9 us per call
+// against 18.5 for seven runs of 4 x 2 (1.75 workgroups per CU).
 inline Shape PickShape(const WeightView &w, int wpg_req, int u_req) {
   const int64_t groups = (w.N + 63) / 64;
   const int units = static_cast<int>(w.K / kUnitK);
@@ -363,7 +364,7 @@ inline Shape PickShape(const WeightView &w, int wpg_req, int u_req) {
     if (segs < units && groups * segs * 100 < static_cast<int64_t>(w.num_cus) * 85) continue;
     for (int min_wpg : {4, 1})
       for (int U : {2, 1})
-        for (int wpg : {8, 4, 2, 1})
+        for (int wpg : {8, 7, 6, 5, 4, 3, 2, 1})
           if (wpg >= min_wpg && wpg * U == per) return Shape{wpg, U, segs};
   }
   return sh;

@@ -1069,11 +1069,21 @@ PrefillKernel(const uint4 *__restrict__ Ah, const uint8_t *__restrict__ Bp,
 // added in segment order by SplitReduceKernel.
 constexpr int kSGroupRows = 64;
 
-template <bool HAS_ZP, int TG, int SPW, int WIN>
+//
+// CVT: the wavefront converts its own activations instead of reading the
+// image (no ConvertAKernel launch; used for small fragment counts, see
+// StreamConverts): it loads A's fp32 values for its SPW steps first (L2-
+// resident, ahead of the weights), reduces each row's largest magnitude over
+// its own k range across the four lanes that hold the row, scales by 2^f and
+// rounds to fp16 as ConvertAKernel does, and scales its tiles by 2^-f before
+// the wavefronts' tiles meet. A finer exponent than the row's, so the
+// operands are ConvertAKernel's except where those fall into fp16
+// subnormals.
+template <bool HAS_ZP, int TG, int SPW, int WIN, bool CVT>
 __global__ __launch_bounds__(512) void StreamKernel(
-    const uint4 *__restrict__ Ah, const uint8_t *__restrict__ Bp, const uint8_t *__restrict__ Sp,
-    float *__restrict__ Y, float *__restrict__ partials, float *__restrict__ H,
-    const int *__restrict__ row_exp, const int *__restrict__ col_exp,
+    const uint4 *__restrict__ Ah, const float *__restrict__ A, const uint8_t *__restrict__ Bp,
+    const uint8_t *__restrict__ Sp, float *__restrict__ Y, float *__restrict__ partials,
+    float *__restrict__ H, const int *__restrict__ row_exp, const int *__restrict__ col_exp,
     const float *__restrict__ bias, int M, int N, int K, int segs, int wpg) {
   extern __shared__ floatx4 sred[];  // [wave][tg * 4 + j][lane]
   const int lane = threadIdx.x & 63;
@@ -1097,9 +1107,28 @@ __global__ __launch_bounds__(512) void StreamKernel(
     for (int h = 0; h < 2; ++h) aoff[tg][h] = Swz(16 * tg + (lane & 15), 4 * h + (lane >> 4)) * 16;
 
   typedef uint32_t u32x4e __attribute__((ext_vector_type(4)));
+  typedef float f32x4e __attribute__((ext_vector_type(4)));
+  // CVT: the wavefront's fp32 activations, [step][tg] pairs of 4 k (k order
+  // 0..3, 4..7 of the lane's 8), loaded before anything else.
+  f32x4e alo[CVT ? SPW : 1][CVT ? TG : 1], ahi[CVT ? SPW : 1][CVT ? TG : 1];
+  if constexpr (CVT) {
+    const __amdgpu_buffer_rsrc_t rA =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, M * K * 4, 0x00020000);
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg) {
+      const int m = 16 * tg + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        // rows past M read past the end of the buffer: zeros
+        const int off = m < M ? (m * K + 32 * (s0 + i) + 8 * (lane >> 4)) * 4 : M * K * 4;
+        alo[i][tg] = __builtin_bit_cast(f32x4e, __builtin_amdgcn_raw_buffer_load_b128(rA, off, 0, 0));
+        ahi[i][tg] = __builtin_bit_cast(f32x4e, __builtin_amdgcn_raw_buffer_load_b128(rA, off + 16, 0, 0));
+      }
+    }
+  }
   struct Slot {
     u32x4e w, sz;
-    half8 a[TG];
+    half8 a[CVT ? 1 : TG];
   };
   Slot ring[WIN];
   auto issue = [&](int i) __attribute__((always_inline)) {
@@ -1107,11 +1136,13 @@ __global__ __launch_bounds__(512) void StreamKernel(
     const int s = s0 + i;
     sl.w = __builtin_bit_cast(u32x4e, __builtin_amdgcn_raw_buffer_load_b128(rb, s * 1024 + 16 * lane, 0, 2));
     sl.sz = __builtin_bit_cast(u32x4e, __builtin_amdgcn_raw_buffer_load_b128(rs, s * 256 + 16 * (lane & 15), 0, 0));
-    const int kt = s >> 1;
+    if constexpr (!CVT) {
+      const int kt = s >> 1;
 #pragma unroll
-    for (int tg = 0; tg < TG; ++tg)
-      sl.a[tg] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
-                                               ra, kt * (AUnits<kSGroupRows>() * 16) + aoff[tg][s & 1], 0, 0));
+      for (int tg = 0; tg < TG; ++tg)
+        sl.a[tg] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 ra, kt * (AUnits<kSGroupRows>() * 16) + aoff[tg][s & 1], 0, 0));
+    }
   };
 #pragma unroll
   for (int i = 0; i < WIN && i < SPW; ++i) issue(i);
@@ -1127,12 +1158,41 @@ __global__ __launch_bounds__(512) void StreamKernel(
     const int x = min(wave + it * wpg, TG * 4 - 1);
     const int m = min(16 * (x >> 2) + (lane & 15), M - 1);
     const int nc = min(kSGroupRows * g + 16 * (x & 3) + 4 * (lane >> 4), N - 4);
-    er[it] = row_exp[m];
+    er[it] = CVT ? 0 : row_exp[m];
     ec[it] = *reinterpret_cast<const int4 *>(col_exp + nc);
     bv[it] = bias != nullptr ? make_float4(bias[nc], bias[nc + 1], bias[nc + 2], bias[nc + 3])
                              : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   __builtin_amdgcn_sched_barrier(0);
+
+  // CVT: each row's exponent over this wavefront's k range (the row's values
+  // sit in lanes r, r + 16, r + 32, r + 48), then the fp16 fragments.
+  half8 af[CVT ? SPW : 1][CVT ? TG : 1];
+  int fw[CVT ? TG : 1];
+  if constexpr (CVT) {
+#pragma unroll
+    for (int tg = 0; tg < TG; ++tg) {
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < SPW; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          amax = fmaxf(amax, fmaxf(fabsf(alo[i][tg][c]), fabsf(ahi[i][tg][c])));
+      amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+      const int f = RangeExponent(amax, kRowExpTarget);
+      fw[tg] = f;
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        auto sc = [f](float v) { return __builtin_amdgcn_ldexpf(v, f); };
+        const f32x4e x = alo[i][tg], y = ahi[i][tg];
+        // k order [0,4,1,5,2,6,3,7], the order DequantWord produces
+        af[i][tg] = __builtin_bit_cast(
+            half8, make_uint4(PackHalf2(sc(x[0]), sc(y[0])), PackHalf2(sc(x[1]), sc(y[1])),
+                              PackHalf2(sc(x[2]), sc(y[2])), PackHalf2(sc(x[3]), sc(y[3]))));
+      }
+    }
+  }
 
   const DequantConsts dq = MakeDequantConsts();
   floatx4 acc[TG][4];
@@ -1151,10 +1211,16 @@ __global__ __launch_bounds__(512) void StreamKernel(
     for (int j = 0; j < 4; ++j)
       bf[j] = __builtin_bit_cast(half8, DequantWord(wv[j], RowFromSz<HAS_ZP>(zv[j]), dq));
 #pragma unroll
-    for (int tg = 0; tg < TG; ++tg)
+    for (int tg = 0; tg < TG; ++tg) {
+      half8 a;
+      if constexpr (CVT)
+        a = af[i][tg];
+      else
+        a = sl.a[tg];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        acc[tg][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], sl.a[tg], acc[tg][j], 0, 0, 0);
+        acc[tg][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], a, acc[tg][j], 0, 0, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (i + WIN < SPW) issue(i + WIN);
     __builtin_amdgcn_sched_barrier(0);
@@ -1167,7 +1233,14 @@ __global__ __launch_bounds__(512) void StreamKernel(
 #pragma unroll
   for (int tg = 0; tg < TG; ++tg)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sred[(wave * TG * 4 + tg * 4 + j) * 64 + lane] = acc[tg][j];
+    for (int j = 0; j < 4; ++j) {
+      floatx4 t = acc[tg][j];
+      if constexpr (CVT) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t[q] = __builtin_amdgcn_ldexpf(t[q], -fw[tg]);
+      }
+      sred[(wave * TG * 4 + tg * 4 + j) * 64 + lane] = t;
+    }
   __syncthreads();
   float *out = seg == 0 ? Y : partials + static_cast<size_t>(seg - 1) * M * N;
 #pragma unroll
@@ -1182,7 +1255,7 @@ __global__ __launch_bounds__(512) void StreamKernel(
     const int ecv[4] = {ec[it].x, ec[it].y, ec[it].z, ec[it].w};
     floatx4 v;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[q] = __builtin_amdgcn_ldexpf(sum[q], -(er[it] + ecv[q]));
+    for (int q = 0; q < 4; ++q) v[q] = __builtin_amdgcn_ldexpf(sum[q], -((CVT ? 0 : er[it]) + ecv[q]));
     const bool ok = m < M && n < N;
     if (H != nullptr) {
       // gate/up pairs (columns n, n + 1 and n + 2, n + 3): H columns n / 2, n / 2 + 1
@@ -1239,39 +1312,58 @@ inline StreamShape PickStreamShape(const WeightView &w, int segs_req, int spw_re
   return best;
 }
 
+// Whether the wavefronts convert their own activations: no RMSNorm input, at
+// most 8 fragments per wavefront, and no more workgroups than CUs. Measured
+// per call against ConvertAKernel + the image: c4 M = 17 / 32 10.45 -> 8.79
+// / 10.76 -> 10.11 us; slower where the fragments or the workgroups are more
+// (c4 M = 48 / 64 +0.4 / +1.2 us, c3 M = 32 with 8 steps per wavefront
+// +4.9 us, c5 qkv M = 32 with 1.5 workgroups per CU +1.4 us).
+inline bool StreamConverts(const WeightView &w, int64_t M, const StreamShape &sh, bool rms) {
+  const int64_t wgs = (w.N + kSGroupRows - 1) / kSGroupRows * sh.segs;
+  return !rms && (M + 15) / 16 * sh.spw <= 8 && wgs <= w.num_cus;
+}
+
 template <bool HAS_ZP, int TG, int SPW>
-hipError_t LaunchStreamT(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, float *P,
-                         float *H, const int *row_exp, const float *bias, const StreamShape &sh,
-                         hipStream_t s) {
+hipError_t LaunchStreamT(const WeightView &w, int64_t M, const uint4 *Ah, const float *A, float *Y,
+                         float *P, float *H, const int *row_exp, const float *bias,
+                         const StreamShape &sh, hipStream_t s) {
   const int64_t groups = (w.N + kSGroupRows - 1) / kSGroupRows;
   const size_t lds = static_cast<size_t>(sh.wpg) * TG * 4 * 64 * 16;
-  hipLaunchKernelGGL((StreamKernel<HAS_ZP, TG, SPW, 4>), dim3(static_cast<unsigned>(groups * sh.segs)),
-                     dim3(64 * sh.wpg), lds, s, Ah, w.Bp, w.Sp, Y, P, H, row_exp, w.col_exp, bias,
-                     static_cast<int>(M), static_cast<int>(w.N), static_cast<int>(w.K), sh.segs,
-                     sh.wpg);
+  const dim3 grid(static_cast<unsigned>(groups * sh.segs)), block(64 * sh.wpg);
+  const int m = static_cast<int>(M), n = static_cast<int>(w.N), k = static_cast<int>(w.K);
+  if (A != nullptr) {
+    if constexpr (TG * SPW <= 16)
+      hipLaunchKernelGGL((StreamKernel<HAS_ZP, TG, SPW, 4, true>), grid, block, lds, s, Ah, A, w.Bp,
+                         w.Sp, Y, P, H, row_exp, w.col_exp, bias, m, n, k, sh.segs, sh.wpg);
+    else
+      return hipErrorInvalidValue;
+  } else {
+    hipLaunchKernelGGL((StreamKernel<HAS_ZP, TG, SPW, 4, false>), grid, block, lds, s, Ah, A, w.Bp,
+                       w.Sp, Y, P, H, row_exp, w.col_exp, bias, m, n, k, sh.segs, sh.wpg);
+  }
   return hipGetLastError();
 }
 
 template <bool HAS_ZP, int TG>
-hipError_t LaunchStreamTG(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, float *P,
-                          float *H, const int *row_exp, const float *bias, const StreamShape &sh,
-                          hipStream_t s) {
+hipError_t LaunchStreamTG(const WeightView &w, int64_t M, const uint4 *Ah, const float *A, float *Y,
+                          float *P, float *H, const int *row_exp, const float *bias,
+                          const StreamShape &sh, hipStream_t s) {
   switch (sh.spw) {
-  case 4: return LaunchStreamT<HAS_ZP, TG, 4>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
-  case 8: return LaunchStreamT<HAS_ZP, TG, 8>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
-  case 16: return LaunchStreamT<HAS_ZP, TG, 16>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
+  case 4: return LaunchStreamT<HAS_ZP, TG, 4>(w, M, Ah, A, Y, P, H, row_exp, bias, sh, s);
+  case 8: return LaunchStreamT<HAS_ZP, TG, 8>(w, M, Ah, A, Y, P, H, row_exp, bias, sh, s);
+  case 16: return LaunchStreamT<HAS_ZP, TG, 16>(w, M, Ah, A, Y, P, H, row_exp, bias, sh, s);
   default: return hipErrorInvalidValue;
   }
 }
 
 template <bool HAS_ZP>
-hipError_t LaunchStreamZp(const WeightView &w, int64_t M, const uint4 *Ah, float *Y, float *P,
-                          float *H, const int *row_exp, const float *bias, const StreamShape &sh,
-                          hipStream_t s) {
+hipError_t LaunchStreamZp(const WeightView &w, int64_t M, const uint4 *Ah, const float *A, float *Y,
+                          float *P, float *H, const int *row_exp, const float *bias,
+                          const StreamShape &sh, hipStream_t s) {
   switch ((M + 15) / 16) {
-  case 2: return LaunchStreamTG<HAS_ZP, 2>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
-  case 3: return LaunchStreamTG<HAS_ZP, 3>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
-  case 4: return LaunchStreamTG<HAS_ZP, 4>(w, M, Ah, Y, P, H, row_exp, bias, sh, s);
+  case 2: return LaunchStreamTG<HAS_ZP, 2>(w, M, Ah, A, Y, P, H, row_exp, bias, sh, s);
+  case 3: return LaunchStreamTG<HAS_ZP, 3>(w, M, Ah, A, Y, P, H, row_exp, bias, sh, s);
+  case 4: return LaunchStreamTG<HAS_ZP, 4>(w, M, Ah, A, Y, P, H, row_exp, bias, sh, s);
   default: return hipErrorInvalidValue;
   }
 }
@@ -1370,7 +1462,7 @@ size_t PrefillPartialBytes(const WeightView &w, int64_t M) {
 }
 
 bool StreamSupportsM(const WeightView &w, int64_t M) {
-  return M >= 17 && M <= 64 && PrefillSupportsShape(w) && w.K <= (int64_t{1} << 23) &&
+  return M >= 17 && M <= 64 && PrefillSupportsShape(w) && w.K <= (int64_t{1} << 22) &&
          PickStreamShape(w, 0, 0).segs > 0;
 }
 
@@ -1408,14 +1500,18 @@ hipError_t LaunchStream(const WeightView &w, int64_t M, const float *A, float *Y
   int *row_exp = reinterpret_cast<int *>(static_cast<char *>(work) + AImageBytes(w, M));
   float *P = reinterpret_cast<float *>(static_cast<char *>(work) + AImageBytes(w, M) +
                                        RowExpBytes(M));
-  hipError_t e = gamma != nullptr
-                     ? LaunchConvertA<kSGroupRows, true>(w, M, A, Ah, row_exp, s, gamma, eps)
-                     : LaunchConvertA<kSGroupRows, false>(w, M, A, Ah, row_exp, s, nullptr, 0.0f);
+  const bool cvt = StreamConverts(w, M, sh, gamma != nullptr);
+  hipError_t e = hipSuccess;
+  if (!cvt)
+    e = gamma != nullptr
+            ? LaunchConvertA<kSGroupRows, true>(w, M, A, Ah, row_exp, s, gamma, eps)
+            : LaunchConvertA<kSGroupRows, false>(w, M, A, Ah, row_exp, s, nullptr, 0.0f);
   if (e != hipSuccess) return e;
   float *Hk = sh.segs == 1 ? H : nullptr;
   const float *bk = sh.segs == 1 ? bias : nullptr;
-  e = w.zp != nullptr ? LaunchStreamZp<true>(w, M, Ah, Y, P, Hk, row_exp, bk, sh, s)
-                      : LaunchStreamZp<false>(w, M, Ah, Y, P, Hk, row_exp, bk, sh, s);
+  const float *Ak = cvt ? A : nullptr;
+  e = w.zp != nullptr ? LaunchStreamZp<true>(w, M, Ah, Ak, Y, P, Hk, row_exp, bk, sh, s)
+                      : LaunchStreamZp<false>(w, M, Ah, Ak, Y, P, Hk, row_exp, bk, sh, s);
   if (e != hipSuccess || sh.segs == 1) return e;
   return DispatchReduce(sh.segs - 1, Y, P, M * w.N, s, H,
                         std::make_integer_sequence<int, kMaxSplits - 1>{}, bias, w.N);
