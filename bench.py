@@ -143,7 +143,7 @@ def copy_leg(torch, dev, steps, warmup, stream):
 
 def stream_ceiling_leg(torch, pkg, dev, nbytes, steps, warmup, stream):
     """The HBM read ceiling for one launch of nbytes: mnb_stream_read (loads
-    only, 16 KiB contiguous records per wavefront) over as many rotated
+    only, 8 KiB contiguous records per wavefront) over as many rotated
     buffers as the headline leg, one launch each, graph-replayed."""
     import ctypes
     rot = max(2, -(-ROTATION_BYTES // nbytes))

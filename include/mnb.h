@@ -233,8 +233,8 @@ int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, 
 #define MNB_STREAM_OUT_WORDS 2048u
 
 /* HBM read ceiling probe: one launch that streams `bytes` (< 2^31) of device
- * memory at dSrc and nothing else (2048 wavefronts, each reading 16 KiB
- * contiguous records with sixteen 16-byte loads in flight), folding them into
+ * memory at dSrc and nothing else (2048 wavefronts, each reading 8 KiB
+ * contiguous records with eight 16-byte loads in flight), folding them into
  * dOut[0 .. MNB_STREAM_OUT_WORDS) so the loads are kept. A decode launch's
  * roofline fraction is reported next to this probe's rate over the same
  * bytes per launch. No counterpart in the reference. */

@@ -1,9 +1,14 @@
 // HBM read ceiling probe: one launch that only streams a buffer, the way the
-// fastest weight-streaming pattern measured on MI355X does (each wavefront
-// reads 16 KiB contiguous records with all sixteen 16-byte loads in flight,
-// 2048 wavefronts), folding the bytes into one word per wavefront so the
-// loads are kept. The decode kernels' roofline fraction is reported next to
-// what this probe reaches over the same number of bytes per launch.
+// fastest streaming pattern of a sweep on MI355X does, folding the bytes into
+// one word per wavefront so the loads are kept. The decode kernels' roofline
+// fraction is reported next to what this probe reaches over the same number
+// of bytes per launch. Sweep (31.5 MB per launch, 35 rotated buffers, graph
+// replays): records of 4 / 8 / 16 / 32 KiB per wavefront with all their
+// 16-byte loads in flight, 1024 to 8192 wavefronts, 256- to 1024-thread
+// workgroups, non-temporal or default loads; the fastest were 8 KiB records
+// over 2048 wavefronts in 256-thread workgroups with non-temporal loads
+// (6.40-6.49 us), 16 KiB records 6.9 us, default-policy loads 0.4-1.0 us
+// slower, 1024-thread workgroups slower still.
 #include "../../include/mnb.h"
 #include "mnb_kernels.h"
 
@@ -12,7 +17,7 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRecordBytes = 16384;
+constexpr int kRecordBytes = 8192;
 constexpr int kLoads = kRecordBytes / 1024;  // 16-byte loads per lane and record
 
 __global__ __launch_bounds__(256) void StreamReadKernel(const uint8_t *__restrict__ src,
