@@ -53,7 +53,7 @@ def _run_every_kernel(pkg, cuda, op, A):
     dA = torch.from_numpy(np.ascontiguousarray(A)).to(cuda)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     out = {}
-    for kernel in range(pkg.KERNEL_GEMV_M1, pkg.KERNEL_GENERIC + 1):
+    for kernel in range(pkg.KERNEL_GEMV_M1, pkg.KERNEL_GEMV_M1_FRAG + 1):
         n = ctypes.c_size_t()
         rc = L.mnb_kernel_workspace_bytes(op._plan, M, kernel, 0, 0, ctypes.byref(n))
         if rc == MNB_ERR_UNSUPPORTED:
@@ -84,7 +84,7 @@ def _check_coverage(pkg, ys, K):
 def _is_gemm(pkg, kernel, auto_path):
     if kernel == "auto":
         return auto_path == pkg.PATH_GEMM
-    return kernel in (pkg.KERNEL_GEMM, pkg.KERNEL_PREFILL)
+    return kernel in (pkg.KERNEL_GEMM, pkg.KERNEL_PREFILL, pkg.KERNEL_STREAM)
 
 
 @pytest.mark.parametrize("case", [c[0] for c in _cases("ref_matmul.npz")])

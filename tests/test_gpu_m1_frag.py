@@ -1,0 +1,147 @@
+"""GPU parity of the M = 1 MFMA decode kernel (GemvM1FragKernel).
+
+It multiplies each activation, split into three fp16 terms after a
+power-of-two scaling per 256-k unit, by the fp16 subnormals q 2^-24 of the
+nibbles on the matrix cores (exact products), applies the zero point through
+each block's activation sum and sums in fp32, so it is held to the decode
+tolerance, max|y - y64| / max|y64| <= 1e-5 against the fp64 oracle, and
+cross-checked against GemvM1Kernel (fp32 mixed FMA, same bound) and the
+reference-order fp32 oracle. Runs are deterministic.
+
+Every case prints its shape and launch shape before touching the GPU.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-5
+GATE_UP_TOL = 4e-5  # the fused SiLU's hardware exp2 / rcp, as the other gate/up routes
+
+
+def _weights(pkg, K, N, bs, zp, seed):
+    p = pkg.workloads.Projection("t", K, N, bs, zp, 1.0, 0.005, 0.02)
+    return pkg.workloads.make_weights(p, seed)
+
+
+@pytest.mark.parametrize("K,N,bs,zp,spws", [
+    (4096, 14336, 128, True, (0, 8, 16, 32)),  # c2: 224 groups, every launch shape
+    (4096, 4096, 32, False, (8,)),             # c1: a block scale per step, no zero points
+    (2048, 200, 64, True, (8, 16)),            # ragged last group (rows past N are zero)
+    (1024, 64, 256, False, (8, 32)),           # one group, a block per unit
+    (12288, 1000, 128, True, (32,)),           # long K: 12 wavefronts of 32 steps
+    (256, 96, 32, True, (8,)),                 # one unit, one wavefront
+])
+def test_m1_frag_vs_oracle_and_m1(pkg, orc, cuda, K, N, bs, zp, spws):
+    import torch
+    B, S, Z = _weights(pkg, K, N, bs, zp, seed=K + N + bs)
+    A = pkg.workloads.make_activations(1, K, 1.0, seed=K + 5)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    dA = torch.from_numpy(A).to(cuda)
+    y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
+    y32 = orc.matmul_nbits_ref_f32(A, B, S, Z, K, N, bs)
+    print(f"case m1-frag K={K} N={N} bs={bs} zp={zp} (GemvM1Kernel)", flush=True)
+    y_m1 = op.run_kernel(dA, pkg.KERNEL_GEMV_M1).cpu().numpy()
+    for spw in spws:
+        print(f"case m1-frag K={K} N={N} bs={bs} zp={zp} steps/wave={spw}", flush=True)
+        y1 = op.run_kernel(dA, pkg.KERNEL_GEMV_M1_FRAG, spw).cpu().numpy()
+        y2 = op.run_kernel(dA, pkg.KERNEL_GEMV_M1_FRAG, spw).cpu().numpy()
+        np.testing.assert_array_equal(y1, y2)
+        e64 = orc.normwise_max_error(y1, y64)
+        e32 = orc.normwise_max_error(y1, y32)
+        em1 = orc.normwise_max_error(y1, y_m1)
+        print(f"  normwise error: vs fp64 {e64:.2e}, vs reference fp32 {e32:.2e}, "
+              f"vs GemvM1Kernel {em1:.2e}")
+        assert e64 <= GEMV_TOL and e32 <= GEMV_TOL and em1 <= 2 * GEMV_TOL
+    op.release()
+
+
+def test_m1_frag_activation_range(pkg, orc, cuda):
+    """Rows whose values span 40 decades, a zero row (exact zeros), one
+    outlier 7 decades above the rest, fp32 subnormals and values near 1e30:
+    each held to the decode tolerance relative to its own largest output."""
+    import torch
+    K, N, bs = 2048, 160, 128
+    B, S, Z = _weights(pkg, K, N, bs, True, seed=77)
+    rng = np.random.default_rng(78)
+    rows = {
+        "40 decades": rng.standard_normal(K) * 10.0 ** rng.uniform(-20, 20, K),
+        "zero": np.zeros(K),
+        "outlier": np.where(np.arange(K) == 700, 1e4, rng.standard_normal(K) * 1e-3),
+        "subnormal": rng.standard_normal(K) * 1e-40,
+        "1e30": rng.standard_normal(K) * 1e30,
+    }
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    for name, a in rows.items():
+        A = a.astype(np.float32)[None, :]
+        print(f"case m1-frag-range K={K} N={N} bs={bs} row={name}", flush=True)
+        y = op.run_kernel(torch.from_numpy(A).to(cuda), pkg.KERNEL_GEMV_M1_FRAG).cpu().numpy()
+        assert np.isfinite(y).all()
+        if name == "zero":
+            assert np.all(y == 0.0)
+            continue
+        err = orc.normwise_max_error(y, orc.matmul_nbits_f64(A, B, S, Z, K, N, bs))
+        print(f"  normwise error {err:.2e}")
+        assert err <= GEMV_TOL, name
+    op.release()
+
+
+def test_m1_frag_auto_path_and_bias(pkg, orc, cuda):
+    """The automatic M = 1 path takes the kernel where its 64-row groups
+    cover most CUs, with the bias input added in its store; narrower weights
+    keep GemvM1Kernel."""
+    import torch
+    K, N, bs = 4096, 14336, 128
+    B, S, Z = _weights(pkg, K, N, bs, True, seed=5)
+    A = pkg.workloads.make_activations(1, K, 1.0, seed=6)
+    bias = np.random.default_rng(7).standard_normal(N).astype(np.float32)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    print(f"case m1-frag-auto K={K} N={N} kernel={op.kernel_name(1)}", flush=True)
+    assert op.kernel_name(1) == "GemvM1FragKernel"
+    dA = torch.from_numpy(A).to(cuda)
+    y_k = op.run_kernel(dA, pkg.KERNEL_GEMV_M1_FRAG).cpu().numpy()
+    np.testing.assert_array_equal(op(dA).cpu().numpy(), y_k)
+    yb = op(dA, bias=torch.from_numpy(bias).to(cuda)).cpu().numpy()
+    np.testing.assert_array_equal(yb, y_k + bias[None, :])
+    op.release()
+    narrow = pkg.MatMulNBits(K, 4096, 4, bs).prepare(*_weights(pkg, K, 4096, bs, True, seed=8))
+    assert narrow.kernel_name(1) == "GemvM1Kernel"
+    narrow.release()
+
+
+def test_m1_frag_gate_up_epilogue(pkg, orc, cuda):
+    """A gate/up plan wide enough for the kernel writes silu(gate) * up
+    itself (rows 2n, 2n + 1 of a 64-row group), within the gate/up routes'
+    bound against the fp64 oracle."""
+    import torch
+    K, I, bs = 2048, 7168, 64
+    p = pkg.workloads.Projection("g", K, I, bs, True, 1.0, 0.005, 0.02)
+    Bg, Sg, Zg = pkg.workloads.make_weights(p, 31)
+    Bu, Su, Zu = pkg.workloads.make_weights(p, 32)
+    fused = pkg.GateUpSiLU(K, I, 4, bs).prepare(Bg, Sg, Zg, Bu, Su, Zu)
+    A = pkg.workloads.make_activations(1, K, 1.0, seed=33)
+    print(f"case m1-frag-gate-up K={K} I={I} bs={bs} kernel={fused.kernel_name(1)}", flush=True)
+    assert fused.kernel_name(1) == "GemvM1FragKernel"
+    H = fused(torch.from_numpy(A).to(cuda)).cpu().numpy()
+    h64 = orc.gate_up_silu_f64(A, Bg, Sg, Zg, Bu, Su, Zu, K, I, bs)
+    err = orc.normwise_max_error(H, h64)
+    print(f"  normwise error vs fp64 {err:.2e}")
+    assert err <= GATE_UP_TOL
+    fused.release()
+
+
+def test_m1_frag_rejects(pkg, cuda):
+    """Shapes the kernel cannot serve are rejected with MNB_ERR_UNSUPPORTED
+    before any launch: M > 1, 512-k blocks, steps per wavefront that are not
+    8, 16 or 32 or that need more than 16 wavefronts."""
+    import torch
+    cases = [((1024, 64, 128), 2, 0), ((2048, 64, 512), 1, 0), ((1024, 64, 128), 1, 24),
+             ((8192, 64, 128), 1, 8)]
+    for (K, N, bs), M, spw in cases:
+        op = pkg.MatMulNBits(K, N, 4, bs).prepare(*_weights(pkg, K, N, bs, False, seed=3))
+        A = torch.zeros((M, K), device=cuda)
+        print(f"case m1-frag-reject K={K} N={N} bs={bs} M={M} spw={spw}", flush=True)
+        with pytest.raises(pkg.MatMulNBitsError) as ei:
+            op.run_kernel(A, pkg.KERNEL_GEMV_M1_FRAG, spw)
+        assert ei.value.status == 4
+        op.release()
