@@ -39,7 +39,7 @@ FP16_PEAK_TFLOPS = 2500.0
 METRIC = "MatMulNBits 4-bit: M=1 achieved HBM GB/s; M=2048 TFLOP/s; % roofline"
 ROTATION_BYTES = 1 << 30
 
-# HBM bytes per launch of the headline kernel (GemvM1FragKernel on c2 M=1),
+# HBM bytes per launch of the headline kernel (GemvFragKernel on c2 M=1),
 # from two rocprofv3 --pmc passes over `bench.py --only decode,copy --eager
 # --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15577.6 KiB and
 # WRITE_SIZE 56.0 KiB per dispatch, each scaled by what the same counter reads

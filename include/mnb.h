@@ -204,7 +204,7 @@ int mnb_select_path(const mnb_plan *plan, int64_t M, int *path);
 #define MNB_KERNEL_GEMV 7         /* GemvKernel: fp32 FMA fallback, M <= 16 */
 #define MNB_KERNEL_GENERIC 8      /* GenericKernel: any shape, one wavefront per output */
 #define MNB_KERNEL_STREAM 9       /* StreamKernel: 17 <= M <= 64, fp16 MFMA, fragment-ordered copy streamed once */
-#define MNB_KERNEL_GEMV_M1_FRAG 10 /* GemvM1FragKernel: M = 1, exact-product MFMA, fragment-ordered copy */
+#define MNB_KERNEL_GEMV_FRAG 10  /* GemvFragKernel: M <= 4, exact-product MFMA, fragment-ordered copy, A staged in LDS */
 
 /* Name of the main kernel mnb_run launches for M rows given workspace_bytes
  * of workspace ("GemvM1Kernel", "DecodeFragKernel", "PrefillKernel", ...;
@@ -220,9 +220,10 @@ const char *mnb_kernel_name(const mnb_plan *plan, int64_t M, size_t workspace_by
  * workgroup), GEMV_MFMA (16-row blocks per item, workgroups per CU),
  * DECODE_FRAG (wavefronts per workgroup, 256-k units per wavefront), GEMM
  * (tile height 32, 64 or 128; K splits), PREFILL (K splits), STREAM (K
- * segments, 32-k steps per wavefront; both or neither), GEMV_M1_FRAG
+ * segments, 32-k steps per wavefront; both or neither), GEMV_FRAG
  * (32-k steps per wavefront: 8, 16 or 32; weight records in flight per
- * wavefront: 4 or 8); GEMV and GENERIC take none. Plain (not gate/up) plans, no bias; MNB_ERR_UNSUPPORTED
+ * wavefront: 4 or 8; for M > 1 only 8 or 16 steps and 8 records); GEMV and
+ * GENERIC take none. Plain (not gate/up) plans, no bias; MNB_ERR_UNSUPPORTED
  * when the kernel cannot serve the plan or M, MNB_ERR_WORKSPACE below
  * mnb_kernel_workspace_bytes. No counterpart in the reference, whose
  * kernels are chosen inside the plan. */

@@ -37,7 +37,7 @@ STATUS = {
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_GENERIC, PATH_EXACT, PATH_PREFILL = 0, 1, 2, 3, 4, 5
 # MNB_KERNEL_* of include/mnb.h (mnb_run_kernel)
 (KERNEL_GEMV_M1, KERNEL_GEMV_SMALL_M, KERNEL_GEMV_MFMA, KERNEL_DECODE_FRAG, KERNEL_GEMM,
- KERNEL_PREFILL, KERNEL_GEMV, KERNEL_GENERIC, KERNEL_STREAM, KERNEL_GEMV_M1_FRAG) = range(1, 11)
+ KERNEL_PREFILL, KERNEL_GEMV, KERNEL_GENERIC, KERNEL_STREAM, KERNEL_GEMV_FRAG) = range(1, 11)
 
 
 class MnbDesc(ctypes.Structure):

@@ -552,7 +552,7 @@ static bool UsesFragDecode(const mnb_plan *plan, int64_t M) {
 
 // The decode kernel path 1 launches for M rows with `work_bytes` of workspace
 // at `work` (M <= 16).
-enum DecodeKernel { kDecM1, kDecM1Frag, kDecFrag, kDecMfma, kDecSmallM, kDecGemv };
+enum DecodeKernel { kDecM1, kDecGemvFrag, kDecFrag, kDecMfma, kDecSmallM, kDecGemv };
 
 // Rows per launch of the exact route (path 4): the decode kernels' limit.
 constexpr int64_t kExactGroupRows = 16;
@@ -563,11 +563,12 @@ static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
 }
 
 // Without the kernel's workspace, M >= 2 falls back to the fp32-FMA kernels.
-// M = 1 takes the MFMA kernel on the fragment-ordered copy where its 64-row
-// groups cover most CUs (not with a fused RMSNorm input), else GemvM1Kernel.
+// M <= 4 takes the LDS-staged MFMA kernel on the fragment-ordered copy where
+// its 64-row groups cover most CUs (not with a fused RMSNorm input); M = 1
+// otherwise GemvM1Kernel.
 static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void *work,
                                      size_t work_bytes, bool rms = false) {
-  if (M == 1 && !rms && mnb::GemvM1FragPreferred(plan->view)) return kDecM1Frag;
+  if (!rms && mnb::GemvFragPreferred(plan->view, M)) return kDecGemvFrag;
   if (M == 1 && mnb::GemvM1Supports(plan->view)) return kDecM1;
   if (UsesFragDecode(plan, M) &&
       HasWorkspace(work, work_bytes, mnb::DecodeFragWorkspaceBytes(plan->view, M)))
@@ -692,8 +693,8 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   switch (path) {
   case 1:
     switch (PickDecodeKernel(plan, M, work, work_bytes, gamma != nullptr)) {
-    case kDecM1Frag:
-      e = mnb::LaunchGemvM1Frag(plan->view, dA, Ys, s, 0, 0, H, dBias);
+    case kDecGemvFrag:
+      e = mnb::LaunchGemvFrag(plan->view, M, dA, Ys, s, 0, 0, H, dBias);
       fused = true;
       bias_done = dBias != nullptr;
       break;
@@ -822,7 +823,7 @@ const char *mnb_kernel_name(const mnb_plan *plan, int64_t M, size_t workspace_by
   case 1:
     switch (PickDecodeKernel(plan, M, work, work_bytes)) {
     case kDecM1: return "GemvM1Kernel";
-    case kDecM1Frag: return "GemvM1FragKernel";
+    case kDecGemvFrag: return "GemvFragKernel";
     case kDecFrag: return "DecodeFragKernel";
     case kDecMfma: return "GemvMfmaKernel";
     case kDecSmallM: return "GemvSmallMKernel";
@@ -842,7 +843,7 @@ const char *mnb_kernel_name(const mnb_plan *plan, int64_t M, size_t workspace_by
 static bool KernelServes(const mnb::WeightView &w, int64_t M, int kernel) {
   switch (kernel) {
   case MNB_KERNEL_GEMV_M1: return M == 1 && mnb::GemvM1Supports(w);
-  case MNB_KERNEL_GEMV_M1_FRAG: return M == 1 && mnb::GemvM1FragSupports(w);
+  case MNB_KERNEL_GEMV_FRAG: return mnb::GemvFragSupports(w, M);
   case MNB_KERNEL_GEMV_SMALL_M: return M >= 2 && mnb::GemvSmallMSupports(w, M);
   case MNB_KERNEL_GEMV_MFMA: return mnb::GemvMfmaSupports(w, M);
   case MNB_KERNEL_DECODE_FRAG: return mnb::DecodeFragSupports(w, M);
@@ -880,7 +881,7 @@ int mnb_kernel_workspace_bytes(const mnb_plan *plan, int64_t M, int kernel, int 
     *bytes = mnb::StreamWorkspaceBytes(w, M, p0, p1);
     return MNB_OK;
   case MNB_KERNEL_GEMV_M1:
-  case MNB_KERNEL_GEMV_M1_FRAG:
+  case MNB_KERNEL_GEMV_FRAG:
   case MNB_KERNEL_GEMV_SMALL_M:
   case MNB_KERNEL_GEMV:
   case MNB_KERNEL_GENERIC:
@@ -908,7 +909,7 @@ int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, 
   case MNB_KERNEL_GEMM: shape_ok = one_of(p0, {0, 32, 64, 128}) && p1 <= 16; break;
   case MNB_KERNEL_PREFILL: shape_ok = p0 <= 16 && p1 == 0; break;
   case MNB_KERNEL_STREAM: shape_ok = p0 <= 16 && one_of(p1, {0, 4, 8, 16}) && (p0 == 0) == (p1 == 0); break;
-  case MNB_KERNEL_GEMV_M1_FRAG: shape_ok = mnb::GemvM1FragShapeOk(plan->view, p0, p1); break;
+  case MNB_KERNEL_GEMV_FRAG: shape_ok = mnb::GemvFragShapeOk(plan->view, M, p0, p1); break;
   default: shape_ok = p0 == 0 && p1 == 0; break;
   }
   if (!shape_ok) return MNB_ERR_UNSUPPORTED;
@@ -925,7 +926,7 @@ int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, 
   hipError_t e = hipSuccess;
   switch (kernel) {
   case MNB_KERNEL_GEMV_M1: e = mnb::LaunchGemvM1(w, dA, dY, s, p0, p1); break;
-  case MNB_KERNEL_GEMV_M1_FRAG: e = mnb::LaunchGemvM1Frag(w, dA, dY, s, p0, p1, nullptr, nullptr); break;
+  case MNB_KERNEL_GEMV_FRAG: e = mnb::LaunchGemvFrag(w, M, dA, dY, s, p0, p1, nullptr, nullptr); break;
   case MNB_KERNEL_GEMV_SMALL_M: e = mnb::LaunchGemvSmallMShape(w, M, dA, dY, s, p0, p1, 0); break;
   case MNB_KERNEL_GEMV_MFMA: e = mnb::LaunchGemvMfmaShape(w, M, dA, dY, dWorkspace, s, p0, p1); break;
   case MNB_KERNEL_DECODE_FRAG: e = mnb::LaunchDecodeFrag(w, M, dA, dY, dWorkspace, s, nullptr, p0, p1); break;

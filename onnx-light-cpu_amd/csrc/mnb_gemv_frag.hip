@@ -1,0 +1,440 @@
+// Decode GEMV for 1 <= M <= 4 activation rows on fp16 MFMA, streaming the
+// plan's fragment-ordered weights.
+//
+// Role in the reference: the roadmap's `int4_gemv` / `int4_small_m` decode
+// side (docs/next_steps/2026/2026_08_qwen3_inference.rst:208-221): fp32
+// accumulation, weights never expanded, each weight byte streamed once; the
+// fp32 semantics are those of the reference engine's skinny-M product
+// (onnx_light_cpu/impl/math/gemm_kernel.cc:1208-1258).
+//
+// Why the matrix cores at M = 1. GemvM1Kernel spends one v_fma_mix_f32 per
+// nibble plus the bit operations that expose it, 1.6 VALU per nibble and 667
+// per wavefront at the c2 shape: on every CU the vector ALUs are busy for
+// about 60% of the time the weights take to stream. Here the products go to
+// the matrix cores, idle otherwise. Masking a packed word w with 0x000F000F
+// and 0x00F000F0, and w >> 8 with the same, leaves its eight nibbles as the
+// fp16 subnormals q 2^-24 (even k) and 16 q 2^-24 (odd k): exactly one lane's
+// B operand of v_mfma_f32_16x16x32_f16 (8 k values, in the order
+// [0,4,1,5,2,6,3,7]). That is 5 VALU per 8 nibbles; the MFMA keeps subnormal
+// operands and forms every product exactly (checked bit for bit on MI355X).
+//
+// Activations. Each wavefront first turns its own part of the fp32 rows (the
+// 256-k units of its steps) into LDS MFMA A operands. Per unit u and row m a
+// power of two 2^e brings the largest magnitude into [2^14, 2^15) (exact), and
+// each scaled value x is split into three fp16 terms, t0 = fp16(x), t1 =
+// fp16(x - t0), t2 = fp16(x - t0 - t1): the differences are exact in fp32 and
+// three 11-bit significands hold x's 24 bits, so x = t0 + t1 + t2 exactly for
+// every x not far below the unit's largest magnitude (absolute error at most
+// 2^-25, i.e. 2^-39 of it, for the rest). A-operand row 4 m + t holds term t
+// of activation row m (rows 4 m + 3 repeat term 0, rows of m >= M repeat row
+// 0; both are ignored), so one MFMA multiplies all terms of all rows and
+// lanes 16 m .. 16 m + 15 of its result hold row m's three partial sums of the
+// same 16 weight rows. Values at odd k are stored divided by 16 (exact),
+// undoing the odd nibbles' factor. Per quantization block b and row m the
+// wavefront also keeps S = 2^-24 sum_k x_k over the block, and per unit e
+// (scalars at M = 1, LDS tables otherwise). Per block, weight row and
+// activation row:
+//   y += 2^(24 - e) scale (C_0 + C_1 + C_2 - zp S)
+// with the 2^(24 - e) applied once per unit (exact). No workgroup barrier
+// precedes the stream: a wavefront only reads the operands it wrote itself.
+//
+// Mapping. One workgroup per group g of 64 weight rows and the whole of K; its
+// wavefront w takes SPW consecutive 32-k steps (whole units and blocks), i.e.
+// SPW records of the plan's fragment-ordered copy Bp (1 KiB each: lane l holds
+// the words of rows 64 g + 16 j + (l & 15), j = 0..3, at k = 32 s + 8 (l >> 4),
+// the B operands of four 16-row slices), with 16-byte non-temporal loads kept
+// WIN steps ahead; the activation loads go first, then the first WIN weight
+// records, then the staging arithmetic. Block scales and zero points come
+// from the plan's decode re-layout (Sd, Zd: per group and block, lane c's
+// float4 holds the scales of rows 64 g + 16 j + c, byte j of its word the zero
+// points). The wavefronts' row sums meet in LDS and are added in wavefront
+// order by one thread per output. No workspace; results do not depend on
+// scheduling.
+#include "mnb_decode_common.h"
+
+#include <algorithm>
+
+namespace mnb {
+namespace gf {
+
+using namespace dec;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kUnitK = 256;                 // k per activation exponent
+constexpr int kUnitSteps = kUnitK / 32;     // 32-k steps per unit
+constexpr int kTerms = 3;                   // fp16 terms per activation
+constexpr int kOpBytes = kTerms * 16;       // one row's three 16-byte operands
+constexpr int kMaxWaves = 16;
+constexpr size_t kLdsLimit = 150 * 1024;
+
+// LDS byte offsets for MT activation rows: the operand image (K / 32 steps,
+// each [quarter][row][term] 16-byte operands), the block sums (nb x MT
+// floats) and unit exponents (K / 256 x MT ints) when MT > 1, the wavefront
+// sums (waves x MT x 64 floats).
+struct LdsLayout {
+  int sums, exps, red, bytes;
+};
+__host__ __device__ inline LdsLayout Layout(int K, int nb, int waves, int mt) {
+  LdsLayout l;
+  l.sums = (K / 32) * 4 * mt * kOpBytes;
+  l.exps = l.sums + (mt > 1 ? nb * mt * 4 : 0);
+  l.red = l.exps + (mt > 1 ? (K / kUnitK) * mt * 4 : 0);
+  l.bytes = l.red + waves * mt * 256;
+  return l;
+}
+
+// SPB = 32-k steps per quantization block (bs / 32, 1..8); SPW = steps per
+// wavefront (whole units); WIN = weight records in flight per wavefront; MT =
+// activation rows the launch is built for (1, 2 or 4; M <= MT).
+template <bool HAS_ZP, int SPB, int SPW, int WIN, int MT>
+__global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
+    const float *__restrict__ A, const uint8_t *__restrict__ Bp, const float *__restrict__ Sd,
+    const uint32_t *__restrict__ Zd, float *__restrict__ Y, float *__restrict__ H,
+    const float *__restrict__ bias, int M, int N, int K, int nb) {
+  constexpr int kUnits = SPW / kUnitSteps;      // units of this wavefront
+  constexpr int kItems = kUnits * MT;           // (unit, row) staging items, 32 lanes each
+  constexpr int kPasses = (kItems + 1) / 2;     // two items per pass
+  constexpr int kBlocks = SPW / SPB;            // quantization blocks of this wavefront
+  constexpr int kBlocksPerUnit = kUnitSteps / SPB;
+  constexpr int kStepBytes = 4 * MT * kOpBytes; // image bytes per step
+  extern __shared__ uint4 lds16[];
+  char *lds = reinterpret_cast<char *>(lds16);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int waves = static_cast<int>(blockDim.x) >> 6;
+  const int g = blockIdx.x;
+  const int T = K >> 5;
+  const int c = lane & 15;
+  const int s0 = wave * SPW;           // first step of this wavefront
+  const int u0 = s0 / kUnitSteps;      // its first unit
+  const LdsLayout L = Layout(K, nb, waves, MT);
+  float *sums = reinterpret_cast<float *>(lds + L.sums);
+  int *exps = reinterpret_cast<int *>(lds + L.exps);
+  float *red = reinterpret_cast<float *>(lds + L.red);
+
+  // 1. This wavefront's activations, before every weight load: in pass p,
+  //    the 32 lanes of half h take the 8 values of quarter l & 31 of item
+  //    2 p + h = (unit, row) (clamped items re-read a valid one and store
+  //    nothing).
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, M * K * 4, 0x00020000);
+  floatx4 va[kPasses][2];
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    const int it = min(2 * p + (lane >> 5), kItems - 1);
+    const int ul = it / MT, m = min(it % MT, M - 1);
+    const int off = (m * K + (u0 + ul) * kUnitK + 8 * (lane & 31)) * 4;
+    va[p][0] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
+    va[p][1] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16, 0, 0));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. The first WIN weight records of this wavefront and their blocks'
+  //    scales and zero points.
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(Bp + static_cast<size_t>(g) * T * 1024), 0, T * 1024, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(Sd + static_cast<size_t>(g) * nb * 64), 0, nb * 256, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t *>(HAS_ZP ? Zd + static_cast<size_t>(g) * nb * 16 : Zd), 0,
+      HAS_ZP ? nb * 64 : 0, 0x00020000);
+  struct Slot {
+    u32x4 w;
+    floatx4 s;
+    uint32_t z;
+  };
+  Slot ring[WIN];
+  auto issue = [&](int i) __attribute__((always_inline)) {
+    Slot &sl = ring[i % WIN];
+    const int s = s0 + i;
+    sl.w = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, s * 1024 + 16 * lane, 0, kNonTemporal));
+    if (i % SPB == 0) {
+      const int blk = s / SPB;
+      sl.s = __builtin_bit_cast(floatx4,
+                                __builtin_amdgcn_raw_buffer_load_b128(rs, blk * 256 + 16 * c, 0, 0));
+      if constexpr (HAS_ZP) sl.z = __builtin_amdgcn_raw_buffer_load_b32(rz, blk * 64 + 4 * c, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < WIN && i < SPW; ++i) issue(i);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. Staging of this wavefront's own steps (no workgroup barrier: a
+  //    wavefront's LDS accesses execute in order): scale each (unit, row),
+  //    split into three fp16 terms, write the operands; the block sums (a
+  //    fixed butterfly over the block's lanes) and unit exponents go to
+  //    scalars (M = 1) or to the LDS tables.
+  float sb[MT == 1 ? kBlocks : 1];
+  int eu[MT == 1 ? kUnits : 1];
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fmaxf(fabsf(va[p][0][i]), fabsf(va[p][1][i])));
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const int e = RangeExponent(amax, 14);
+    half8 h[kTerms];
+    float ssum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = ldexpf(i < 4 ? va[p][0][i] : va[p][1][i - 4], e);
+      ssum += x;
+      const float xs = (i & 1) ? x * 0.0625f : x;
+      const _Float16 t0 = static_cast<_Float16>(xs);
+      const float r1 = __builtin_isfinite(xs) ? xs - static_cast<float>(t0) : 0.f;
+      const _Float16 t1 = static_cast<_Float16>(r1);
+      const _Float16 t2 = static_cast<_Float16>(r1 - static_cast<float>(t1));
+      const int o = (i & 3) * 2 + (i >> 2);  // [0,4,1,5,2,6,3,7]
+      h[0][o] = t0;
+      h[1][o] = t1;
+      h[2][o] = t2;
+    }
+#pragma unroll
+    for (int o = 1; o < 4 * SPB; o <<= 1) ssum += __shfl_xor(ssum, o, 64);
+    ssum *= 5.9604644775390625e-8f;  // 2^-24 (exact), before the block sums leave the lanes
+    const int it = 2 * p + (lane >> 5);
+    const int ul = it / MT, m = it % MT;
+    const int q = lane & 31;  // quarter of the unit
+    if (it < kItems && m < M) {
+      uint4 *dst = reinterpret_cast<uint4 *>(lds + ((u0 + ul) * kUnitSteps + (q >> 2)) * kStepBytes +
+                                             (q & 3) * (MT * kOpBytes) + m * kOpBytes);
+#pragma unroll
+      for (int t = 0; t < kTerms; ++t) dst[t] = __builtin_bit_cast(uint4, h[t]);
+      if constexpr (MT > 1) {
+        if (q == 0) exps[(u0 + ul) * MT + m] = e;
+        if ((q & (4 * SPB - 1)) == 0)
+          sums[((u0 + ul) * kBlocksPerUnit + q / (4 * SPB)) * MT + m] = ssum;
+      }
+    }
+    if constexpr (MT == 1) {
+#pragma unroll
+      for (int uh = 0; uh < 2; ++uh) {
+        if (2 * p + uh >= kUnits) continue;
+        eu[2 * p + uh] = __builtin_amdgcn_readlane(e, 32 * uh);
+#pragma unroll
+        for (int bb = 0; bb < kBlocksPerUnit; ++bb)
+          sb[(2 * p + uh) * kBlocksPerUnit + bb] =
+              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 32 * uh + 4 * SPB * bb));
+      }
+    }
+  }
+  // The image writes above precede the operand reads below.
+  __asm__ volatile("" ::: "memory");
+
+  // 4. The wavefront's steps. Lane l's A operand is term (l & 3) of row
+  //    (l & 15) >> 2 of quarter l >> 4 (term 3 -> 0, rows past M -> row 0);
+  //    lane l's results are row mc = l >> 4's (clamped: rows past M are
+  //    computed and not stored).
+  const int ma = min((lane & 15) >> 2, M - 1), ta = (lane & 3) == 3 ? 0 : (lane & 3);
+  const int mc = min(lane >> 4, M - 1);
+  const int a16 = (s0 * kStepBytes + (lane >> 4) * (MT * kOpBytes) + ma * kOpBytes + ta * 16) >> 4;
+  const floatx4 zero4 = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 tmp[4];
+  float racc[4], acc[4];  // per slice: the unit's sum, the wavefront's sum
+  floatx4 bsc = zero4;
+  uint32_t zw = 0x08080808u;  // zero points 8 without the input
+  float sbv = 0.f;
+  int ev = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    tmp[j] = zero4;
+    racc[j] = 0.f;
+    acc[j] = 0.f;
+  }
+  auto step = [&](int i) __attribute__((always_inline)) {
+    Slot &sl = ring[i % WIN];
+    // Pins the step's arithmetic here (left free, the compiler hoists work
+    // on later steps' registers into this one and waits for their loads).
+    // The operand's LDS index passes through the pin too, so its read is
+    // issued here and not hoisted to the top (a register quad per step).
+    int ai = a16;
+    __asm__ volatile("" : "+v"(sl.w), "+v"(ai));
+    const half8 a = __builtin_bit_cast(half8, lds16[ai + i * (kStepBytes / 16)]);
+    if (i % SPB == 0) {
+      bsc = sl.s;
+      if constexpr (HAS_ZP) zw = sl.z;
+      if constexpr (MT > 1) sbv = sums[((s0 + i) / SPB) * MT + mc];
+    }
+    if constexpr (MT > 1) {
+      if (i % kUnitSteps == 0) ev = exps[((s0 + i) / kUnitSteps) * MT + mc];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = sl.w[j], w8 = w >> 8;
+      const u32x4 qv = u32x4{w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u};
+      tmp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8, qv),
+                                                      i % SPB == 0 ? zero4 : tmp[j], 0, 0, 0);
+    }
+    if ((i + 1) % SPB == 0) {
+      const float sbi = MT == 1 ? sb[MT == 1 ? i / SPB : 0] : sbv;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // rows 4 mc .. 4 mc + 2 of the tile: the three terms' sums
+        float t = (tmp[j][0] + tmp[j][1]) + tmp[j][2];
+        const float zp = static_cast<float>((zw >> (8 * j)) & 0xFFu);
+        t = fmaf(-zp, sbi, t);
+        racc[j] = fmaf(bsc[j], t, racc[j]);
+      }
+      // Only some lanes store these sums: unpinned, the compiler sinks the
+      // block and unit arithmetic into that branch after the last step and
+      // keeps every block's tiles live until then.
+      __asm__ volatile("" : "+v"(racc[0]), "+v"(racc[1]), "+v"(racc[2]), "+v"(racc[3]));
+    }
+    if ((i + 1) % kUnitSteps == 0) {
+      const int e = MT == 1 ? eu[MT == 1 ? i / kUnitSteps : 0] : ev;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[j] += __builtin_amdgcn_ldexpf(racc[j], 24 - e);
+        racc[j] = 0.f;
+      }
+      __asm__ volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    step(i);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + WIN < SPW) issue(i + WIN);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // 5. Wavefront sums in LDS (lanes 16 m + c hold rows 16 j + c of
+  //    activation row m), added in wavefront order; one thread per output.
+  if ((lane >> 4) < M) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[(wave * MT + (lane >> 4)) * 64 + 16 * j + c] = acc[j];
+  }
+  __syncthreads();
+  // whole wavefronts per iteration (M * 64 and the block are multiples of 64)
+  for (int idx = static_cast<int>(threadIdx.x); idx < M * 64; idx += static_cast<int>(blockDim.x)) {
+    const int m = idx >> 6, r = idx & 63;
+    float y = red[m * 64 + r];
+    for (int w = 1; w < waves; ++w) y += red[(w * MT + m) * 64 + r];
+    const int n = 64 * g + r;
+    if (H != nullptr) {
+      // gate/up pairs: rows 2 n', 2 n' + 1 in lanes r, r ^ 1 (N even)
+      const float other = PairSwap(y);
+      if ((r & 1) == 0 && n < N) H[m * (N >> 1) + (n >> 1)] = SiluMul(y, other);
+    } else if (n < N) {
+      if (bias != nullptr) y += bias[n];  // MatMulNBits input 5
+      Y[m * N + n] = y;
+    }
+  }
+}
+
+inline int RowsBuilt(int64_t M) { return M == 1 ? 1 : (M == 2 ? 2 : 4); }
+
+template <bool HAS_ZP, int SPB>
+hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipStream_t s, int spw,
+                     int win, float *H, const float *bias) {
+  const int K = static_cast<int>(w.K), N = static_cast<int>(w.N), nb = static_cast<int>(w.nb);
+  const int waves = K / 32 / spw;
+  const int mt = RowsBuilt(M);
+  const int lds = Layout(K, nb, waves, mt).bytes;
+  const dim3 grid(static_cast<unsigned>((w.N + 63) / 64)), block(static_cast<unsigned>(64 * waves));
+#define MNB_GF_LAUNCH(SPWV, WINV, MTV)                                                          \
+  hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, WINV, MTV>), grid, block, lds, s, A,   \
+                     w.Bp, w.Sd, w.Zd, Y, H, bias, M, N, K, nb)
+  if (mt > 1) {
+    // more rows: window 8, 8 or 16 steps per wavefront (checked by the caller)
+    if (mt == 2) {
+      if (spw == 8) MNB_GF_LAUNCH(8, 8, 2);
+      else MNB_GF_LAUNCH(16, 8, 2);
+    } else {
+      if (spw == 8) MNB_GF_LAUNCH(8, 8, 4);
+      else MNB_GF_LAUNCH(16, 8, 4);
+    }
+  } else if (win == 8) {
+    switch (spw) {
+    case 8: MNB_GF_LAUNCH(8, 8, 1); break;
+    case 16: MNB_GF_LAUNCH(16, 8, 1); break;
+    default: MNB_GF_LAUNCH(32, 8, 1); break;
+    }
+  } else {
+    switch (spw) {
+    case 8: MNB_GF_LAUNCH(8, 4, 1); break;
+    case 16: MNB_GF_LAUNCH(16, 4, 1); break;
+    default: MNB_GF_LAUNCH(32, 4, 1); break;
+    }
+  }
+#undef MNB_GF_LAUNCH
+  return hipGetLastError();
+}
+
+template <bool HAS_ZP>
+hipError_t LaunchZp(const WeightView &w, int M, const float *A, float *Y, hipStream_t s, int spw,
+                    int win, float *H, const float *bias) {
+  switch (w.block_size / 32) {
+  case 1: return LaunchSpw<HAS_ZP, 1>(w, M, A, Y, s, spw, win, H, bias);
+  case 2: return LaunchSpw<HAS_ZP, 2>(w, M, A, Y, s, spw, win, H, bias);
+  case 4: return LaunchSpw<HAS_ZP, 4>(w, M, A, Y, s, spw, win, H, bias);
+  default: return LaunchSpw<HAS_ZP, 8>(w, M, A, Y, s, spw, win, H, bias);
+  }
+}
+
+inline bool ShapeFits(const WeightView &w, int64_t M, int spw, int win) {
+  const int T = static_cast<int>(w.K / 32);
+  if (spw != 8 && spw != 16 && spw != 32) return false;
+  if (win != 4 && win != 8) return false;
+  if (M > 1 && (spw == 32 || win != 8)) return false;  // the launches built for M > 1
+  if (M > 2 && w.block_size == 32 && spw != 8) return false;  // 16 steps spill registers
+  if (T % spw != 0 || T / spw > kMaxWaves) return false;
+  return static_cast<size_t>(
+             Layout(static_cast<int>(w.K), static_cast<int>(w.nb), T / spw, RowsBuilt(M)).bytes) <=
+         kLdsLimit;
+}
+
+// Steps per wavefront: 16 where that gives at most 16 wavefronts, else 32
+// (M = 1), else 8 (K below 512); window 8. Measured on MI355X at M = 1
+// (interleaved medians; steps / window): c2 16 / 8 7.31 us, 16 / 4 7.42,
+// 8 / 4 7.70, 8 / 8 7.94, 32 / 4 8.47; c5 gate+up 12.69, 12.65, 13.04,
+// 14.38, 12.76.
+inline int PickSpw(const WeightView &w, int64_t M) {
+  for (int spw : {16, 32, 8})
+    if (ShapeFits(w, M, spw, 8)) return spw;
+  return 0;
+}
+
+} // namespace gf
+
+bool GemvFragSupports(const WeightView &w, int64_t M) {
+  // The plan's fragment-ordered weights and decode scales; blocks of 32 to
+  // 256 k (each block inside one 256-k unit, each step inside one block);
+  // whole units per wavefront for some SPW with the image in LDS; 32-bit
+  // buffer offsets.
+  return M >= 1 && M <= 4 && w.Bp != nullptr && w.Sd != nullptr &&
+         (w.zp == nullptr || w.Zd != nullptr) && w.block_size >= 32 && w.block_size <= 256 &&
+         (w.block_size & (w.block_size - 1)) == 0 && (w.K % gf::kUnitK) == 0 &&
+         gf::PickSpw(w, M) > 0 && (w.K / 32) * 1024 < (int64_t{1} << 31) &&
+         w.nb * 256 < (int64_t{1} << 31) && M * w.K * 4 < (int64_t{1} << 31) &&
+         M * w.N < (int64_t{1} << 30);
+}
+
+bool GemvFragShapeOk(const WeightView &w, int64_t M, int spw, int win) {
+  return GemvFragSupports(w, M) && gf::ShapeFits(w, M, spw == 0 ? gf::PickSpw(w, M) : spw,
+                                                  win == 0 ? 8 : win);
+}
+
+bool GemvFragPreferred(const WeightView &w, int64_t M) {
+  // One workgroup per 64-row group: worth it where the groups cover most of
+  // the CUs.
+  return GemvFragSupports(w, M) &&
+         ((w.N + 63) / 64) * 100 >= static_cast<int64_t>(w.num_cus) * 85;
+}
+
+hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s,
+                          int spw, int win, float *H, const float *bias) {
+  if (spw == 0) spw = gf::PickSpw(w, M);
+  if (win == 0) win = 8;
+  if (!GemvFragSupports(w, M) || !gf::ShapeFits(w, M, spw, win)) return hipErrorInvalidValue;
+  const int m = static_cast<int>(M);
+  return w.zp != nullptr ? gf::LaunchZp<true>(w, m, A, Y, s, spw, win, H, bias)
+                         : gf::LaunchZp<false>(w, m, A, Y, s, spw, win, H, bias);
+}
+
+} // namespace mnb

@@ -108,18 +108,19 @@ bool GemvSmallMSupports(const WeightView &w, int64_t M);
 hipError_t LaunchGemvSmallMShape(const WeightView &w, int64_t M, const float *A, float *Y,
                                  hipStream_t s, int max_tokens, int waves, int rows_per_wave);
 
-// Decode GEMV for M == 1 on fp16 MFMA with exact products (activations split
-// into three fp16 terms in LDS, nibbles masked into fp16 subnormals),
+// Decode GEMV for 1 <= M <= 4 on fp16 MFMA with exact products (activations
+// split into three fp16 terms in LDS, nibbles masked into fp16 subnormals),
 // streaming the plan's fragment-ordered weights: one workgroup per 64-row
-// group, `steps_per_wave` (8, 16 or 32) 32-k steps per wavefront with
-// `window` (4 or 8) weight records in flight; 0 picks either.
-// Needs Bp / Sd (/ Zd) and 32 <= block_size <= 256. H and bias as below.
-bool GemvM1FragSupports(const WeightView &w);
-bool GemvM1FragShapeOk(const WeightView &w, int steps_per_wave, int window);
-// Whether the auto path takes it for M == 1: its groups cover most CUs.
-bool GemvM1FragPreferred(const WeightView &w);
-hipError_t LaunchGemvM1Frag(const WeightView &w, const float *A, float *Y, hipStream_t s,
-                            int steps_per_wave, int window, float *H, const float *bias);
+// group, `steps_per_wave` (8, 16 or 32; 8 or 16 when M > 1) 32-k steps per
+// wavefront with `window` (4 or 8; 8 when M > 1) weight records in flight; 0
+// picks either. Needs Bp / Sd (/ Zd) and 32 <= block_size <= 256. H and bias
+// as below.
+bool GemvFragSupports(const WeightView &w, int64_t M);
+bool GemvFragShapeOk(const WeightView &w, int64_t M, int steps_per_wave, int window);
+// Whether the auto path takes it: its groups cover most CUs.
+bool GemvFragPreferred(const WeightView &w, int64_t M);
+hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s,
+                          int steps_per_wave, int window, float *H, const float *bias);
 
 // Decode GEMV for M == 1 (fp16-subnormal mixed FMA): one workgroup per band
 // of `band_rows` weight rows, `rows_per_wave` (1, 2, 4 or 8) rows per

@@ -1,12 +1,12 @@
-"""GPU parity of the M = 1 MFMA decode kernel (GemvM1FragKernel).
+"""GPU parity of the LDS-staged MFMA decode kernel (GemvFragKernel, M <= 4).
 
 It multiplies each activation, split into three fp16 terms after a
-power-of-two scaling per 256-k unit, by the fp16 subnormals q 2^-24 of the
+power-of-two scaling per 256-k unit and row, by the fp16 subnormals q 2^-24 of the
 nibbles on the matrix cores (exact products), applies the zero point through
 each block's activation sum and sums in fp32, so it is held to the decode
 tolerance, max|y - y64| / max|y64| <= 1e-5 against the fp64 oracle, and
-cross-checked against GemvM1Kernel (fp32 mixed FMA, same bound) and the
-reference-order fp32 oracle. Runs are deterministic.
+cross-checked against GemvM1Kernel / the fp32-FMA decode kernel (same bound)
+and the reference-order fp32 oracle. Runs are deterministic.
 
 Every case prints its shape and launch shape before touching the GPU.
 """
@@ -44,8 +44,8 @@ def test_m1_frag_vs_oracle_and_m1(pkg, orc, cuda, K, N, bs, zp, spws):
     y_m1 = op.run_kernel(dA, pkg.KERNEL_GEMV_M1).cpu().numpy()
     for spw in spws:
         print(f"case m1-frag K={K} N={N} bs={bs} zp={zp} steps/wave={spw}", flush=True)
-        y1 = op.run_kernel(dA, pkg.KERNEL_GEMV_M1_FRAG, spw).cpu().numpy()
-        y2 = op.run_kernel(dA, pkg.KERNEL_GEMV_M1_FRAG, spw).cpu().numpy()
+        y1 = op.run_kernel(dA, pkg.KERNEL_GEMV_FRAG, spw).cpu().numpy()
+        y2 = op.run_kernel(dA, pkg.KERNEL_GEMV_FRAG, spw).cpu().numpy()
         np.testing.assert_array_equal(y1, y2)
         e64 = orc.normwise_max_error(y1, y64)
         e32 = orc.normwise_max_error(y1, y32)
@@ -53,6 +53,38 @@ def test_m1_frag_vs_oracle_and_m1(pkg, orc, cuda, K, N, bs, zp, spws):
         print(f"  normwise error: vs fp64 {e64:.2e}, vs reference fp32 {e32:.2e}, "
               f"vs GemvM1Kernel {em1:.2e}")
         assert e64 <= GEMV_TOL and e32 <= GEMV_TOL and em1 <= 2 * GEMV_TOL
+    op.release()
+
+
+@pytest.mark.parametrize("K,N,bs,zp,M", [
+    (4096, 14336, 128, True, 2),    # c2, two rows
+    (4096, 14336, 128, True, 3),    # three rows in a four-row launch
+    (4096, 14336, 128, True, 4),
+    (2048, 200, 32, False, 4),      # a block scale per step, ragged last group
+    (1024, 64, 256, True, 2),       # one group, a block per unit
+])
+def test_gemv_frag_rows_vs_oracle(pkg, orc, cuda, K, N, bs, zp, M):
+    import torch
+    B, S, Z = _weights(pkg, K, N, bs, zp, seed=K + N + M)
+    A = pkg.workloads.make_activations(M, K, 1.0, seed=M + 40)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    dA = torch.from_numpy(A).to(cuda)
+    print(f"case gemv-frag K={K} N={N} bs={bs} zp={zp} M={M}", flush=True)
+    spw = 8 if (bs == 32 and M > 2) else 16  # the launch shape M rows pick
+    y1 = op.run_kernel(dA, pkg.KERNEL_GEMV_FRAG, spw).cpu().numpy()
+    y2 = op.run_kernel(dA, pkg.KERNEL_GEMV_FRAG).cpu().numpy()
+    np.testing.assert_array_equal(y1, y2)
+    y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
+    y32 = orc.matmul_nbits_ref_f32(A, B, S, Z, K, N, bs)
+    for m in range(M):
+        # each row alone through the one-row launch of the same shape: the
+        # same bits (rows are independent, summed in the same order)
+        y_row = op.run_kernel(dA[m:m + 1], pkg.KERNEL_GEMV_FRAG, spw).cpu().numpy()
+        np.testing.assert_array_equal(y1[m:m + 1], y_row)
+    e64 = orc.normwise_max_error(y1, y64)
+    e32 = orc.normwise_max_error(y1, y32)
+    print(f"  normwise error: vs fp64 {e64:.2e}, vs reference fp32 {e32:.2e}")
+    assert e64 <= GEMV_TOL and e32 <= GEMV_TOL
     op.release()
 
 
@@ -75,7 +107,7 @@ def test_m1_frag_activation_range(pkg, orc, cuda):
     for name, a in rows.items():
         A = a.astype(np.float32)[None, :]
         print(f"case m1-frag-range K={K} N={N} bs={bs} row={name}", flush=True)
-        y = op.run_kernel(torch.from_numpy(A).to(cuda), pkg.KERNEL_GEMV_M1_FRAG).cpu().numpy()
+        y = op.run_kernel(torch.from_numpy(A).to(cuda), pkg.KERNEL_GEMV_FRAG).cpu().numpy()
         assert np.isfinite(y).all()
         if name == "zero":
             assert np.all(y == 0.0)
@@ -97,9 +129,9 @@ def test_m1_frag_auto_path_and_bias(pkg, orc, cuda):
     bias = np.random.default_rng(7).standard_normal(N).astype(np.float32)
     op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
     print(f"case m1-frag-auto K={K} N={N} kernel={op.kernel_name(1)}", flush=True)
-    assert op.kernel_name(1) == "GemvM1FragKernel"
+    assert op.kernel_name(1) == "GemvFragKernel"
     dA = torch.from_numpy(A).to(cuda)
-    y_k = op.run_kernel(dA, pkg.KERNEL_GEMV_M1_FRAG).cpu().numpy()
+    y_k = op.run_kernel(dA, pkg.KERNEL_GEMV_FRAG).cpu().numpy()
     np.testing.assert_array_equal(op(dA).cpu().numpy(), y_k)
     yb = op(dA, bias=torch.from_numpy(bias).to(cuda)).cpu().numpy()
     np.testing.assert_array_equal(yb, y_k + bias[None, :])
@@ -121,7 +153,7 @@ def test_m1_frag_gate_up_epilogue(pkg, orc, cuda):
     fused = pkg.GateUpSiLU(K, I, 4, bs).prepare(Bg, Sg, Zg, Bu, Su, Zu)
     A = pkg.workloads.make_activations(1, K, 1.0, seed=33)
     print(f"case m1-frag-gate-up K={K} I={I} bs={bs} kernel={fused.kernel_name(1)}", flush=True)
-    assert fused.kernel_name(1) == "GemvM1FragKernel"
+    assert fused.kernel_name(1) == "GemvFragKernel"
     H = fused(torch.from_numpy(A).to(cuda)).cpu().numpy()
     h64 = orc.gate_up_silu_f64(A, Bg, Sg, Zg, Bu, Su, Zu, K, I, bs)
     err = orc.normwise_max_error(H, h64)
@@ -132,16 +164,16 @@ def test_m1_frag_gate_up_epilogue(pkg, orc, cuda):
 
 def test_m1_frag_rejects(pkg, cuda):
     """Shapes the kernel cannot serve are rejected with MNB_ERR_UNSUPPORTED
-    before any launch: M > 1, 512-k blocks, steps per wavefront that are not
-    8, 16 or 32 or that need more than 16 wavefronts."""
+    before any launch: M > 4, 512-k blocks, steps per wavefront that are not
+    8, 16 or 32 or that need more than 16 wavefronts, 32 steps with M > 1."""
     import torch
-    cases = [((1024, 64, 128), 2, 0), ((2048, 64, 512), 1, 0), ((1024, 64, 128), 1, 24),
-             ((8192, 64, 128), 1, 8)]
+    cases = [((1024, 64, 128), 5, 0), ((2048, 64, 512), 1, 0), ((1024, 64, 128), 1, 24),
+             ((8192, 64, 128), 1, 8), ((4096, 64, 128), 2, 32)]
     for (K, N, bs), M, spw in cases:
         op = pkg.MatMulNBits(K, N, 4, bs).prepare(*_weights(pkg, K, N, bs, False, seed=3))
         A = torch.zeros((M, K), device=cuda)
         print(f"case m1-frag-reject K={K} N={N} bs={bs} M={M} spw={spw}", flush=True)
         with pytest.raises(pkg.MatMulNBitsError) as ei:
-            op.run_kernel(A, pkg.KERNEL_GEMV_M1_FRAG, spw)
+            op.run_kernel(A, pkg.KERNEL_GEMV_FRAG, spw)
         assert ei.value.status == 4
         op.release()

@@ -53,7 +53,7 @@ def _run_every_kernel(pkg, cuda, op, A):
     dA = torch.from_numpy(np.ascontiguousarray(A)).to(cuda)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     out = {}
-    for kernel in range(pkg.KERNEL_GEMV_M1, pkg.KERNEL_GEMV_M1_FRAG + 1):
+    for kernel in range(pkg.KERNEL_GEMV_M1, pkg.KERNEL_GEMV_FRAG + 1):
         n = ctypes.c_size_t()
         rc = L.mnb_kernel_workspace_bytes(op._plan, M, kernel, 0, 0, ctypes.byref(n))
         if rc == MNB_ERR_UNSUPPORTED:
