@@ -118,9 +118,13 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
  * plan's device. M == 0 is a no-op. Replaces the operator's compute call,
  * MatMulKernel::operator() -> MatMulPlan<float>::Execute
  * (onnx_light_cpu/kernels/math/matmul_kernel.cc:117-134, gemm_plan.cc:539-570).
- * M <= 4: fp32-FMA decode GEMV; 5 <= M <= 16 (from M = 4 when N >= 3K,
- * M = 3 when N >= 6K): decode GEMV on fp16 MFMA with exact products (A split
- * into three fp16 terms after a power-of-two scaling) and fp32 sums;
+ * M <= 4 on plans whose 64-row groups cover most CUs: decode GEMV on fp16
+ * MFMA with exact products (A split into three fp16 terms after a
+ * power-of-two scaling per 256-k unit, nibbles as fp16 subnormals) and fp32
+ * sums; other M = 1 plans: fp32 mixed-FMA GEMV; M <= 4 otherwise: fp32-FMA
+ * decode GEMV; 5 <= M <= 16 (from M = 4 when N >= 3K, M = 3 when N >= 6K):
+ * decode GEMV on fp16 MFMA with A split into two fp16 terms (22 bits) after
+ * a power-of-two scaling, exact q - zp, fp32 sums;
  * M > 16: fp16-MFMA prefill GEMM. Its A row m is scaled by a power of two
  * 2^f_m (largest magnitude in [2^14, 2^15)) and rounded to fp16 (round to
  * nearest even, half_conversion.h:42-78); each weight row's block scales are
