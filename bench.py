@@ -40,12 +40,12 @@ METRIC = "MatMulNBits 4-bit: M=1 achieved HBM GB/s; M=2048 TFLOP/s; % roofline"
 ROTATION_BYTES = 1 << 30
 
 # HBM bytes per launch of the headline kernel (GemvFragKernel on c2 M=1),
-# from two rocprofv3 --pmc passes over `bench.py --only decode,copy --eager
-# --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15577.6 KiB and
+# from two rocprofv3 --pmc passes over `bench.py --only decode,gemm,sweep,copy --eager
+# --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15580.1 KiB and
 # WRITE_SIZE 56.0 KiB per dispatch, each scaled by what the same counter reads
 # for the copy leg's 512 MiB device copy (FETCH_SIZE 262155.5 KiB -> x1.99992,
 # WRITE_SIZE 524288.0 KiB -> x1.00000). Re-measure when the kernel changes.
-GEMV_M1_C2_TRAFFIC_BYTES = round((15577.6 * (524288.0 / 262155.5) + 56.0) * 1024)
+GEMV_M1_C2_TRAFFIC_BYTES = round((15580.1 * (524288.0 / 262155.5) + 56.0) * 1024)
 
 
 def parse_args():
