@@ -564,11 +564,11 @@ static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
 
 // Without the kernel's workspace, M >= 2 falls back to the fp32-FMA kernels.
 // M <= 4 takes the LDS-staged MFMA kernel on the fragment-ordered copy where
-// its 64-row groups cover most CUs (not with a fused RMSNorm input); M = 1
+// its 64-row groups cover most CUs (a fused RMSNorm input at M = 1 too); M = 1
 // otherwise GemvM1Kernel.
 static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void *work,
                                      size_t work_bytes, bool rms = false) {
-  if (!rms && mnb::GemvFragPreferred(plan->view, M)) return kDecGemvFrag;
+  if (mnb::GemvFragPreferred(plan->view, M, rms)) return kDecGemvFrag;
   if (M == 1 && mnb::GemvM1Supports(plan->view)) return kDecM1;
   if (UsesFragDecode(plan, M) &&
       HasWorkspace(work, work_bytes, mnb::DecodeFragWorkspaceBytes(plan->view, M)))
@@ -694,7 +694,7 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   case 1:
     switch (PickDecodeKernel(plan, M, work, work_bytes, gamma != nullptr)) {
     case kDecGemvFrag:
-      e = mnb::LaunchGemvFrag(plan->view, M, dA, Ys, s, 0, 0, H, dBias);
+      e = mnb::LaunchGemvFrag(plan->view, M, dA, Ys, s, 0, 0, H, dBias, gamma, eps);
       fused = true;
       bias_done = dBias != nullptr;
       break;

@@ -75,25 +75,31 @@ constexpr size_t kLdsLimit = 150 * 1024;
 // floats) and unit exponents (K / 256 x MT ints) when MT > 1, the wavefront
 // sums (waves x MT x 64 floats).
 struct LdsLayout {
-  int sums, exps, red, bytes;
+  int sums, exps, red, sq, bytes;
 };
 __host__ __device__ inline LdsLayout Layout(int K, int nb, int waves, int mt) {
   LdsLayout l;
   l.sums = (K / 32) * 4 * mt * kOpBytes;
   l.exps = l.sums + (mt > 1 ? nb * mt * 4 : 0);
   l.red = l.exps + (mt > 1 ? (K / kUnitK) * mt * 4 : 0);
-  l.bytes = l.red + waves * mt * 256;
+  l.sq = l.red + waves * mt * 256;  // per wavefront: its units' sum of squares (RMSNorm)
+  l.bytes = l.sq + kMaxWaves * 4;
   return l;
 }
 
 // SPB = 32-k steps per quantization block (bs / 32, 1..8); SPW = steps per
 // wavefront (whole units); WIN = weight records in flight per wavefront; MT =
-// activation rows the launch is built for (1, 2 or 4; M <= MT).
-template <bool HAS_ZP, int SPB, int SPW, int WIN, int MT>
+// activation rows the launch is built for (1, 2 or 4; M <= MT). RMS (MT = 1):
+// the input is RMSNorm(A) = A / sqrt(mean(A^2) + eps) * gamma; the staging
+// multiplies by gamma and sums A^2 over the wavefront's units, and the row's
+// 1 / rms scales the final sums (it is common to every product).
+template <bool HAS_ZP, int SPB, int SPW, int WIN, int MT, bool RMS>
 __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     const float *__restrict__ A, const uint8_t *__restrict__ Bp, const float *__restrict__ Sd,
     const uint32_t *__restrict__ Zd, float *__restrict__ Y, float *__restrict__ H,
-    const float *__restrict__ bias, int M, int N, int K, int nb) {
+    const float *__restrict__ bias, const float *__restrict__ gamma, float eps, int M, int N,
+    int K, int nb) {
+  static_assert(!RMS || MT == 1, "RMSNorm input at M = 1 only");
   constexpr int kUnits = SPW / kUnitSteps;      // units of this wavefront
   constexpr int kItems = kUnits * MT;           // (unit, row) staging items, 32 lanes each
   constexpr int kPasses = (kItems + 1) / 2;     // two items per pass
@@ -114,6 +120,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
   float *sums = reinterpret_cast<float *>(lds + L.sums);
   int *exps = reinterpret_cast<int *>(lds + L.exps);
   float *red = reinterpret_cast<float *>(lds + L.red);
+  float *sq_lds = reinterpret_cast<float *>(lds + L.sq);
 
   // 1. This wavefront's activations, before every weight load: in pass p,
   //    the 32 lanes of half h take the 8 values of quarter l & 31 of item
@@ -121,7 +128,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
   //    nothing).
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, M * K * 4, 0x00020000);
-  floatx4 va[kPasses][2];
+  const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(RMS ? gamma : A), 0, K * 4, 0x00020000);
+  floatx4 va[kPasses][2], vg[RMS ? kPasses : 1][2];
 #pragma unroll
   for (int p = 0; p < kPasses; ++p) {
     const int it = min(2 * p + (lane >> 5), kItems - 1);
@@ -129,6 +138,11 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     const int off = (m * K + (u0 + ul) * kUnitK + 8 * (lane & 31)) * 4;
     va[p][0] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
     va[p][1] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16, 0, 0));
+    if constexpr (RMS) {
+      const int goff = ((u0 + ul) * kUnitK + 8 * (lane & 31)) * 4;
+      vg[p][0] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rg, goff, 0, 0));
+      vg[p][1] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rg, goff + 16, 0, 0));
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -170,8 +184,19 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
   //    scalars (M = 1) or to the LDS tables.
   float sb[MT == 1 ? kBlocks : 1];
   int eu[MT == 1 ? kUnits : 1];
+  float sq = 0.f;  // RMS: sum of A^2 over this lane's valid values
 #pragma unroll
   for (int p = 0; p < kPasses; ++p) {
+    if constexpr (RMS) {
+      float q2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        q2 += va[p][0][i] * va[p][0][i] + va[p][1][i] * va[p][1][i];
+        va[p][0][i] *= vg[p][0][i];
+        va[p][1][i] *= vg[p][1][i];
+      }
+      sq += 2 * p + (lane >> 5) < kItems ? q2 : 0.f;
+    }
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fmaxf(fabsf(va[p][0][i]), fabsf(va[p][1][i])));
@@ -222,6 +247,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ssum), 32 * uh + 4 * SPB * bb));
       }
     }
+  }
+  if constexpr (RMS) {
+    // the wavefront's sum of squares (fixed butterfly), to LDS for the end
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
+    if (lane == 0) sq_lds[wave] = sq;
   }
   // The image writes above precede the operand reads below.
   __asm__ volatile("" ::: "memory");
@@ -310,11 +341,18 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     for (int j = 0; j < 4; ++j) red[(wave * MT + (lane >> 4)) * 64 + 16 * j + c] = acc[j];
   }
   __syncthreads();
+  float inv_rms = 1.0f;
+  if constexpr (RMS) {
+    float tot = 0.0f;
+    for (int w = 0; w < waves; ++w) tot += sq_lds[w];
+    inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+  }
   // whole wavefronts per iteration (M * 64 and the block are multiples of 64)
   for (int idx = static_cast<int>(threadIdx.x); idx < M * 64; idx += static_cast<int>(blockDim.x)) {
     const int m = idx >> 6, r = idx & 63;
     float y = red[m * 64 + r];
     for (int w = 1; w < waves; ++w) y += red[(w * MT + m) * 64 + r];
+    if constexpr (RMS) y *= inv_rms;
     const int n = 64 * g + r;
     if (H != nullptr) {
       // gate/up pairs: rows 2 n', 2 n' + 1 in lanes r, r ^ 1 (N even)
@@ -331,35 +369,45 @@ inline int RowsBuilt(int64_t M) { return M == 1 ? 1 : (M == 2 ? 2 : 4); }
 
 template <bool HAS_ZP, int SPB>
 hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipStream_t s, int spw,
-                     int win, float *H, const float *bias) {
+                     int win, float *H, const float *bias, const float *gamma, float eps) {
   const int K = static_cast<int>(w.K), N = static_cast<int>(w.N), nb = static_cast<int>(w.nb);
   const int waves = K / 32 / spw;
   const int mt = RowsBuilt(M);
   const int lds = Layout(K, nb, waves, mt).bytes;
   const dim3 grid(static_cast<unsigned>((w.N + 63) / 64)), block(static_cast<unsigned>(64 * waves));
-#define MNB_GF_LAUNCH(SPWV, WINV, MTV)                                                          \
-  hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, WINV, MTV>), grid, block, lds, s, A,   \
-                     w.Bp, w.Sd, w.Zd, Y, H, bias, M, N, K, nb)
-  if (mt > 1) {
+#define MNB_GF_LAUNCH(SPWV, WINV, MTV, RMSV)                                                    \
+  hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, WINV, MTV, RMSV>), grid, block, lds, s, \
+                     A, w.Bp, w.Sd, w.Zd, Y, H, bias, gamma, eps, M, N, K, nb)
+  if (gamma != nullptr) {
+    // RMSNorm input (M = 1, window 8, no 32-step launch with 32-k blocks:
+    // checked by the caller)
+    switch (spw) {
+    case 8: MNB_GF_LAUNCH(8, 8, 1, true); break;
+    case 16: MNB_GF_LAUNCH(16, 8, 1, true); break;
+    default:
+      if constexpr (SPB > 1) MNB_GF_LAUNCH(32, 8, 1, true);
+      break;
+    }
+  } else if (mt > 1) {
     // more rows: window 8, 8 or 16 steps per wavefront (checked by the caller)
     if (mt == 2) {
-      if (spw == 8) MNB_GF_LAUNCH(8, 8, 2);
-      else MNB_GF_LAUNCH(16, 8, 2);
+      if (spw == 8) MNB_GF_LAUNCH(8, 8, 2, false);
+      else MNB_GF_LAUNCH(16, 8, 2, false);
     } else {
-      if (spw == 8) MNB_GF_LAUNCH(8, 8, 4);
-      else MNB_GF_LAUNCH(16, 8, 4);
+      if (spw == 8) MNB_GF_LAUNCH(8, 8, 4, false);
+      else MNB_GF_LAUNCH(16, 8, 4, false);
     }
   } else if (win == 8) {
     switch (spw) {
-    case 8: MNB_GF_LAUNCH(8, 8, 1); break;
-    case 16: MNB_GF_LAUNCH(16, 8, 1); break;
-    default: MNB_GF_LAUNCH(32, 8, 1); break;
+    case 8: MNB_GF_LAUNCH(8, 8, 1, false); break;
+    case 16: MNB_GF_LAUNCH(16, 8, 1, false); break;
+    default: MNB_GF_LAUNCH(32, 8, 1, false); break;
     }
   } else {
     switch (spw) {
-    case 8: MNB_GF_LAUNCH(8, 4, 1); break;
-    case 16: MNB_GF_LAUNCH(16, 4, 1); break;
-    default: MNB_GF_LAUNCH(32, 4, 1); break;
+    case 8: MNB_GF_LAUNCH(8, 4, 1, false); break;
+    case 16: MNB_GF_LAUNCH(16, 4, 1, false); break;
+    default: MNB_GF_LAUNCH(32, 4, 1, false); break;
     }
   }
 #undef MNB_GF_LAUNCH
@@ -368,12 +416,12 @@ hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipSt
 
 template <bool HAS_ZP>
 hipError_t LaunchZp(const WeightView &w, int M, const float *A, float *Y, hipStream_t s, int spw,
-                    int win, float *H, const float *bias) {
+                    int win, float *H, const float *bias, const float *gamma, float eps) {
   switch (w.block_size / 32) {
-  case 1: return LaunchSpw<HAS_ZP, 1>(w, M, A, Y, s, spw, win, H, bias);
-  case 2: return LaunchSpw<HAS_ZP, 2>(w, M, A, Y, s, spw, win, H, bias);
-  case 4: return LaunchSpw<HAS_ZP, 4>(w, M, A, Y, s, spw, win, H, bias);
-  default: return LaunchSpw<HAS_ZP, 8>(w, M, A, Y, s, spw, win, H, bias);
+  case 1: return LaunchSpw<HAS_ZP, 1>(w, M, A, Y, s, spw, win, H, bias, gamma, eps);
+  case 2: return LaunchSpw<HAS_ZP, 2>(w, M, A, Y, s, spw, win, H, bias, gamma, eps);
+  case 4: return LaunchSpw<HAS_ZP, 4>(w, M, A, Y, s, spw, win, H, bias, gamma, eps);
+  default: return LaunchSpw<HAS_ZP, 8>(w, M, A, Y, s, spw, win, H, bias, gamma, eps);
   }
 }
 
@@ -420,21 +468,27 @@ bool GemvFragShapeOk(const WeightView &w, int64_t M, int spw, int win) {
                                                   win == 0 ? 8 : win);
 }
 
-bool GemvFragPreferred(const WeightView &w, int64_t M) {
+bool GemvFragPreferred(const WeightView &w, int64_t M, bool rms) {
   // One workgroup per 64-row group: worth it where the groups cover most of
-  // the CUs.
+  // the CUs. The RMSNorm input: M = 1, and not 32 steps per wavefront with
+  // 32-k blocks (the launch that would spill registers).
+  if (rms && (M != 1 || (gf::PickSpw(w, 1) == 32 && w.block_size == 32))) return false;
   return GemvFragSupports(w, M) &&
          ((w.N + 63) / 64) * 100 >= static_cast<int64_t>(w.num_cus) * 85;
 }
 
 hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s,
-                          int spw, int win, float *H, const float *bias) {
+                          int spw, int win, float *H, const float *bias, const float *gamma,
+                          float eps) {
   if (spw == 0) spw = gf::PickSpw(w, M);
   if (win == 0) win = 8;
   if (!GemvFragSupports(w, M) || !gf::ShapeFits(w, M, spw, win)) return hipErrorInvalidValue;
+  if (gamma != nullptr && (M != 1 || win != 8 || (spw == 32 && w.block_size == 32) ||
+                           (reinterpret_cast<uintptr_t>(gamma) % 16) != 0))
+    return hipErrorInvalidValue;
   const int m = static_cast<int>(M);
-  return w.zp != nullptr ? gf::LaunchZp<true>(w, m, A, Y, s, spw, win, H, bias)
-                         : gf::LaunchZp<false>(w, m, A, Y, s, spw, win, H, bias);
+  return w.zp != nullptr ? gf::LaunchZp<true>(w, m, A, Y, s, spw, win, H, bias, gamma, eps)
+                         : gf::LaunchZp<false>(w, m, A, Y, s, spw, win, H, bias, gamma, eps);
 }
 
 } // namespace mnb

@@ -113,14 +113,16 @@ hipError_t LaunchGemvSmallMShape(const WeightView &w, int64_t M, const float *A,
 // streaming the plan's fragment-ordered weights: one workgroup per 64-row
 // group, `steps_per_wave` (8, 16 or 32; 8 or 16 when M > 1) 32-k steps per
 // wavefront with `window` (4 or 8; 8 when M > 1) weight records in flight; 0
-// picks either. Needs Bp / Sd (/ Zd) and 32 <= block_size <= 256. H and bias
-// as below.
+// picks either. Needs Bp / Sd (/ Zd) and 32 <= block_size <= 256. H, bias and
+// the RMSNorm input (gamma, M = 1, window 8) as below.
 bool GemvFragSupports(const WeightView &w, int64_t M);
 bool GemvFragShapeOk(const WeightView &w, int64_t M, int steps_per_wave, int window);
-// Whether the auto path takes it: its groups cover most CUs.
-bool GemvFragPreferred(const WeightView &w, int64_t M);
+// Whether the auto path takes it: its groups cover most CUs (with `rms`, for
+// a fused RMSNorm input).
+bool GemvFragPreferred(const WeightView &w, int64_t M, bool rms = false);
 hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s,
-                          int steps_per_wave, int window, float *H, const float *bias);
+                          int steps_per_wave, int window, float *H, const float *bias,
+                          const float *gamma = nullptr, float eps = 0.0f);
 
 // Decode GEMV for M == 1 (fp16-subnormal mixed FMA): one workgroup per band
 // of `band_rows` weight rows, `rows_per_wave` (1, 2, 4 or 8) rows per

@@ -141,6 +141,41 @@ def test_m1_frag_auto_path_and_bias(pkg, orc, cuda):
     narrow.release()
 
 
+def test_gemv_frag_rows_bias_and_gate_up(pkg, orc, cuda):
+    """M = 2..4 on wide plans: the bias added in the final store (bit-identical
+    to y + bias) and the gate/up activation written by the kernel (within the
+    gate/up bound of the fp64 oracle)."""
+    import torch
+    K, N, bs = 4096, 14336, 128
+    B, S, Z = _weights(pkg, K, N, bs, True, seed=51)
+    bias = np.random.default_rng(52).standard_normal(N).astype(np.float32)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    for M in (2, 3):
+        A = pkg.workloads.make_activations(M, K, 1.0, seed=53 + M)
+        dA = torch.from_numpy(A).to(cuda)
+        print(f"case gemv-frag-bias K={K} N={N} M={M} kernel={op.kernel_name(M)}", flush=True)
+        assert op.kernel_name(M) == "GemvFragKernel"
+        y = op(dA).cpu().numpy()
+        yb = op(dA, bias=torch.from_numpy(bias).to(cuda)).cpu().numpy()
+        np.testing.assert_array_equal(yb, y + bias[None, :])
+    op.release()
+    K, I, bs = 2048, 7168, 64
+    p = pkg.workloads.Projection("g", K, I, bs, True, 1.0, 0.005, 0.02)
+    Bg, Sg, Zg = pkg.workloads.make_weights(p, 61)
+    Bu, Su, Zu = pkg.workloads.make_weights(p, 62)
+    fused = pkg.GateUpSiLU(K, I, 4, bs).prepare(Bg, Sg, Zg, Bu, Su, Zu)
+    for M in (2, 4):
+        A = pkg.workloads.make_activations(M, K, 1.0, seed=63 + M)
+        print(f"case gemv-frag-gate-up K={K} I={I} M={M} kernel={fused.kernel_name(M)}", flush=True)
+        assert fused.kernel_name(M) == "GemvFragKernel"
+        H = fused(torch.from_numpy(A).to(cuda)).cpu().numpy()
+        h64 = orc.gate_up_silu_f64(A, Bg, Sg, Zg, Bu, Su, Zu, K, I, bs)
+        err = orc.normwise_max_error(H, h64)
+        print(f"  normwise error vs fp64 {err:.2e}")
+        assert err <= GATE_UP_TOL
+    fused.release()
+
+
 def test_m1_frag_gate_up_epilogue(pkg, orc, cuda):
     """A gate/up plan wide enough for the kernel writes silu(gate) * up
     itself (rows 2n, 2n + 1 of a 64-row group), within the gate/up routes'

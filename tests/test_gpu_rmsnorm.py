@@ -27,6 +27,7 @@ def _torch_rms(torch, X, g, eps):
 @pytest.mark.parametrize("K,N,bs,zp,Ms,eps", [
     (4096, 768, 128, True, (1, 3, 8, 40, 512), 1e-5),
     (1024, 200, 32, False, (1, 16, 33), 1e-6),
+    (4096, 14336, 128, True, (1, 3), 1e-5),   # wide: GemvFragKernel with the RMSNorm input at M = 1
 ])
 def test_rmsnorm_plain_plan(pkg, orc, cuda, K, N, bs, zp, Ms, eps):
     import torch
@@ -42,6 +43,8 @@ def test_rmsnorm_plain_plan(pkg, orc, cuda, K, N, bs, zp, Ms, eps):
         X = (rng.standard_normal((M, K)) * rng.uniform(0.1, 10, (M, 1))).astype(np.float32)
         dX = torch.from_numpy(X).to(cuda)
         Y = op.run_rmsnorm(dX, dg, eps).cpu().numpy()
+        if N >= 14336:
+            assert op.kernel_name(M) == "GemvFragKernel"
         Yu = op(_torch_rms(torch, dX, dg, eps).contiguous()).cpu().numpy()
         An = orc.rmsnorm_f64(X, gamma, eps).astype(np.float32)
         y64 = orc.matmul_nbits_f64(An, B, S, Z, K, N, bs)
