@@ -86,8 +86,10 @@ SETTLE_S = 0.2
 
 def time_graph(torch, launches, steps, warmup, stream):
     """Captures `launches` (a callable issuing one step) into a graph, replays it
-    (or, with --eager, calls it directly). Returns (ms per step from events on
-    `stream`, wall seconds of the timed region)."""
+    (or, with --eager, calls it directly). Returns (ms per step from the events
+    bracketing all steps on `stream`, wall seconds of the timed region, median
+    and interquartile range of the per-step ms from an event before every
+    step)."""
     with torch.cuda.stream(stream):
         launches()  # eager warmup outside capture; allocates any workspace
     torch.cuda.synchronize()
@@ -113,17 +115,18 @@ def time_graph(torch, launches, steps, warmup, stream):
         for _ in range(warmup):
             step()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
-        start.record(stream)
-        for _ in range(steps):
+        for i in range(steps):
+            marks[i].record(stream)
             step()
-        end.record(stream)
+        marks[steps].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return start.elapsed_time(end) / steps, wall
+    per = [marks[i].elapsed_time(marks[i + 1]) for i in range(steps)]
+    q = statistics.quantiles(per, n=4) if steps >= 2 else [per[0], per[0], per[0]]
+    return marks[0].elapsed_time(marks[steps]) / steps, wall, statistics.median(per), q[2] - q[0]
 
 
 def copy_leg(torch, dev, steps, warmup, stream):
@@ -136,7 +139,7 @@ def copy_leg(torch, dev, steps, warmup, stream):
     def launches():
         dst.copy_(src)
 
-    ms, wall = time_graph(torch, launches, steps, warmup, stream)
+    ms, wall, med, iqr = time_graph(torch, launches, steps, warmup, stream)
     return {"bytes_read": n, "bytes_written": n, "us_per_launch": ms * 1e3,
             "GBps": 2 * n / (ms * 1e-3) / 1e9, "wall_s": wall}
 
@@ -159,7 +162,7 @@ def stream_ceiling_leg(torch, pkg, dev, nbytes, steps, warmup, stream):
             if rc != 0:
                 raise RuntimeError(f"mnb_stream_read: status {rc}")
 
-    ms, _ = time_graph(torch, launches, steps, warmup, stream)
+    ms, _, _, _ = time_graph(torch, launches, steps, warmup, stream)
     us = ms * 1e3 / rot
     del bufs
     torch.cuda.empty_cache()
@@ -183,7 +186,7 @@ def fp16_gemm_reference(torch, dev, p, M, steps, warmup, stream):
         for _ in range(CALLS_PER_STEP):
             torch.matmul(A, Wt.t(), out=Y)
 
-    ms, _ = time_graph(torch, launches, steps, warmup, stream)
+    ms, _, _, _ = time_graph(torch, launches, steps, warmup, stream)
     us = ms * 1e3 / CALLS_PER_STEP
     tflops = p.flops(M) / (us * 1e-6) / 1e12
     return {"what": "torch.matmul fp16 x fp16 -> fp16 (hipBLASLt), dense weights",
@@ -247,7 +250,7 @@ def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
         for op in ops:
             op(A, out=Y, stream=torch.cuda.current_stream())
 
-    ms, wall = time_graph(torch, launches, steps, warmup, stream)
+    ms, wall, med, iqr = time_graph(torch, launches, steps, warmup, stream)
     per_launch_us = ms * 1e3 / rot
     nbytes = p.algorithmic_bytes(M)
     for op in ops:
@@ -258,7 +261,8 @@ def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
         "K": p.K, "N": p.N, "M": M, "block_size": p.block_size,
         "zero_points": p.has_zero_points, "path": path, "kernel": kernel,
         "rotation_copies": rot,
-        "us_per_launch": per_launch_us, "bytes_per_launch": nbytes,
+        "us_per_launch": per_launch_us, "us_per_launch_median": med * 1e3 / rot,
+        "us_per_launch_iqr": iqr * 1e3 / rot, "bytes_per_launch": nbytes,
         "GBps": nbytes / (per_launch_us * 1e-6) / 1e9, "ms_per_step": ms, "wall_s": wall,
         "wall_ms_per_step": wall * 1e3 / steps,
         "launches_per_step": rot,
@@ -283,13 +287,15 @@ def gemm_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
         for _ in range(CALLS_PER_STEP):
             op(A, out=Y, stream=torch.cuda.current_stream())
 
-    ms, wall = time_graph(torch, launches, steps, warmup, stream)
+    ms, wall, med, iqr = time_graph(torch, launches, steps, warmup, stream)
     us = ms * 1e3 / CALLS_PER_STEP
     flops = p.flops(M)
     tflops = flops / (us * 1e-6) / 1e12
     res = {"K": p.K, "N": p.N, "M": M, "block_size": p.block_size, "path": op.select_path(M),
            "kernel": op.kernel_name(M), "calls_per_step": CALLS_PER_STEP,
-           "us_per_launch": us, "TFLOPs": tflops, "frac_fp16_peak": tflops / FP16_PEAK_TFLOPS,
+           "us_per_launch": us, "us_per_launch_median": med * 1e3 / CALLS_PER_STEP,
+           "us_per_launch_iqr": iqr * 1e3 / CALLS_PER_STEP,
+           "TFLOPs": tflops, "frac_fp16_peak": tflops / FP16_PEAK_TFLOPS,
            "bytes_per_launch": p.algorithmic_bytes(M), "wall_s": wall,
            "wall_ms_per_step": wall * 1e3 / steps}
     op.release()
@@ -343,7 +349,7 @@ def gate_up_leg(torch, pkg, dev, Ms, steps, warmup, stream):
         r = {"M": M, "weight_copies": n, "calls_per_step": n * reps}
         for name, fn in (("fused_us", run_fused), ("unfused_us", run_unfused),
                          ("matmul_only_us", run_plain)):
-            ms, _ = time_graph(torch, fn, steps, warmup, stream)
+            ms, _, _, _ = time_graph(torch, fn, steps, warmup, stream)
             r[name] = ms * 1e3 / (n * reps)
         r["gain"] = r["unfused_us"] / r["fused_us"]
         out.append(r)
@@ -393,7 +399,7 @@ def rmsnorm_leg(torch, pkg, dev, Ms, steps, warmup, stream):
         r = {"M": M, "weight_copies": n, "calls_per_step": n * reps}
         for name, fn in (("fused_us", run_fused), ("unfused_us", run_unfused),
                          ("matmul_only_us", run_plain)):
-            ms, _ = time_graph(torch, fn, steps, warmup, stream)
+            ms, _, _, _ = time_graph(torch, fn, steps, warmup, stream)
             r[name] = ms * 1e3 / (n * reps)
         r["gain"] = r["unfused_us"] / r["fused_us"]
         out.append(r)
@@ -427,10 +433,11 @@ def c5_leg(torch, pkg, dev, M, steps, warmup, stream):
         for p, op in ops:
             op(acts[p.K], out=outs[p.N], stream=torch.cuda.current_stream())
 
-    ms, wall = time_graph(torch, launches, steps, warmup, stream)
+    ms, wall, med, iqr = time_graph(torch, launches, steps, warmup, stream)
     nbytes = sum(p.algorithmic_bytes(M) for p, _ in ops)
     flops = sum(p.flops(M) for p, _ in ops)
     res = {"M": M, "layers": c.layers, "launches_per_step": len(ops), "ms_per_step": ms,
+           "ms_per_step_median": med, "ms_per_step_iqr": iqr,
            "us_per_launch": ms * 1e3 / len(ops), "bytes_per_step": nbytes,
            "flops_per_step": flops, "GBps": nbytes / (ms * 1e-3) / 1e9,
            "TFLOPs": flops / (ms * 1e-3) / 1e12, "wall_ms_per_step": wall * 1e3 / steps}
@@ -580,7 +587,9 @@ def main():
             q = W.CONFIGS[cname].projections[0]
             r = decode_leg(torch, pkg, dev, q, M, max(3, args.steps // 4), 2, 19 + M, stream)
             gemm["small_m"].append({"config": cname, "M": M, "kernel": r["kernel"],
-                                    "us_per_launch": r["us_per_launch"], "GBps": r["GBps"],
+                                    "us_per_launch": r["us_per_launch"],
+                                    "us_per_launch_median": r["us_per_launch_median"],
+                                    "us_per_launch_iqr": r["us_per_launch_iqr"], "GBps": r["GBps"],
                                     "TFLOPs": q.flops(M) / (r["us_per_launch"] * 1e-6) / 1e12})
             print(f"# small-M gemm {cname} M={M}: {r['us_per_launch']:.2f} us, {r['GBps']:.0f} GB/s",
                   file=sys.stderr, flush=True)
@@ -597,8 +606,8 @@ def main():
             for M in Ms:
                 r = decode_leg(torch, pkg, dev, p, M, max(3, args.steps // 4), 2, 17 + M, stream)
                 r["config"] = cname
-                sweep.append({k: r[k] for k in ("config", "M", "us_per_launch", "GBps", "path",
-                                                 "kernel")})
+                sweep.append({k: r[k] for k in ("config", "M", "us_per_launch", "us_per_launch_median",
+                                                 "us_per_launch_iqr", "GBps", "path", "kernel")})
                 print(f"# decode {cname} M={M}: {r['us_per_launch']:.2f} us, {r['GBps']:.0f} GB/s",
                       file=sys.stderr, flush=True)
     c5 = []
@@ -656,6 +665,8 @@ def main():
                 "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                 "copy-calibrated)",
                 "kernel": f"{head['kernel']} (c2 M=1)", "us_per_launch": head["us_per_launch"],
+                "us_per_launch_median": head["us_per_launch_median"],
+                "us_per_launch_iqr": head["us_per_launch_iqr"],
                 "bytes_per_launch": head["bytes_per_launch"]}
         if ceiling is not None:
             roof["ceiling"] = ceiling["frac_of_peak"]
@@ -668,7 +679,7 @@ def main():
     out = {
         "metric": METRIC, "value": value, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "u4xf32 (fp32 FMA)",
+        "scaling": "weak", "vs_baseline": None, "dtype": "u4xf32 (exact products on fp16 MFMA, fp32 sums)",
         "data": "synthetic (seeded uniform nibbles, uniform scales, N(0,1) activations)",
         "config": {"workload": workload, "M": 1, "K": 4096, "N": 14336, "block_size": 128,
                    "zero_points": True},
