@@ -679,7 +679,7 @@ def main():
     out = {
         "metric": METRIC, "value": value, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "u4xf32 (exact products on fp16 MFMA, fp32 sums)",
+        "scaling": "weak", "vs_baseline": None, "dtype": "u4xf32 (fp16 MFMA on 3-term fp16 activations and nibble subnormals, fp32 sums)",
         "data": "synthetic (seeded uniform nibbles, uniform scales, N(0,1) activations)",
         "config": {"workload": workload, "M": 1, "K": 4096, "N": 14336, "block_size": 128,
                    "zero_points": True},

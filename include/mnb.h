@@ -119,9 +119,9 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
  * MatMulKernel::operator() -> MatMulPlan<float>::Execute
  * (onnx_light_cpu/kernels/math/matmul_kernel.cc:117-134, gemm_plan.cc:539-570).
  * M <= 4 on plans whose 64-row groups cover most CUs: decode GEMV on fp16
- * MFMA with exact products (A split into three fp16 terms after a
- * power-of-two scaling per 256-k unit, nibbles as fp16 subnormals) and fp32
- * sums; other M = 1 plans: fp32 mixed-FMA GEMV; M <= 4 otherwise: fp32-FMA
+ * MFMA (A split into three fp16 terms after a power-of-two scaling per 256-k
+ * unit, nibbles as fp16 subnormals; fp32 sums within about 2^-22 of
+ * sum |a w| per output); other M = 1 plans: fp32 mixed-FMA GEMV; M <= 4 otherwise: fp32-FMA
  * decode GEMV; 5 <= M <= 16 (from M = 4 when N >= 3K, M = 3 when N >= 6K):
  * decode GEMV on fp16 MFMA with A split into two fp16 terms (22 bits) after
  * a power-of-two scaling, exact q - zp, fp32 sums;
@@ -208,7 +208,7 @@ int mnb_select_path(const mnb_plan *plan, int64_t M, int *path);
 #define MNB_KERNEL_GEMV 7         /* GemvKernel: fp32 FMA fallback, M <= 16 */
 #define MNB_KERNEL_GENERIC 8      /* GenericKernel: any shape, one wavefront per output */
 #define MNB_KERNEL_STREAM 9       /* StreamKernel: 17 <= M <= 64, fp16 MFMA, fragment-ordered copy streamed once */
-#define MNB_KERNEL_GEMV_FRAG 10  /* GemvFragKernel: M <= 4, exact-product MFMA, fragment-ordered copy, A staged in LDS */
+#define MNB_KERNEL_GEMV_FRAG 10  /* GemvFragKernel: M <= 4, fp16 MFMA on nibble subnormals, fragment-ordered copy, A staged in LDS */
 
 /* Name of the main kernel mnb_run launches for M rows given workspace_bytes
  * of workspace ("GemvM1Kernel", "DecodeFragKernel", "PrefillKernel", ...;

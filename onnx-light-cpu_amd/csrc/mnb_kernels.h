@@ -108,8 +108,9 @@ bool GemvSmallMSupports(const WeightView &w, int64_t M);
 hipError_t LaunchGemvSmallMShape(const WeightView &w, int64_t M, const float *A, float *Y,
                                  hipStream_t s, int max_tokens, int waves, int rows_per_wave);
 
-// Decode GEMV for 1 <= M <= 4 on fp16 MFMA with exact products (activations
-// split into three fp16 terms in LDS, nibbles masked into fp16 subnormals),
+// Decode GEMV for 1 <= M <= 4 on fp16 MFMA (activations split into three fp16
+// terms in LDS, nibbles masked into fp16 subnormals, fp32 sums within about
+// 2^-22 of sum |a w| per output),
 // streaming the plan's fragment-ordered weights: one workgroup per 64-row
 // group, `steps_per_wave` (8, 16 or 32; 8 or 16 when M > 1) 32-k steps per
 // wavefront with `window` (4 or 8; 8 when M > 1) weight records in flight; 0

@@ -2,7 +2,9 @@
 
 It multiplies each activation, split into three fp16 terms after a
 power-of-two scaling per 256-k unit and row, by the fp16 subnormals q 2^-24 of the
-nibbles on the matrix cores (exact products), applies the zero point through
+nibbles on the matrix cores (each product exact; the matrix core's sum of a
+step's products keeps about 2^-22 of sum |a w| for the nibbles in the low
+mantissa bits), applies the zero point through
 each block's activation sum and sums in fp32, so it is held to the decode
 tolerance, max|y - y64| / max|y64| <= 1e-5 against the fp64 oracle, and
 cross-checked against GemvM1Kernel / the fp32-FMA decode kernel (same bound)
