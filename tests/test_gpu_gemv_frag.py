@@ -214,3 +214,32 @@ def test_m1_frag_rejects(pkg, cuda):
             op.run_kernel(A, pkg.KERNEL_GEMV_FRAG, spw)
         assert ei.value.status == 4
         op.release()
+
+
+# Per-output bound of the kernel's sums: the matrix core aligns a step's
+# products to the largest one's nominal exponent and keeps about 24 bits, and
+# the even-k nibbles (fp16 subnormals q 2^-24, nominal exponent -14) sit up to
+# 10 bits below it, so an output may be off by about 2^-22 of
+# sum_k |a_k w_k| (2.5e-7 to 2.8e-7 measured at these shapes). 2^-20 leaves
+# room for other seeds; a lost second activation term would be ~2^-11.
+PER_OUTPUT_BOUND = 2.0 ** -20
+
+
+@pytest.mark.parametrize("K,N,bs,zp,M", [
+    (4096, 14336, 128, True, 1),   # c2
+    (4096, 14336, 128, True, 4),
+    (4096, 4096, 32, False, 2),    # c1-shaped, a block scale per step
+])
+def test_gemv_frag_per_output_bound(pkg, orc, cuda, K, N, bs, zp, M):
+    import torch
+    B, S, Z = _weights(pkg, K, N, bs, zp, seed=K + N + 7 * M)
+    A = pkg.workloads.make_activations(M, K, 1.0, seed=M + 90)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    print(f"case gemv-frag-bound K={K} N={N} bs={bs} zp={zp} M={M}", flush=True)
+    y = op.run_kernel(torch.from_numpy(A).to(cuda), pkg.KERNEL_GEMV_FRAG).cpu().numpy()
+    op.release()
+    y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
+    den = orc.abs_dot_f64(A, B, S, Z, K, N, bs)
+    worst = float(np.max(np.abs(y.astype(np.float64) - y64) / den))
+    print(f"  max |y - y64| / sum|a w| = {worst:.2e}")
+    assert worst <= PER_OUTPUT_BOUND
