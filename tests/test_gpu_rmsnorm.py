@@ -28,6 +28,7 @@ def _torch_rms(torch, X, g, eps):
     (4096, 768, 128, True, (1, 3, 8, 40, 512), 1e-5),
     (1024, 200, 32, False, (1, 16, 33), 1e-6),
     (4096, 14336, 128, True, (1, 3), 1e-5),   # wide: GemvFragKernel with the RMSNorm input at M = 1
+    (2048, 14336, 32, False, (1,), 1e-5),     # wide, a block scale per step, 16 steps per wavefront
 ])
 def test_rmsnorm_plain_plan(pkg, orc, cuda, K, N, bs, zp, Ms, eps):
     import torch
