@@ -35,6 +35,7 @@ def _no_alloc(pkg, op, A, cols):
     (4096, 1024, 128, True, (300, 8), 0),     # GEMM, then the MFMA decode (partials)
     (2048, 768, 32, False, (16, 1), 0),       # MFMA decode, then the M = 1 GEMV
     (1024, 512, 64, True, (40, 17), 1),       # exact route (groups of 16) twice
+    (4096, 4096, 128, False, (64, 32), 0),    # small-M GEMM: image + K-split partials, then own conversion
 ])
 def test_no_alloc_matches_run_with_workspace(pkg, orc, cuda, K, N, bs, zp, Ms, level):
     import torch
