@@ -88,3 +88,19 @@ def test_duplicated_rows_give_duplicated_outputs(pkg, cuda, cfg, M):
     Y = run(A2)
     op.release()
     np.testing.assert_array_equal(Y[half:], Y[:half])
+
+
+@pytest.mark.parametrize("cfg,M", [("c1", 1), ("c2", 1), ("c2", 4), ("c3", 2), ("c2", 16),
+                                   ("c4", 32), ("c4", 2048)])
+def test_zero_activations_and_zero_scales_give_zeros(pkg, cuda, cfg, M):
+    """Zero activations, or all-zero block scales, give exactly zero in every
+    output (no NaN from a zero row's exponent, no residue from the zero-point
+    term), on the kernel the automatic path picks."""
+    p, B, S, Z, A = _config(pkg, cfg, M)
+    op, run = _runner(pkg, cuda, p, B, S, Z)
+    print(f"case zeros {cfg} M={M} kernel={op.kernel_name(M)}", flush=True)
+    np.testing.assert_array_equal(run(np.zeros_like(A)), np.zeros((M, p.N), np.float32))
+    op.release()
+    op, run = _runner(pkg, cuda, p, B, np.zeros_like(S), Z)
+    np.testing.assert_array_equal(run(A), np.zeros((M, p.N), np.float32))
+    op.release()
