@@ -47,8 +47,10 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // LDS layout: two slice buffers of MT * 512 float4 (per token 64 chunks of 8
-// float4, float4 v of chunk c stored at c * 8 + (v ^ (c & 7))), then per
-// wavefront its R * nb pairs (scale, zp), plus 4 spare pairs.
+// float4, float4 v of chunk c stored at c * 8 + (v ^ ((c ^ c >> 3) & 7))),
+// then per wavefront its R * nb pairs (scale, zp), plus 4 spare pairs. In the
+// token loop lanes l and l + 8 read chunks 1 KiB apart; an XOR by c & 7 alone
+// would leave their reads in the same banks.
 __host__ __device__ inline size_t SliceF4(int mt) { return static_cast<size_t>(mt) * 512; }
 inline size_t LdsBytes(int mt, int waves, int R, int64_t nb) {
   return 2 * SliceF4(mt) * 16 + (static_cast<size_t>(waves) * R * nb + 4) * 8;
@@ -103,7 +105,7 @@ __device__ __forceinline__ void DotHalf(const float *a, const uint32_t *hz, int 
 // Slice i of A: MT * 512 float4, thread t of the W-wavefront workgroup holds
 // slots s = 64 W p + t (W divides 8 MT):
 // token s / 512, chunk 64 i + (s / 8) % 64 (clamped to the last chunk),
-// float4 v = s % 8 of it; stored at LDS slot (token, chunk c, v ^ (c & 7)).
+// float4 v = s % 8 of it; stored at LDS slot (token, chunk c, v ^ ((c ^ c >> 3) & 7)).
 template <int MT, int W>
 __device__ __forceinline__ void LoadSlice(f32x4 (&st)[MT * 8 / W], const f32x4 *a4, int K4, int i,
                                           int nchunks) {
@@ -122,7 +124,7 @@ __device__ __forceinline__ void StoreSlice(const f32x4 (&st)[MT * 8 / W], float4
   for (int p = 0; p < MT * 8 / W; ++p) {
     const int sl = 64 * W * p + threadIdx.x;
     const int m = sl >> 9, cl = (sl >> 3) & 63, v = sl & 7;
-    dst[m * 512 + cl * 8 + (v ^ (cl & 7))] = st[p];
+    dst[m * 512 + cl * 8 + (v ^ ((cl ^ (cl >> 3)) & 7))] = st[p];
   }
 }
 
@@ -200,7 +202,7 @@ __global__ __launch_bounds__(64 * W) void GemvSmallMKernel(const float *__restri
   // (A into registers, then weights), the token loop from LDS and registers,
   // then slice i + 1 into the other LDS buffer and the barrier that
   // publishes it.
-  const int sw = lane & 7;
+  const int sw = (lane ^ (lane >> 3)) & 7;  // chunk lane's slot swizzle
   auto step = [&](int i, int b, const uint4 *cur, uint4 *nxt) __attribute__((always_inline)) {
     const int c = 64 * i + lane;
     const int blk = min(c, nchunks - 1) >> chunk_shift;
