@@ -878,6 +878,7 @@ int mnb_kernel_workspace_bytes(const mnb_plan *plan, int64_t M, int kernel, int 
     if (p0 <= 0) *bytes = std::max(*bytes, mnb::GemmWorkspaceBytes(w, M));
     return MNB_OK;
   case MNB_KERNEL_STREAM:
+    if (!mnb::StreamShapeOk(w, M, p0, p1)) return MNB_ERR_UNSUPPORTED;
     *bytes = mnb::StreamWorkspaceBytes(w, M, p0, p1);
     return MNB_OK;
   case MNB_KERNEL_GEMV_M1:

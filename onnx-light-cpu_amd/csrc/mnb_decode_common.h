@@ -31,6 +31,55 @@ __device__ __forceinline__ float MixHi0(float a, uint32_t h) {
   return r;
 }
 
+// The reference engine's fp32 product of one activation row with one weight
+// row: each weight dequantized on its own, w = float(q - zp) * scale, and
+// acc = acc + a * w with the product rounded, k ascending (MatMulPlan<float>
+// over the dequantized weights, onnx_light_cpu/impl/math/gemm_kernel.cc:
+// 1208-1258). The fast decode kernels apply the zero point through each
+// block's activation sum (y += scale (sum a q - zp sum a)), so an infinite
+// activation meets inf - inf there and gives NaN where the reference gives
+// +-inf (NaN only where q == zp or the signs differ). Each kernel therefore
+// recomputes an output whose fast result is not finite with this function;
+// finite activations never take it unless the fast sum overflows, and then
+// the reference's own overflow is the answer. One thread reads the whole
+// row: slow, and only on non-finite outputs.
+//   nib(k8)  -> the packed word of nibbles k = 8 k8 .. 8 k8 + 7 (low first)
+//   blk(b)   -> float2(scale, zero point) of block b
+template <class Nibbles, class Block>
+__device__ __forceinline__ float ReferenceRowDot(const float *__restrict__ a, int K, int log2_bs,
+                                                 Nibbles nib, Block blk) {
+#pragma clang fp contract(off)
+  float acc = 0.0f;
+  for (int k8 = 0; k8 < (K >> 3); ++k8) {
+    const uint32_t word = nib(k8);
+    const float2 sz = blk((k8 << 3) >> log2_bs);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float w = static_cast<float>(static_cast<int>((word >> (4 * i)) & 0xFu) -
+                                         static_cast<int>(sz.y)) *
+                      sz.x;
+      const float p = a[8 * k8 + i] * w;
+      acc = acc + p;
+    }
+  }
+  return acc;
+}
+
+// ReferenceRowDot over one weight row in the MatMulNBits layout: its packed
+// nibbles brow (4-byte aligned), block scales srow and packed zero points
+// zrow (nullptr: 8).
+__device__ __forceinline__ float ReferenceRowDotPlain(const float *__restrict__ a, int K,
+                                                      int log2_bs, const uint8_t *brow,
+                                                      const float *srow, const uint8_t *zrow) {
+  return ReferenceRowDot(
+      a, K, log2_bs, [&](int k8) { return *reinterpret_cast<const uint32_t *>(brow + 4 * k8); },
+      [&](int b) {
+        const float zp =
+            zrow != nullptr ? static_cast<float>((zrow[b >> 1] >> (4 * (b & 1))) & 0xFu) : 8.0f;
+        return make_float2(srow[b], zp);
+      });
+}
+
 template <int CTRL>
 __device__ __forceinline__ float DppAdd(float v) {
   const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false);

@@ -1487,15 +1487,21 @@ size_t StreamWorkspaceBytes(const WeightView &w, int64_t M, int segs, int spw) {
   return AImageBytes(w, M) + RowExpBytes(M) + StreamPartialBytes(w, M, sh.segs);
 }
 
+// The epilogue finishes fragments wave, wave + wpg, ... up to TG of them per
+// wavefront, so it needs wpg >= 4 to reach all 4 TG; at most 8 wavefronts.
+bool StreamShapeOk(const WeightView &w, int64_t M, int segs, int spw) {
+  const StreamShape sh = PickStreamShape(w, segs, spw);
+  return StreamSupportsM(w, M) && sh.segs >= 1 && sh.segs <= kMaxSplits && sh.wpg >= 4 &&
+         sh.wpg <= 8 && sh.segs * sh.wpg * sh.spw == w.K / 32;
+}
+
 // ConvertA (64-row tiling), the streaming kernel, and the ordered reduction
 // of the segments' partial sums when K is split.
 hipError_t LaunchStream(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                         hipStream_t s, float *H, const float *gamma, float eps, const float *bias,
                         int segs, int spw) {
   const StreamShape sh = PickStreamShape(w, segs, spw);
-  if (!StreamSupportsM(w, M) || sh.segs < 1 || sh.wpg < 1 || sh.wpg > 8 || sh.segs > kMaxSplits ||
-      sh.segs * sh.wpg * sh.spw != w.K / 32)
-    return hipErrorInvalidValue;
+  if (!StreamShapeOk(w, M, segs, spw)) return hipErrorInvalidValue;
   uint4 *Ah = static_cast<uint4 *>(work);
   int *row_exp = reinterpret_cast<int *>(static_cast<char *>(work) + AImageBytes(w, M));
   float *P = reinterpret_cast<float *>(static_cast<char *>(work) + AImageBytes(w, M) +

@@ -17,7 +17,7 @@
 // conversion per nibble and no per-nibble zero-point subtraction. The A chunk
 // and its sum are loaded once and reused for all R rows. A 64-lane butterfly
 // reduces each accumulator at the end.
-#include "mnb_kernels.h"
+#include "mnb_decode_common.h"
 
 namespace mnb {
 namespace {
@@ -136,8 +136,20 @@ __global__ __launch_bounds__(256) void GemvKernel(const float *__restrict__ A,
     for (int r = 0; r < R; ++r) {
       if (n0 + r < N) {
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-          if (m < M) Y[static_cast<size_t>(m) * N + n0 + r] = acc[r][m];
+        for (int m = 0; m < MT; ++m) {
+          if (m < M) {
+            float y = acc[r][m];
+            // A non-finite activation: the reference's +-inf / NaN (the
+            // zero point applied through asum gives inf - inf = NaN).
+            if (!__builtin_isfinite(y)) {
+              const size_t n = static_cast<size_t>(n0 + r);
+              y = dec::ReferenceRowDotPlain(A + static_cast<size_t>(m) * K, K, chunk_shift + 5,
+                                            B + n * row_bytes, S + n * nb,
+                                            HAS_ZP ? Z + n * zp_row_bytes : nullptr);
+            }
+            Y[static_cast<size_t>(m) * N + n0 + r] = y;
+          }
+        }
       }
     }
   }

@@ -369,6 +369,29 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     for (int w = 1; w < waves; ++w) y += red[(w * MT + m) * 64 + r];
     if constexpr (RMS) y *= inv_rms;
     const int n = 64 * g + r;
+    if constexpr (!RMS) {
+      // A non-finite activation: the reference's +-inf / NaN (see
+      // ReferenceRowDot). Row r of the group is slice j = r >> 4, lane
+      // column r & 15 of the fragment-ordered records.
+      if (!__builtin_isfinite(y) && n < N) {
+        constexpr int kLog2Bs = 5 + (SPB == 1 ? 0 : (SPB == 2 ? 1 : (SPB == 4 ? 2 : 3)));
+        const int j = r >> 4, cc = r & 15;
+        const uint8_t *grp = Bp + static_cast<size_t>(g) * T * 1024;
+        const float *sg = Sd + static_cast<size_t>(g) * nb * 64;
+        const uint32_t *zg = HAS_ZP ? Zd + static_cast<size_t>(g) * nb * 16 : Zd;
+        y = ReferenceRowDot(
+            A + static_cast<size_t>(m) * K, K, kLog2Bs,
+            [&](int k8) {
+              return *reinterpret_cast<const uint32_t *>(grp + (k8 >> 2) * 1024 +
+                                                         16 * ((k8 & 3) * 16 + cc) + 4 * j);
+            },
+            [&](int b) {
+              const float zp = HAS_ZP ? static_cast<float>((zg[b * 16 + cc] >> (8 * j)) & 0xFFu)
+                                      : 8.0f;
+              return make_float2(sg[b * 64 + cc * 4 + j], zp);
+            });
+      }
+    }
     if (H != nullptr) {
       // gate/up pairs: rows 2 n', 2 n' + 1 in lanes r, r ^ 1 (N even)
       const float other = PairSwap(y);

@@ -355,6 +355,14 @@ __global__ __launch_bounds__(1024) void GemvM1Kernel(const float *__restrict__ A
     mine = lane == r ? t : mine;
   }
   if constexpr (RMS) mine *= inv_rms;
+  if constexpr (!RMS) {
+    // A non-finite activation: the reference's +-inf / NaN (see ReferenceRowDot).
+    if (lane < R && wr0 + lane < rows && !__builtin_isfinite(mine)) {
+      const size_t n = static_cast<size_t>(row0 + wr0 + lane);
+      mine = ReferenceRowDotPlain(A, K, chunk_shift + 5, B + n * row_bytes, S + n * nb,
+                                  HAS_ZP ? Z + n * zp_row_bytes : nullptr);
+    }
+  }
   if (H != nullptr) {
     // Gate/up pairs: band row 2n is a gate, 2n + 1 its up (R and G even, so a
     // pair never straddles wavefronts or bands).

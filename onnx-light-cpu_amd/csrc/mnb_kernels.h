@@ -211,6 +211,9 @@ bool PrefillSupports(const WeightView &w, int64_t M);
 // Adds `bias` itself.
 bool StreamSupports(const WeightView &w, int64_t M);
 size_t StreamWorkspaceBytes(const WeightView &w, int64_t M, int segs, int spw);
+// Whether (segs, spw) gives a launch the kernel serves (4 to 8 wavefronts per
+// workgroup, whole steps per wavefront).
+bool StreamShapeOk(const WeightView &w, int64_t M, int segs, int spw);
 hipError_t LaunchStream(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                         hipStream_t s, float *H, const float *gamma, float eps, const float *bias,
                         int segs, int spw);
