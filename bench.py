@@ -126,7 +126,18 @@ def time_graph(torch, launches, steps, warmup, stream):
     wall = time.perf_counter() - t0
     per = [marks[i].elapsed_time(marks[i + 1]) for i in range(steps)]
     q = statistics.quantiles(per, n=4) if steps >= 2 else [per[0], per[0], per[0]]
+    SAMPLES.append(per)
     return marks[0].elapsed_time(marks[steps]) / steps, wall, statistics.median(per), q[2] - q[0]
+
+
+# Per-step ms of every time_graph call, in call order: each leg takes the
+# samples of its own timed region from here (last_samples) into its record.
+SAMPLES = []
+
+
+def last_samples(per_step_divisor=1.0):
+    """The raw per-step samples of the last timed region, in us per launch."""
+    return [round(v * 1e3 / per_step_divisor, 4) for v in SAMPLES[-1]]
 
 
 def copy_leg(torch, dev, steps, warmup, stream):
@@ -162,13 +173,71 @@ def stream_ceiling_leg(torch, pkg, dev, nbytes, steps, warmup, stream):
             if rc != 0:
                 raise RuntimeError(f"mnb_stream_read: status {rc}")
 
-    ms, _, _, _ = time_graph(torch, launches, steps, warmup, stream)
+    ms, _, med, _ = time_graph(torch, launches, steps, warmup, stream)
     us = ms * 1e3 / rot
     del bufs
     torch.cuda.empty_cache()
     return {"kernel": "StreamReadKernel (mnb_stream_read)", "bytes_per_launch": nbytes,
-            "rotation_copies": rot, "us_per_launch": us, "GBps": nbytes / (us * 1e-6) / 1e9,
+            "rotation_copies": rot, "us_per_launch": us, "us_per_launch_median": med * 1e3 / rot,
+            "us_per_launch_samples": last_samples(rot), "GBps": nbytes / (us * 1e-6) / 1e9,
             "frac_of_peak": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
+def launch_floor_leg(torch, pkg, dev, steps, warmup, stream, launches_per_step=35):
+    """The fixed cost of one graph-replayed launch: mnb_stream_read over 1 KiB
+    (the ceiling kernel's grid, 2048 wavefronts, almost no loads), replayed
+    back to back like the decode legs' rotated launches."""
+    import ctypes
+    buf = torch.zeros(1024, dtype=torch.uint8, device=dev)
+    out = torch.empty(2048, dtype=torch.int32, device=dev)
+    L = pkg.library()
+
+    def launches():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for _ in range(launches_per_step):
+            rc = L.mnb_stream_read(ctypes.c_void_p(buf.data_ptr()), buf.numel(),
+                                   ctypes.c_void_p(out.data_ptr()), out.numel(), st)
+            if rc != 0:
+                raise RuntimeError(f"mnb_stream_read: status {rc}")
+
+    ms, _, med, iqr = time_graph(torch, launches, steps, warmup, stream)
+    return {"kernel": "StreamReadKernel (mnb_stream_read, 1 KiB)",
+            "launches_per_step": launches_per_step,
+            "us_per_launch": ms * 1e3 / launches_per_step,
+            "us_per_launch_median": med * 1e3 / launches_per_step,
+            "us_per_launch_samples": last_samples(launches_per_step)}
+
+
+def gpu_metadata(torch, dev):
+    """The device and software the run measured: gfx arch, CUs, memory, L2,
+    HIP runtime and driver versions, current clocks (rocm-smi)."""
+    import ctypes
+    pr = torch.cuda.get_device_properties(dev)
+    md = {"name": pr.name, "gcnArchName": getattr(pr, "gcnArchName", None),
+          "compute_units": pr.multi_processor_count, "total_memory_bytes": pr.total_memory,
+          "L2_cache_bytes": getattr(pr, "L2_cache_size", None),
+          "clock_rate_khz": getattr(pr, "clock_rate", None),
+          "torch": torch.__version__, "torch_hip": torch.version.hip}
+    try:
+        path = next(line.split()[-1] for line in open("/proc/self/maps")
+                    if "libamdhip64" in line)
+        hip = ctypes.CDLL(path)
+        v = ctypes.c_int()
+        if hip.hipRuntimeGetVersion(ctypes.byref(v)) == 0:
+            md["hip_runtime_version"] = v.value
+        if hip.hipDriverGetVersion(ctypes.byref(v)) == 0:
+            md["hip_driver_version"] = v.value
+    except (OSError, StopIteration, AttributeError) as e:
+        md["hip_versions_error"] = str(e)
+    try:
+        r = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True,
+                           text=True, timeout=30)
+        clocks = json.loads(r.stdout) if r.returncode == 0 else {}
+        md["clocks_after_run"] = {card: {k: v for k, v in vals.items() if "clk" in k.lower()}
+                        for card, vals in clocks.items() if isinstance(vals, dict)}
+    except (OSError, subprocess.SubprocessError, ValueError) as e:
+        md["clocks_error"] = str(e)
+    return md
 
 
 def fp16_gemm_reference(torch, dev, p, M, steps, warmup, stream):
@@ -192,6 +261,53 @@ def fp16_gemm_reference(torch, dev, p, M, steps, warmup, stream):
     return {"what": "torch.matmul fp16 x fp16 -> fp16 (hipBLASLt), dense weights",
             "calls_per_step": CALLS_PER_STEP,
             "us_per_launch": us, "TFLOPs": tflops, "frac_fp16_peak": tflops / FP16_PEAK_TFLOPS}
+
+
+DECODE_TOL, GEMM_TOL = 1e-5, 2e-3
+
+
+def reference_columns(torch, p, A, B, S, Z, cols):
+    """fp64 Y[:, cols] = A * W[cols]^T with W[n, k] = (q - zp) * scale from the
+    MatMulNBits definition (low nibble first, zero point 8 when absent),
+    computed with torch on the device from the weights the timed launches
+    read: an independent check of the timed kernels' output."""
+    n = cols.numel()
+    Bc = B[cols].reshape(n, -1)
+    q = torch.stack([Bc & 15, Bc >> 4], dim=-1).reshape(n, p.nb, p.block_size)
+    if Z is not None:
+        Zc = Z[cols]
+        z = torch.stack([Zc & 15, Zc >> 4], dim=-1).reshape(n, -1)[:, :p.nb]
+    else:
+        z = torch.full((n, p.nb), 8, dtype=torch.uint8, device=B.device)
+    w = (q.to(torch.float64) - z.to(torch.float64)[..., None]) * S[cols].to(torch.float64)[..., None]
+    return A.to(torch.float64) @ w.reshape(n, -1)[:, :p.K].T
+
+
+def validate(torch, p, A, weights, Y, path, ncols=512, seed=0):
+    """Checks a timed leg's output after timing (outside the timed region):
+    Y on ncols sampled weight rows (all of A's rows) against
+    reference_columns, at the path's bound: max|dy| / max|y| <= 1e-5 on the
+    decode path, ||dy||_2 / ||y||_2 <= 2e-3 on the fp16 GEMM."""
+    B, S, Z = weights
+    g = torch.Generator(device=Y.device)
+    g.manual_seed(seed)
+    cols = torch.randperm(p.N, device=Y.device, generator=g)[:min(ncols, p.N)]
+    ref = reference_columns(torch, p, A, B, S, Z, cols)
+    got = Y[:, cols].to(torch.float64)
+    if path == 2:
+        err = float(torch.linalg.vector_norm(got - ref) / torch.linalg.vector_norm(ref))
+        tol, metric = GEMM_TOL, "l2 relative"
+    else:
+        err = float((got - ref).abs().max() / ref.abs().max())
+        tol, metric = DECODE_TOL, "normwise max"
+    ok = bool(err <= tol) and bool(torch.isfinite(got).all())
+    if not ok:
+        FAILED_CHECKS.append(f"{p.name} M={A.shape[0]}: {metric} error {err:.3e} > {tol}")
+    return {"checked": f"{A.shape[0]} rows x {cols.numel()} sampled columns vs fp64 torch "
+                       f"reference", "metric": metric, "error": err, "tolerance": tol, "ok": ok}
+
+
+FAILED_CHECKS = []
 
 
 def plan_create_leg(torch, pkg, dev):
@@ -251,8 +367,11 @@ def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
             op(A, out=Y, stream=torch.cuda.current_stream())
 
     ms, wall, med, iqr = time_graph(torch, launches, steps, warmup, stream)
+    samples = last_samples(rot)
     per_launch_us = ms * 1e3 / rot
     nbytes = p.algorithmic_bytes(M)
+    # the last launch of a step wrote Y with the last weight copy
+    check = validate(torch, p, A, sets[-1], Y, path, seed=seed)
     for op in ops:
         op.release()
     del sets
@@ -262,10 +381,11 @@ def decode_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
         "zero_points": p.has_zero_points, "path": path, "kernel": kernel,
         "rotation_copies": rot,
         "us_per_launch": per_launch_us, "us_per_launch_median": med * 1e3 / rot,
-        "us_per_launch_iqr": iqr * 1e3 / rot, "bytes_per_launch": nbytes,
+        "us_per_launch_iqr": iqr * 1e3 / rot, "us_per_launch_samples": samples,
+        "bytes_per_launch": nbytes,
         "GBps": nbytes / (per_launch_us * 1e-6) / 1e9, "ms_per_step": ms, "wall_s": wall,
         "wall_ms_per_step": wall * 1e3 / steps,
-        "launches_per_step": rot,
+        "launches_per_step": rot, "validation": check,
     }
 
 
@@ -288,16 +408,18 @@ def gemm_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
             op(A, out=Y, stream=torch.cuda.current_stream())
 
     ms, wall, med, iqr = time_graph(torch, launches, steps, warmup, stream)
+    samples = last_samples(CALLS_PER_STEP)
     us = ms * 1e3 / CALLS_PER_STEP
     flops = p.flops(M)
     tflops = flops / (us * 1e-6) / 1e12
     res = {"K": p.K, "N": p.N, "M": M, "block_size": p.block_size, "path": op.select_path(M),
            "kernel": op.kernel_name(M), "calls_per_step": CALLS_PER_STEP,
            "us_per_launch": us, "us_per_launch_median": med * 1e3 / CALLS_PER_STEP,
-           "us_per_launch_iqr": iqr * 1e3 / CALLS_PER_STEP,
+           "us_per_launch_iqr": iqr * 1e3 / CALLS_PER_STEP, "us_per_launch_samples": samples,
            "TFLOPs": tflops, "frac_fp16_peak": tflops / FP16_PEAK_TFLOPS,
            "bytes_per_launch": p.algorithmic_bytes(M), "wall_s": wall,
-           "wall_ms_per_step": wall * 1e3 / steps}
+           "wall_ms_per_step": wall * 1e3 / steps,
+           "validation": validate(torch, p, A, sets[0], Y, op.select_path(M), seed=seed)}
     op.release()
     return res
 
@@ -315,14 +437,46 @@ def gate_up_leg(torch, pkg, dev, Ms, steps, warmup, stream):
     K, I, bs = 4096, 14336, 128
     p = W.Projection("gate_up", K, I, bs, True, 1.0, 0.005, 0.02)
     copies = 4 if min(Ms) <= 16 else 1
-    fused, plain = [], []
+    fused, plain, host = [], [], []
     for c in range(copies):
         Bg, Sg, Zg = W.make_weights(p, 1000 + 2 * c)
         Bu, Su, Zu = W.make_weights(p, 1001 + 2 * c)
+        host.append(((Bg, Sg, Zg), (Bu, Su, Zu)))
         fused.append(pkg.GateUpSiLU(K, I, 4, bs).prepare(Bg, Sg, Zg, Bu, Su, Zu))
         cat = [np.concatenate([x.reshape(I, -1), y.reshape(I, -1)])
                for x, y in ((Bg, Bu), (Sg, Su), (Zg, Zu))]
         plain.append(pkg.MatMulNBits(K, 2 * I, 4, bs).prepare(*cat))
+
+    def check(M, A, out_t, c, what):
+        # H (or [g | u]) of weight copy c on sampled columns against fp64
+        rng = np.random.default_rng(M)
+        cols = np.sort(rng.choice(I, 256, replace=False))
+        dev_rows = lambda w: tuple(torch.from_numpy(np.ascontiguousarray(x[cols])).to(dev)
+                                   for x in w)
+        idx = torch.arange(cols.size, device=dev)
+        q = W.Projection("gate_up", K, cols.size, bs, True)
+        gr = reference_columns(torch, q, A, *dev_rows(host[c][0]), idx)
+        ur = reference_columns(torch, q, A, *dev_rows(host[c][1]), idx)
+        if what == "plain":
+            ref = torch.cat([gr, ur], dim=1)
+            got = torch.cat([out_t[:, torch.from_numpy(cols).to(dev)],
+                             out_t[:, torch.from_numpy(cols + I).to(dev)]], dim=1)
+        else:
+            ref = gr * torch.sigmoid(gr) * ur
+            got = out_t[:, torch.from_numpy(cols).to(dev)]
+        got = got.to(torch.float64)
+        if M > 16:
+            err = float(torch.linalg.vector_norm(got - ref) / torch.linalg.vector_norm(ref))
+            tol, metric = GEMM_TOL, "l2 relative"
+        else:
+            err = float((got - ref).abs().max() / ref.abs().max())
+            # two products within 1e-5 each, composed through silu
+            tol, metric = (4 * DECODE_TOL if what != "plain" else DECODE_TOL), "normwise max"
+        ok = err <= tol and bool(torch.isfinite(got).all())
+        if not ok:
+            FAILED_CHECKS.append(f"gate_up {what} M={M}: {metric} error {err:.3e} > {tol}")
+        return {"metric": metric, "error": err, "tolerance": tol, "ok": ok}
+
     out = []
     for M in Ms:
         n = copies if M <= 16 else 1
@@ -346,11 +500,14 @@ def gate_up_leg(torch, pkg, dev, Ms, steps, warmup, stream):
                 op(A, out=Y, stream=torch.cuda.current_stream())
                 torch.mul(F.silu(Y[:, :I]), Y[:, I:], out=H)
 
-        r = {"M": M, "weight_copies": n, "calls_per_step": n * reps}
-        for name, fn in (("fused_us", run_fused), ("unfused_us", run_unfused),
-                         ("matmul_only_us", run_plain)):
+        r = {"M": M, "weight_copies": n, "calls_per_step": n * reps, "validation": {}}
+        for name, fn, what, res in (("fused_us", run_fused, "fused", H),
+                                    ("unfused_us", run_unfused, "unfused", H),
+                                    ("matmul_only_us", run_plain, "plain", Y)):
             ms, _, _, _ = time_graph(torch, fn, steps, warmup, stream)
             r[name] = ms * 1e3 / (n * reps)
+            r[name.replace("_us", "_samples_us")] = last_samples(n * reps)
+            r["validation"][what] = check(M, A, res, n - 1, what)
         r["gain"] = r["unfused_us"] / r["fused_us"]
         out.append(r)
     for op in fused + plain:
@@ -396,11 +553,18 @@ def rmsnorm_leg(torch, pkg, dev, Ms, steps, warmup, stream):
             for op in ops[:n] * reps:
                 op(X, out=Y, stream=torch.cuda.current_stream())
 
-        r = {"M": M, "weight_copies": n, "calls_per_step": n * reps}
-        for name, fn in (("fused_us", run_fused), ("unfused_us", run_unfused),
-                         ("matmul_only_us", run_plain)):
+        # fp64 RMSNorm of X, the input the fused and unfused runs multiply
+        X64 = X.to(torch.float64)
+        Xn64 = X64 / torch.sqrt((X64 * X64).mean(dim=1, keepdim=True) + eps) * gamma.to(torch.float64)
+        path = ops[0].select_path(M)
+        r = {"M": M, "weight_copies": n, "calls_per_step": n * reps, "validation": {}}
+        for name, fn, inp in (("fused_us", run_fused, Xn64), ("unfused_us", run_unfused, Xn64),
+                              ("matmul_only_us", run_plain, X64)):
             ms, _, _, _ = time_graph(torch, fn, steps, warmup, stream)
             r[name] = ms * 1e3 / (n * reps)
+            r[name.replace("_us", "_samples_us")] = last_samples(n * reps)
+            r["validation"][name[:-3]] = validate(torch, p, inp, sets[n - 1], Y, path,
+                                                  ncols=256, seed=M)
         r["gain"] = r["unfused_us"] / r["fused_us"]
         out.append(r)
     for op in ops:
@@ -434,10 +598,18 @@ def c5_leg(torch, pkg, dev, M, steps, warmup, stream):
             op(acts[p.K], out=outs[p.N], stream=torch.cuda.current_stream())
 
     ms, wall, med, iqr = time_graph(torch, launches, steps, warmup, stream)
+    samples = [round(v, 5) for v in SAMPLES[-1]]
+    # each output buffer holds the last layer's projection of its width
+    last = {}
+    for (p, op), s in zip(ops, sets):
+        last[p.N] = (p, op, s[0])
+    checks = [validate(torch, p, acts[p.K], w, outs[N], op.select_path(M), ncols=256, seed=N)
+              for N, (p, op, w) in sorted(last.items())]
     nbytes = sum(p.algorithmic_bytes(M) for p, _ in ops)
     flops = sum(p.flops(M) for p, _ in ops)
     res = {"M": M, "layers": c.layers, "launches_per_step": len(ops), "ms_per_step": ms,
-           "ms_per_step_median": med, "ms_per_step_iqr": iqr,
+           "ms_per_step_median": med, "ms_per_step_iqr": iqr, "ms_per_step_samples": samples,
+           "validation": checks,
            "us_per_launch": ms * 1e3 / len(ops), "bytes_per_step": nbytes,
            "flops_per_step": flops, "GBps": nbytes / (ms * 1e-3) / 1e9,
            "TFLOPs": flops / (ms * 1e-3) / 1e12, "wall_ms_per_step": wall * 1e3 / steps}
@@ -558,7 +730,8 @@ def main():
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(device=dev)
     legs = (set(args.only.split(",")) if args.only
-            else {"decode", "ceiling", "gemm", "sweep", "c5", "gate_up", "rmsnorm", "plan", "cpu"})
+            else {"decode", "ceiling", "gemm", "sweep", "lm_head", "c5", "gate_up", "rmsnorm",
+                  "plan", "cpu"})
     W = pkg.workloads
 
     t_start = time.perf_counter()
@@ -610,6 +783,15 @@ def main():
                                                  "us_per_launch_iqr", "GBps", "path", "kernel")})
                 print(f"# decode {cname} M={M}: {r['us_per_launch']:.2f} us, {r['GBps']:.0f} GB/s",
                       file=sys.stderr, flush=True)
+    lm_head = None
+    if "lm_head" in legs:
+        # Llama-3-8B's LM head at decode: the one decode launch large enough
+        # (281 MB) for the kernel's streaming rate to dominate its fixed cost
+        p = W.Projection("lm_head", 4096, 128256, 128, True)
+        lm_head = decode_leg(torch, pkg, dev, p, 1, max(3, args.steps // 4), 2, 23, stream)
+        lm_head["frac_hbm"] = lm_head["GBps"] / HBM_PEAK_GBS
+        print(f"# decode LM head M=1: {lm_head['us_per_launch']:.2f} us, "
+              f"{lm_head['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
     c5 = []
     if "c5" in legs:
         for M in (1, 512):
@@ -632,13 +814,24 @@ def main():
             print(f"# RMSNorm + qkv M={r['M']}: fused {r['fused_us']:.1f} us, unfused "
                   f"{r['unfused_us']:.1f} us ({r['gain']:.2f}x), matmul alone "
                   f"{r['matmul_only_us']:.1f} us", file=sys.stderr, flush=True)
-    ceiling = None
-    if "ceiling" in legs and head is not None:
-        ceiling = stream_ceiling_leg(torch, pkg, dev, head["bytes_per_launch"], args.steps,
-                                     args.warmup, stream)
-        print(f"# read ceiling, {ceiling['bytes_per_launch']} B per launch: "
-              f"{ceiling['us_per_launch']:.2f} us, {ceiling['GBps']:.0f} GB/s",
-              file=sys.stderr, flush=True)
+    ceiling, ceilings, floor = None, [], None
+    if "ceiling" in legs:
+        # plain-read ceilings of one launch at the decode shapes' byte counts,
+        # and the fixed cost of a launch
+        sizes = [("c2 M=1", W.CONFIGS["c2"].projections[0].algorithmic_bytes(1)),
+                 ("c1 M=1", W.CONFIGS["c1"].projections[0].algorithmic_bytes(1)),
+                 ("c3 M=1", W.CONFIGS["c3"].projections[0].algorithmic_bytes(1)),
+                 ("LM head M=1", W.Projection("lm_head", 4096, 128256, 128, True)
+                  .algorithmic_bytes(1))]
+        for name, nbytes in sizes:
+            r = stream_ceiling_leg(torch, pkg, dev, nbytes, args.steps, args.warmup, stream)
+            r["for"] = name
+            ceilings.append(r)
+            print(f"# read ceiling {name}, {nbytes} B per launch: {r['us_per_launch']:.2f} us, "
+                  f"{r['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
+        ceiling = ceilings[0]
+        floor = launch_floor_leg(torch, pkg, dev, args.steps, args.warmup, stream)
+        print(f"# launch floor: {floor['us_per_launch']:.2f} us", file=sys.stderr, flush=True)
     plans = []
     if "plan" in legs:
         plans = plan_create_leg(torch, pkg, dev)
@@ -668,6 +861,7 @@ def main():
                 "us_per_launch_median": head["us_per_launch_median"],
                 "us_per_launch_iqr": head["us_per_launch_iqr"],
                 "bytes_per_launch": head["bytes_per_launch"]}
+        roof["validation"] = head["validation"]
         if ceiling is not None:
             roof["ceiling"] = ceiling["frac_of_peak"]
             roof["ceiling_GBps"] = ceiling["GBps"]
@@ -690,13 +884,23 @@ def main():
         "c5_layer_stack": c5,
         "gate_up_fusion": gate_up,
         "read_ceiling": ceiling,
+        "read_ceilings": ceilings,
+        "launch_floor": floor,
+        "lm_head_decode": lm_head,
+        "headline_samples_us_per_launch": head["us_per_launch_samples"] if head else None,
         "plan_create": plans,
         "rmsnorm_fusion": rms,
         "copy_calibration": copy,
         "timing": "eager launches" if EAGER else "HIP graph replay",
+        "gpu": gpu_metadata(torch, dev),
+        "validation_failures": FAILED_CHECKS,
         "bench_wall_s": time.perf_counter() - t_start,
     }
     print(json.dumps(out), flush=True)
+    if FAILED_CHECKS:
+        print("bench.py: outputs of timed legs failed validation: " + "; ".join(FAILED_CHECKS),
+              file=sys.stderr, flush=True)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

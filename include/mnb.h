@@ -74,8 +74,13 @@ int mnb_plan_create(const mnb_desc *desc, const uint8_t *B, const float *scales,
                     const uint8_t *zero_points, mnb_plan **out_plan);
 
 /* Same as mnb_plan_create, but B, scales and zero_points are device pointers
- * on the current device that the plan borrows without copying: the caller
- * keeps them alive and unchanged for the plan's lifetime. */
+ * on the current device that the plan borrows: the caller keeps them alive
+ * and unchanged for the plan's lifetime. The call first waits for all work
+ * already issued on the device (hipDeviceSynchronize), so writes to the
+ * buffers on any stream must have been issued before it; it then derives the
+ * plan's own re-laid copies from the buffers' contents at that point (the
+ * kernels read those copies, so later changes to the buffers are not seen
+ * by every path). */
 int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float *dScales,
                            const uint8_t *dZeroPoints, mnb_plan **out_plan);
 
@@ -90,9 +95,11 @@ int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float 
  * creation (row 2n = gate row n, row 2n + 1 = up row n), so each pair meets
  * in one wavefront. mnb_run / mnb_run_path / mnb_run_ex on it write H
  * (M x N floats); bias is rejected (MNB_ERR_UNSUPPORTED). The workspace
- * (mnb_workspace_bytes) is required on every path: it starts with the
- * M x 2N fp32 sum for the kernels whose epilogue cannot apply the
- * activation (M = 2..4 and the fallbacks, followed by a separate pass). */
+ * (mnb_workspace_bytes) starts with the M x 2N fp32 sum that the kernels
+ * whose epilogue cannot apply the activation write (followed by a separate
+ * pass); it is required on every path except the decode path where the
+ * fragment-ordered M <= 4 GEMV serves the plan (its epilogue applies the
+ * activation). */
 int mnb_plan_create_gate_up(const mnb_desc *desc, const uint8_t *Bg, const float *Sg,
                             const uint8_t *Zg, const uint8_t *Bu, const float *Su,
                             const uint8_t *Zu, mnb_plan **out_plan);
@@ -107,10 +114,12 @@ int mnb_plan_destroy(mnb_plan *plan);
  *    (ceil(M/128)*128 int32, rounded up to 256 bytes), then, when the GEMM
  *    splits K into S > 1 parts, (S - 1)*M*N*4 bytes of fp32 partial sums
  *    (S <= 16, chosen from the shape);
- *  - where the MFMA decode kernel serves min(M, 16) rows (5 <= M <= 16, from
- *    M = 4 or 3 for wide weights, as mnb_run; the exact route serves larger M
- *    16 rows at a time), its (K/512 - 1)*min(M,16)*N*4 bytes of fp32 partial
- *    sums of its 512-k ranges.
+ *  - where an MFMA decode kernel with a workspace serves min(M, 16) rows
+ *    (5 <= M <= 16, from M = 4, 3 or 2 for wide weights, as mnb_run; the
+ *    exact route serves larger M 16 rows at a time), its split activation
+ *    image and fp32 partial sums (none where the fragment-ordered M <= 4
+ *    GEMV serves them);
+ *  - on a gate/up plan, plus the M x 2N fp32 scratch sum.
  * Without it (NULL or smaller) the decode path runs its fp32-FMA kernels. */
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
 
@@ -185,9 +194,10 @@ int mnb_run_rmsnorm(const mnb_plan *plan, int64_t M, const float *dX, const floa
  * address is looked up on the first call on each device). No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). Fails with MNB_ERR_WORKSPACE, before any launch, when
- * mnb_workspace_bytes(plan, M) exceeds the array (e.g. the prefill GEMM above
- * M * K * 2 of about 32 MiB, or a gate/up plan's M x 2N scratch sum). Every
+ * hipMalloc). Fails with MNB_ERR_WORKSPACE, before any launch, when the
+ * workspace of the kernels mnb_run would launch for these M rows (at most
+ * mnb_workspace_bytes(plan, M); e.g. the prefill GEMM above M * K * 2 of
+ * about 32 MiB, or a gate/up plan's M x 2N scratch sum) exceeds the array. Every
  * call on a GPU shares that GPU's array: calls that overlap in time on one
  * GPU (several streams or threads) race and must be ordered by the caller.
  * No kernel reads scratch bytes it did not write in the same call, so the

@@ -448,6 +448,15 @@ int mnb_plan_create_device(const mnb_desc *desc, const uint8_t *dB, const float 
   p->dB = const_cast<uint8_t *>(dB);
   p->dS = const_cast<float *>(dScales);
   p->dZ = const_cast<uint8_t *>(dZeroPoints);
+  // The derived copies are made once, on the null stream, which does not wait
+  // for non-blocking streams: every write to the borrowed buffers already
+  // issued on any stream of the device must land first.
+  const hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    SetLastError("hipDeviceSynchronize", e);
+    delete p;
+    return MNB_ERR_HIP;
+  }
   st = DerivePlanConstants(p);
   if (st != MNB_OK) {
     FreePlanMemory(p);
@@ -579,6 +588,23 @@ static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void
   return mnb::GemvSmallMSupports(plan->view, M) ? kDecSmallM : kDecGemv;
 }
 
+// Workspace bytes the decode kernel PickDecodeKernel chooses for M rows when
+// the caller passes enough: 0 for the kernels that need none.
+static size_t DecodeNeed(const mnb_plan *plan, int64_t M, bool rms = false) {
+  if (mnb::GemvFragPreferred(plan->view, M, rms)) return 0;
+  if (M == 1 && mnb::GemvM1Supports(plan->view)) return 0;
+  if (UsesFragDecode(plan, M)) return mnb::DecodeFragWorkspaceBytes(plan->view, M);
+  if (!mnb::DecodeFragSupports(plan->view, M) && UsesMfmaDecode(plan, M))
+    return mnb::GemvMfmaWorkspaceBytes(plan->view, M);
+  return 0;
+}
+
+// Whether a gate/up plan's run of M rows on `path` applies the activation in
+// the fragment-ordered GEMV's epilogue and so needs no scratch sum.
+static bool GateUpFusedInGemv(const mnb_plan *plan, int64_t M, int path, bool rms = false) {
+  return plan->gate_up && path == 1 && mnb::GemvFragPreferred(plan->view, M, rms);
+}
+
 
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
   if (plan == nullptr || bytes == nullptr) return MNB_ERR_NULL_POINTER;
@@ -589,16 +615,15 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
   // A gate/up plan adds the scratch sum in front of either.
   // The exact route (path 4) runs the decode kernels over groups of at most
   // 16 rows, one after another in the same workspace.
+  // Decode launches served by the fragment-ordered GEMV need none.
   size_t need = 0;
   if (M > 0 && mnb::GemmSupports(plan->view, M)) need = mnb::GemmWorkspaceBytes(plan->view, M);
   const int64_t md = std::min<int64_t>(M, kExactGroupRows);
-  if (UsesFragDecode(plan, md))
-    need = std::max(need, mnb::DecodeFragWorkspaceBytes(plan->view, md));
-  else if (!mnb::DecodeFragSupports(plan->view, md) && UsesMfmaDecode(plan, md))
-    need = std::max(need, mnb::GemvMfmaWorkspaceBytes(plan->view, md));
+  if (md > 0) need = std::max(need, DecodeNeed(plan, md));
   *bytes = need + GateUpScratchBytes(plan, M);
   return MNB_OK;
 }
+
 
 // accuracy_level is ONNX Runtime's MatMulNBits attribute: the lowest accuracy
 // at which A may enter the computation (0 unset, 1 fp32, 2 fp16, 3 bf16,
@@ -620,6 +645,23 @@ static int SelectPath(const mnb_plan *plan, int64_t M, const float *dA) {
   if (Fp32ActivationsOnly(plan)) return ExactGroupsSupported(plan, a_aligned) ? 4 : 3;
   if (a_aligned && mnb::GemmSupports(plan->view, M)) return 2;
   return 3;
+}
+
+// Workspace the automatic path (mnb_run) takes for M rows of dA: the chosen
+// kernel's own, plus a gate/up plan's scratch sum where its epilogue does not
+// apply the activation (the exact route: per group of 16 rows).
+static size_t AutoWorkspaceBytes(const mnb_plan *plan, int64_t M, const float *dA) {
+  const int path = SelectPath(plan, M, dA);
+  switch (path) {
+  case 1:
+    return DecodeNeed(plan, M) + (GateUpFusedInGemv(plan, M, 1) ? 0 : GateUpScratchBytes(plan, M));
+  case 2: return mnb::GemmWorkspaceBytes(plan->view, M) + GateUpScratchBytes(plan, M);
+  case 4: {
+    const int64_t md = std::min<int64_t>(M, kExactGroupRows);
+    return DecodeNeed(plan, md) + GateUpScratchBytes(plan, md);
+  }
+  default: return GateUpScratchBytes(plan, M);
+  }
 }
 
 int mnb_select_path(const mnb_plan *plan, int64_t M, int *path) {
@@ -664,12 +706,13 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   }
   // A gate/up plan's runs start with the scratch sum; the path's own
   // workspace follows it.
-  const size_t scratch = GateUpScratchBytes(plan, M);
+  const size_t scratch =
+      GateUpFusedInGemv(plan, M, path, gamma != nullptr) ? 0 : GateUpScratchBytes(plan, M);
   if (scratch > 0 && (dWorkspace == nullptr || workspace_bytes < scratch ||
                       (reinterpret_cast<uintptr_t>(dWorkspace) % 16) != 0))
     return MNB_ERR_WORKSPACE;
   float *Ys = scratch > 0 ? static_cast<float *>(dWorkspace) : dY;
-  float *H = scratch > 0 ? dY : nullptr;
+  float *H = plan->gate_up ? dY : nullptr;
   void *work = scratch > 0 ? static_cast<void *>(static_cast<char *>(dWorkspace) + scratch)
                            : dWorkspace;
   const size_t work_bytes = scratch > 0 ? workspace_bytes - scratch : workspace_bytes;
@@ -954,9 +997,8 @@ int mnb_run_no_alloc(const mnb_plan *plan, int64_t M, const float *dA, float *dY
   if (M < 0 || M > (int64_t{1} << 30)) return MNB_ERR_BAD_SHAPE;
   if (M == 0) return MNB_OK;
   if (dA == nullptr || dY == nullptr) return MNB_ERR_NULL_POINTER;
-  size_t need = 0;
-  int st = mnb_workspace_bytes(plan, M, &need);
-  if (st != MNB_OK) return st;
+  const size_t need = AutoWorkspaceBytes(plan, M, dA);
+  int st = MNB_OK;
   if (need > kScratchBytes) {
     std::snprintf(g_last_error, sizeof(g_last_error),
                   "mnb_run_no_alloc: %zu workspace bytes needed for M = %lld, the scratch holds %zu",

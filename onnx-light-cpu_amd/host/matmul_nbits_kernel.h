@@ -55,6 +55,13 @@ private:
 
   // The plan of these constant buffers, created once and never destroyed
   // before the kernel object (a run on another thread may be using it).
+  // Plans are keyed by the buffers' addresses and never evicted: the inputs
+  // must be constants that stay allocated and unchanged while the kernel
+  // object lives (a graph's initializers over a session). A buffer freed and
+  // reallocated at the same address would meet the plan derived from the old
+  // contents. Device buffers are read once, when the plan is created, after
+  // all work issued on the device so far has finished
+  // (mnb_plan_create_device).
   const mnb_plan *Plan(const TensorView &b, const TensorView &scales,
                        const TensorView *zero_points);
 

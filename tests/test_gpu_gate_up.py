@@ -110,3 +110,29 @@ def test_gate_up_generic_path_and_rejections(pkg, orc, cuda):
         op(dA, bias=bias)
     torch.cuda.synchronize()
     op.release()
+
+
+def test_gate_up_fused_gemv_needs_no_workspace(pkg, cuda):
+    """Where the fragment-ordered M <= 4 GEMV serves a gate/up plan, its
+    epilogue applies the activation, so the run needs no scratch sum: without
+    a workspace it gives the same H as with one, bit for bit."""
+    import torch
+    K, I, bs = 1024, 8192, 64  # 16384 interleaved rows: 256 groups of 64
+    (Bg, Sg, Zg), (Bu, Su, Zu) = _weights(pkg, K, I, bs, True, seed=17)
+    op = pkg.GateUpSiLU(K, I, 4, bs).prepare(Bg, Sg, Zg, Bu, Su, Zu)
+    L = pkg.library()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    try:
+        for M in (1, 2, 4):
+            print(f"case gate-up no workspace K={K} I={I} M={M} kernel={op.kernel_name(M)}",
+                  flush=True)
+            assert op.kernel_name(M).endswith("GemvFragKernel"), op.kernel_name(M)
+            dA = torch.from_numpy(pkg.workloads.make_activations(M, K, 1.0, seed=M)).to(cuda)
+            ref = op(dA).cpu().numpy()
+            out = torch.full((M, I), float("nan"), device=cuda)
+            assert L.mnb_run_ex(op._plan, M, P(dA), None, P(out), None, 0, stream, 0) == 0
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    finally:
+        op.release()
