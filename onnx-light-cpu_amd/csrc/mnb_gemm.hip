@@ -1368,13 +1368,15 @@ hipError_t LaunchStreamZp(const WeightView &w, int64_t M, const uint4 *Ah, const
   }
 }
 
-// Splits of a prefill launch: enough workgroups for one per CU when the
-// tiles alone do not fill the chip, each split at least 8 k-tiles long.
+// Splits of a prefill launch: as many as keep the workgroups within one per
+// CU when the tiles alone do not fill the chip (a second, partial wave costs
+// a whole k-loop), at most kPrefillMaxSplits, each split at least 8 k-tiles.
+constexpr int kPrefillMaxSplits = 8;
 inline int PrefillSplits(const WeightView &w, int64_t M) {
   const int64_t tiles = (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN);
   const int ktiles = static_cast<int>(w.K / kBK);
   int64_t splits = std::max<int64_t>(1, w.num_cus / tiles);
-  splits = std::min<int64_t>({splits, kMaxSplits, std::max(1, ktiles / 8)});
+  splits = std::min<int64_t>({splits, kPrefillMaxSplits, std::max(1, ktiles / 8)});
   const int per = static_cast<int>((ktiles + splits - 1) / splits);
   return (ktiles + per - 1) / per;
 }
@@ -1441,18 +1443,29 @@ bool PrefillSupportsM(const WeightView &w, int64_t M) {
          (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN) * kMaxSplits < (int64_t{1} << 31);
 }
 
-// The prefill kernel serves the automatic GEMM path when its 128 x 256 tiles
-// alone fill the CUs in whole waves (its last wave at least 85% full): then
-// it needs no split-K, and one workgroup per CU keeps every CU busy to the
-// end. Measured on MI355X (c4, c5 shapes): 10-17% faster than GemmKernel at
-// M = 2048 on c4, c5 o, gate+up and down; slower where split-K must supply
-// the workgroups (M = 512: 45 -> 68 us on c4) or a last wave is half empty
-// (c5 qkv at M = 2048, 1.5 waves: 146 -> 156 us), which GemmKernel keeps.
+// The prefill kernel serves the automatic GEMM path
+// - when its 128 x 256 tiles alone fill the CUs in whole waves (the last
+//   wave at least 85% full): no split-K, one workgroup per CU busy to the
+//   end; a half-empty last wave (c5 qkv at M = 2048, 1.5 waves: 146 against
+//   156 us) stays with GemmKernel;
+// - when they do not fill one wave, with K split (PrefillSplits) as long as
+//   each split keeps at least 12 k-tiles (shorter splits spend most of their
+//   time in the prologue and the epilogue).
+// Measured on MI355X (us per call, GemmKernel's best shape against the
+// prefill kernel with PrefillSplits): M = 2048 c4, c5 o, gate+up, down
+// 10-17% faster; M = 1024 c5 qkv 81.5 -> 61.8, o 61.8 -> 52.8, down
+// 162.7 -> 125.9, c4 60.2 -> 52.6; M = 512 qkv 55.1 -> 46.3, down 96.4 ->
+// 77.2, o and c4 within 3%; M = 256 gate+up 84.8 -> 63.8, qkv 34.6 -> about
+// 32, down 56.8 -> 50.0; with fewer than 12 k-tiles per split (o and c4 at
+// M <= 256, qkv at M = 128) GemmKernel's smaller tiles were 1-2 us faster.
 bool UsePrefill(const WeightView &w, int64_t M) {
   if (M < 65 || !PrefillSupportsM(w, M)) return false;
   const int64_t tiles = (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN);
   const int64_t cus = w.num_cus;
-  if (tiles < cus) return false;
+  if (tiles < cus) {
+    const int64_t splits = std::min<int64_t>(cus / tiles, kPrefillMaxSplits);
+    return w.K / kBK >= 12 * splits;
+  }
   const int64_t waves = (tiles + cus - 1) / cus;
   return tiles * 100 >= waves * cus * 85;
 }
