@@ -173,11 +173,14 @@ int mnb_run_ex(const mnb_plan *plan, int64_t M, const float *dA, const float *dB
  * the schema the roadmap targets: docs/next_steps/2026/2026_08_qwen3_inference.rst:143, 282),
  * fused as the roadmap's "RMSNorm into packed projection input" (:371-373).
  * dX fp32 [M, K] and dGamma fp32 [K] are device pointers, 16-byte aligned,
- * K % 4 == 0 (else MNB_ERR_UNSUPPORTED); epsilon >= 0. M = 1 on the decode
- * path: one kernel (the GEMV reduces the row's mean square while staging it);
- * the GEMM path: a per-row 1/rms pass, then gamma and 1/rms folded into the
- * GEMM's conversion of A to fp16; every other path: the normalized input is
- * written to the workspace first. Works on gate/up plans too (H of the
+ * K % 4 == 0 (else MNB_ERR_UNSUPPORTED); epsilon >= 0. Decode path: the
+ * M = 1 GEMV and the M <= 4 fragment-ordered GEMV in one kernel (each
+ * reduces its rows' mean squares while staging them); the small-M MFMA
+ * decode in its own two launches (the activation split multiplies by gamma
+ * and sums x^2 per 256-k unit, the main kernel scales each row's sums by
+ * 1/rms); the GEMM path: a per-row 1/rms pass, then gamma and 1/rms folded
+ * into the GEMM's conversion of A to fp16; every other kernel (the fp32-FMA
+ * decode fallbacks): the normalized input is written to the workspace first. Works on gate/up plans too (H of the
  * normalized input). The workspace is required:
  * mnb_rmsnorm_workspace_bytes. */
 int mnb_rmsnorm_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);

@@ -588,6 +588,11 @@ static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void
   return mnb::GemvSmallMSupports(plan->view, M) ? kDecSmallM : kDecGemv;
 }
 
+// Decode kernels that multiply a fused RMSNorm input themselves.
+static bool DecodeTakesRms(const mnb_plan *plan, DecodeKernel k) {
+  return k == kDecGemvFrag || k == kDecM1 || (k == kDecFrag && mnb::DecodeFragTakesRms(plan->view));
+}
+
 // Workspace bytes the decode kernel PickDecodeKernel chooses for M rows when
 // the caller passes enough: 0 for the kernels that need none.
 static size_t DecodeNeed(const mnb_plan *plan, int64_t M, bool rms = false) {
@@ -734,8 +739,11 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   // the others, SiluMulKernel turns the scratch sum into H.
   bool fused = false, bias_done = false;
   switch (path) {
-  case 1:
-    switch (PickDecodeKernel(plan, M, work, work_bytes, gamma != nullptr)) {
+  case 1: {
+    const DecodeKernel dk = PickDecodeKernel(plan, M, work, work_bytes, gamma != nullptr);
+    // only these kernels take an RMSNorm input (mnb_run_rmsnorm checks first)
+    if (gamma != nullptr && !DecodeTakesRms(plan, dk)) return MNB_ERR_UNSUPPORTED;
+    switch (dk) {
     case kDecGemvFrag:
       e = mnb::LaunchGemvFrag(plan->view, M, dA, Ys, s, 0, 0, H, dBias, gamma, eps);
       fused = true;
@@ -752,7 +760,7 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
       }
       break;
     case kDecFrag:
-      e = mnb::LaunchDecodeFrag(plan->view, M, dA, Ys, work, s, H, 0, 0, dBias);
+      e = mnb::LaunchDecodeFrag(plan->view, M, dA, Ys, work, s, H, 0, 0, dBias, gamma, eps);
       fused = true;
       bias_done = dBias != nullptr;
       break;
@@ -764,6 +772,7 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
     default: e = mnb::LaunchGemv(plan->view, M, dA, Ys, s); break;
     }
     break;
+  }
   case 2:
     // The GEMM's fused stores address H with 32-bit byte offsets: H's bytes
     // and those of a whole tile of rows (up to 128) must stay below 2^31.
@@ -832,7 +841,11 @@ int mnb_run_rmsnorm(const mnb_plan *plan, int64_t M, const float *dX, const floa
   if (hipGetDevice(&cur) != hipSuccess || cur != plan->device) return MNB_ERR_NO_DEVICE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int path = SelectPath(plan, M, dX);
-  if ((path == 1 && M == 1 && mnb::GemvM1Supports(plan->view)) || path == 2)
+  // Fused where the kernel multiplies the normalized input itself: the GEMM,
+  // and the decode kernels that take gamma (the M = 1 GEMV, the M <= 4
+  // fragment GEMV, the small-M MFMA decode with its workspace).
+  if (path == 2 ||
+      (path == 1 && DecodeTakesRms(plan, PickDecodeKernel(plan, M, rest, rest_bytes, true))))
     return RunImpl(plan, M, dX, nullptr, dY, rest, rest_bytes, stream, path, dGamma, epsilon);
   const hipError_t e = mnb::LaunchRmsNorm(dX, dGamma, Xn, M, plan->view.K, epsilon, s);
   if (e != hipSuccess) {

@@ -74,6 +74,7 @@ constexpr int kTok = 16;               // tokens per MFMA tile (M padded)
 constexpr int kMaxWaves = 8;
 constexpr int kTerms = 2;              // fp16 terms per activation
 constexpr int kStepBytes = kTerms * 1024;  // image bytes per 32-k step
+constexpr int kMaxSqUnits = 64;            // RMSNorm input: K <= 64 units (16384)
 
 __device__ __forceinline__ uint32_t PkAddF16(uint32_t a, uint32_t b) {
   const half2v r = __builtin_bit_cast(half2v, a) + __builtin_bit_cast(half2v, b);
@@ -111,9 +112,16 @@ __device__ __forceinline__ half8 DecodeQ(uint32_t w, uint32_t neg_lo, uint32_t n
 // img[((u * 8 + ch / 4) * kTerms + term) * 64 + 16 (ch % 4) + t] and
 // exps[u * 16 + t]. (One 128-thread workgroup per unit, each thread taking 32
 // values, kept 16 workgroups busy for about 4 us at M = 16.)
+// RMS (RMSNorm fused into the input): the values split are a * gamma, and
+// sq[u * 16 + t] receives the token's sum of a^2 over the unit (a fixed
+// butterfly), from which the main kernel forms 1 / rms.
+template <bool RMS>
 __global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A,
                                                      uint4 *__restrict__ img,
-                                                     int *__restrict__ exps, int M, int K) {
+                                                     int *__restrict__ exps,
+                                                     float *__restrict__ sq,
+                                                     const float *__restrict__ gamma, int M,
+                                                     int K) {
   const int u = static_cast<int>(blockIdx.x) >> 3;
   const int t = (static_cast<int>(blockIdx.x) & 7) * 2 + static_cast<int>(threadIdx.x >> 5);
   const int ch = threadIdx.x & 31;
@@ -121,8 +129,20 @@ __global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, M * K * 4, 0x00020000);
   // tokens past M read past the end of the buffer: zeros
   const int vo = t < M ? (t * K + kUnitK * u + 8 * ch) * 4 : M * K * 4;
-  const floatx4 v0 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo, 0, 0));
-  const floatx4 v1 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo + 16, 0, 0));
+  floatx4 v0 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo, 0, 0));
+  floatx4 v1 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo + 16, 0, 0));
+  if constexpr (RMS) {
+    const float4 *gp = reinterpret_cast<const float4 *>(gamma + kUnitK * u + 8 * ch);
+    const float4 g0 = gp[0], g1 = gp[1];
+    float q = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q += v0[c] * v0[c] + v1[c] * v1[c];
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) q += __shfl_xor(q, o);
+    if (ch == 0) sq[u * kTok + t] = q;
+    v0 *= floatx4{g0.x, g0.y, g0.z, g0.w};
+    v1 *= floatx4{g1.x, g1.y, g1.z, g1.w};
+  }
   float amax = 0.f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) amax = fmaxf(amax, fmaxf(fabsf(v0[c]), fabsf(v1[c])));
@@ -150,13 +170,19 @@ __global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A
 
 // Group g of 64 weight rows, run `seg` of WPG * U units. SPB = 32-k steps
 // per quantization block within a unit (bs / 32, at most 8).
-template <bool HAS_ZP, int SPB, int U, int WIN>
+// RMS: the image holds A * gamma; every run scales its sums by each token's
+// 1 / rms = 1 / sqrt(sum_k A^2 / K + eps), from SplitActKernel's per-unit
+// sums of squares added in unit order.
+template <bool HAS_ZP, int SPB, int U, int WIN, bool RMS>
 __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
     const uint8_t *__restrict__ Bp, const float *__restrict__ Sd, const uint32_t *__restrict__ Zd,
     const uint4 *__restrict__ img, const int *__restrict__ exps, float *__restrict__ Y,
     float *__restrict__ partials, float *__restrict__ H, const float *__restrict__ bias, int M,
-    int N, int K, int nb, int log2_bs, int segs, int wpg) {
+    int N, int K, int nb, int log2_bs, int segs, int wpg, const float *__restrict__ sq,
+    float eps) {
   __shared__ float red[kMaxWaves * 16 * 64];  // 32 KiB: [wave][slice * 4 + v][lane]
+  __shared__ float rinv[kTok];                // RMS: each token's 1 / rms
+  __shared__ float sqs[RMS ? kMaxSqUnits * kTok : 1];  // RMS: the per-unit sums of squares
   constexpr int kSteps = U * kUnitSteps;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -177,6 +203,20 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
   const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t *>(HAS_ZP ? Zd + static_cast<size_t>(g) * nb * 16 : Zd), 0,
       HAS_ZP ? nb * 64 : 0, 0x00020000);
+
+  // RMS: wavefront 0 copies the per-unit sums of squares ([unit][token],
+  // 64 bytes per unit, L2-resident) straight into LDS first, with no
+  // registers held, and adds them up after the stream. Lanes past the end
+  // copy the last 16 bytes again (in bounds; those LDS bytes are not read).
+  if constexpr (RMS) {
+    if (wave == 0) {
+      const int bytes = (T / kUnitSteps) * kTok * 4;
+      const uint32_t base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sqs));
+      for (int i = 0; i * 1024 < bytes; ++i)
+        CopyToLds16(reinterpret_cast<const char *>(sq) + min(i * 1024 + 16 * lane, bytes - 16),
+                    base + static_cast<uint32_t>(i * 1024));
+    }
+  }
 
   // Each unit's token exponents: lane quarter qd holds tokens 4 qd .. 4 qd + 3.
   int4 ue[U];
@@ -286,6 +326,19 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int v = 0; v < 4; ++v) red[(wave * 16 + j * 4 + v) * 64 + lane] = acc[j][v];
+  if constexpr (RMS) {
+    if (wave == 0) {
+      // the copies have landed (vmcnt counts them), then lane t adds token
+      // t's units in order
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+      __asm__ volatile("" ::: "memory");
+      if (lane < kTok) {
+        float tot = 0.f;
+        for (int u = 0; u < T / kUnitSteps; ++u) tot += sqs[u * kTok + lane];
+        rinv[lane] = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+      }
+    }
+  }
   __syncthreads();
   float *out = seg == 0 ? Y : partials + static_cast<size_t>(seg - 1) * M * N;
   const int y_end = M * N * 4;
@@ -296,6 +349,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
     const int j = x >> 2, v = x & 3;
     const int n = 64 * g + 16 * j + c;
     const int tok = 4 * qd + v;
+    if constexpr (RMS) sum *= rinv[tok];
     if (H != nullptr) {
       // gate/up pairs (rows 2 n', 2 n' + 1 in lanes c, c ^ 1; N even)
       const float other = PairSwap(sum);
@@ -374,34 +428,53 @@ inline size_t ImageBytes(const WeightView &w) { return static_cast<size_t>(w.K /
 inline size_t ExpBytes(const WeightView &w) {
   return (static_cast<size_t>(w.K / kUnitK) * kTok * 4 + 255) / 256 * 256;
 }
+// The per-unit sums of squares of a fused RMSNorm input: the same size.
+inline size_t SqBytes(const WeightView &w) { return ExpBytes(w); }
+
+// The workspace's image, exponents, per-unit sums of squares (RMS) and
+// partial sums; sq is null without RMSNorm.
+struct Work {
+  const uint4 *img;
+  const int *exps;
+  const float *sq;
+  float *P;
+  float eps;
+};
 
 template <bool HAS_ZP, int SPB, int U>
-hipError_t LaunchMain(const WeightView &w, int64_t M, const uint4 *img, const int *exps, float *Y,
-                      float *P, float *H, const float *bias, const Shape &sh, hipStream_t s) {
+hipError_t LaunchMain(const WeightView &w, int64_t M, const Work &wk, float *Y, float *H,
+                      const float *bias, const Shape &sh, hipStream_t s) {
   const int64_t groups = (w.N + 63) / 64;
   constexpr int kWin = 4;
-  hipLaunchKernelGGL((DecodeFragKernel<HAS_ZP, SPB, U, kWin>),
-                     dim3(static_cast<unsigned>(groups * sh.segs)), dim3(64 * sh.wpg), 0, s, w.Bp,
-                     w.Sd, w.Zd, img, exps, Y, P, H, bias, static_cast<int>(M), static_cast<int>(w.N),
-                     static_cast<int>(w.K), static_cast<int>(w.nb), w.log2_bs, sh.segs, sh.wpg);
+  const dim3 grid(static_cast<unsigned>(groups * sh.segs)), block(64 * sh.wpg);
+  const int m = static_cast<int>(M), n = static_cast<int>(w.N), k = static_cast<int>(w.K),
+            nb = static_cast<int>(w.nb);
+  if (wk.sq != nullptr)
+    hipLaunchKernelGGL((DecodeFragKernel<HAS_ZP, SPB, U, kWin, true>), grid, block, 0, s, w.Bp,
+                       w.Sd, w.Zd, wk.img, wk.exps, Y, wk.P, H, bias, m, n, k, nb, w.log2_bs,
+                       sh.segs, sh.wpg, wk.sq, wk.eps);
+  else
+    hipLaunchKernelGGL((DecodeFragKernel<HAS_ZP, SPB, U, kWin, false>), grid, block, 0, s, w.Bp,
+                       w.Sd, w.Zd, wk.img, wk.exps, Y, wk.P, H, bias, m, n, k, nb, w.log2_bs,
+                       sh.segs, sh.wpg, nullptr, 0.0f);
   return hipGetLastError();
 }
 
 template <bool HAS_ZP, int SPB>
-hipError_t LaunchU(const WeightView &w, int64_t M, const uint4 *img, const int *exps, float *Y,
-                   float *P, float *H, const float *bias, const Shape &sh, hipStream_t s) {
-  return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2>(w, M, img, exps, Y, P, H, bias, sh, s)
-                                : LaunchMain<HAS_ZP, SPB, 1>(w, M, img, exps, Y, P, H, bias, sh, s);
+hipError_t LaunchU(const WeightView &w, int64_t M, const Work &wk, float *Y, float *H,
+                   const float *bias, const Shape &sh, hipStream_t s) {
+  return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2>(w, M, wk, Y, H, bias, sh, s)
+                                : LaunchMain<HAS_ZP, SPB, 1>(w, M, wk, Y, H, bias, sh, s);
 }
 
 template <bool HAS_ZP>
-hipError_t LaunchZp(const WeightView &w, int64_t M, const uint4 *img, const int *exps, float *Y,
-                    float *P, float *H, const float *bias, const Shape &sh, hipStream_t s) {
+hipError_t LaunchZp(const WeightView &w, int64_t M, const Work &wk, float *Y, float *H,
+                    const float *bias, const Shape &sh, hipStream_t s) {
   switch (std::min(w.block_size / 32, kUnitSteps)) {
-  case 1: return LaunchU<HAS_ZP, 1>(w, M, img, exps, Y, P, H, bias, sh, s);
-  case 2: return LaunchU<HAS_ZP, 2>(w, M, img, exps, Y, P, H, bias, sh, s);
-  case 4: return LaunchU<HAS_ZP, 4>(w, M, img, exps, Y, P, H, bias, sh, s);
-  default: return LaunchU<HAS_ZP, 8>(w, M, img, exps, Y, P, H, bias, sh, s);
+  case 1: return LaunchU<HAS_ZP, 1>(w, M, wk, Y, H, bias, sh, s);
+  case 2: return LaunchU<HAS_ZP, 2>(w, M, wk, Y, H, bias, sh, s);
+  case 4: return LaunchU<HAS_ZP, 4>(w, M, wk, Y, H, bias, sh, s);
+  default: return LaunchU<HAS_ZP, 8>(w, M, wk, Y, H, bias, sh, s);
   }
 }
 
@@ -433,32 +506,44 @@ bool DecodeFragSupports(const WeightView &w, int64_t M) {
          (w.K / 32) * df::kStepBytes < (int64_t{1} << 31);
 }
 
+bool DecodeFragTakesRms(const WeightView &w) { return w.K <= df::kMaxSqUnits * df::kUnitK; }
+
 size_t DecodeFragWorkspaceBytes(const WeightView &w, int64_t M, int wpg, int units_per_wave) {
   const df::Shape sh = df::PickShape(w, wpg, units_per_wave);
-  return df::ImageBytes(w) + df::ExpBytes(w) +
+  return df::ImageBytes(w) + df::ExpBytes(w) + df::SqBytes(w) +
          static_cast<size_t>(std::max(sh.segs, 1) - 1) * static_cast<size_t>(M) * w.N * 4;
 }
 
 hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                             hipStream_t s, float *H, int wpg, int units_per_wave,
-                            const float *bias) {
+                            const float *bias, const float *gamma, float eps) {
   const df::Shape sh = df::PickShape(w, wpg, units_per_wave);
   const int units = static_cast<int>(w.K / df::kUnitK);
   if (sh.wpg < 1 || sh.wpg > df::kMaxWaves || sh.segs < 1 ||
       sh.segs * sh.wpg * sh.units_per_wave != units || (sh.units_per_wave != 1 && sh.units_per_wave != 2))
     return hipErrorInvalidValue;
-  uint4 *img = static_cast<uint4 *>(work);
-  int *exps = reinterpret_cast<int *>(static_cast<char *>(work) + df::ImageBytes(w));
-  float *P = reinterpret_cast<float *>(static_cast<char *>(work) + df::ImageBytes(w) + df::ExpBytes(w));
-  hipLaunchKernelGGL(df::SplitActKernel, dim3(static_cast<unsigned>(units * 8)), dim3(64), 0, s, A, img,
-                     exps, static_cast<int>(M), static_cast<int>(w.K));
+  if (gamma != nullptr && !DecodeFragTakesRms(w)) return hipErrorInvalidValue;
+  if (gamma != nullptr && (reinterpret_cast<uintptr_t>(gamma) % 16) != 0) return hipErrorInvalidValue;
+  char *base = static_cast<char *>(work);
+  uint4 *img = reinterpret_cast<uint4 *>(base);
+  int *exps = reinterpret_cast<int *>(base + df::ImageBytes(w));
+  float *sq = reinterpret_cast<float *>(base + df::ImageBytes(w) + df::ExpBytes(w));
+  float *P = reinterpret_cast<float *>(base + df::ImageBytes(w) + df::ExpBytes(w) + df::SqBytes(w));
+  const dim3 sgrid(static_cast<unsigned>(units * 8)), sblock(64);
+  if (gamma != nullptr)
+    hipLaunchKernelGGL(df::SplitActKernel<true>, sgrid, sblock, 0, s, A, img, exps, sq, gamma,
+                       static_cast<int>(M), static_cast<int>(w.K));
+  else
+    hipLaunchKernelGGL(df::SplitActKernel<false>, sgrid, sblock, 0, s, A, img, exps, nullptr,
+                       nullptr, static_cast<int>(M), static_cast<int>(w.K));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // One run per group: the kernel writes Y (or H) itself and adds the bias.
   float *Hk = sh.segs == 1 ? H : nullptr;
   const float *bk = sh.segs == 1 ? bias : nullptr;
-  e = w.zp != nullptr ? df::LaunchZp<true>(w, M, img, exps, Y, P, Hk, bk, sh, s)
-                      : df::LaunchZp<false>(w, M, img, exps, Y, P, Hk, bk, sh, s);
+  const df::Work wk{img, exps, gamma != nullptr ? sq : nullptr, P, eps};
+  e = w.zp != nullptr ? df::LaunchZp<true>(w, M, wk, Y, Hk, bk, sh, s)
+                      : df::LaunchZp<false>(w, M, wk, Y, Hk, bk, sh, s);
   if (e != hipSuccess || sh.segs == 1) return e;
   return LaunchSumPartials(Y, P, M * w.N, sh.segs - 1, H, s, bias, w.N);
 }

@@ -97,24 +97,24 @@ __host__ __device__ inline LdsLayout Layout(int K, int nb, int waves, int mt) {
   l.sums = (K / 32) * StepBytes(mt);
   l.exps = l.sums + (mt > 1 ? nb * mt * 4 : 0);
   l.red = l.exps + (mt > 1 ? (K / kUnitK) * mt * 4 : 0);
-  l.sq = l.red + waves * mt * 256;  // per wavefront: its units' sum of squares (RMSNorm)
-  l.bytes = l.sq + kMaxWaves * 4;
+  l.sq = l.red + waves * mt * 256;  // per wavefront and row: its units' sum of squares (RMSNorm)
+  l.bytes = l.sq + kMaxWaves * 4 * 4;
   return l;
 }
 
 // SPB = 32-k steps per quantization block (bs / 32, 1..8); SPW = steps per
 // wavefront (whole units); WIN = weight records in flight per wavefront; MT =
-// activation rows the launch is built for (1, 2 or 4; M <= MT). RMS (MT = 1):
-// the input is RMSNorm(A) = A / sqrt(mean(A^2) + eps) * gamma; the staging
-// multiplies by gamma and sums A^2 over the wavefront's units, and the row's
-// 1 / rms scales the final sums (it is common to every product).
+// activation rows the launch is built for (1, 2 or 4; M <= MT). RMS: the
+// input is RMSNorm(A) = A / sqrt(mean(A^2) + eps) * gamma, row by row; the
+// staging multiplies by gamma and sums A^2 per row over the wavefront's
+// units, and each row's 1 / rms scales its final sums (it is common to
+// every product of the row).
 template <bool HAS_ZP, int SPB, int SPW, int WIN, int MT, bool RMS>
 __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     const float *__restrict__ A, const uint8_t *__restrict__ Bp, const float *__restrict__ Sd,
     const uint32_t *__restrict__ Zd, float *__restrict__ Y, float *__restrict__ H,
     const float *__restrict__ bias, const float *__restrict__ gamma, float eps, int M, int N,
     int K, int nb) {
-  static_assert(!RMS || MT == 1, "RMSNorm input at M = 1 only");
   constexpr int kUnits = SPW / kUnitSteps;      // units of this wavefront
   constexpr int kItems = kUnits * MT;           // (unit, row) staging items, 32 lanes each
   constexpr int kPasses = (kItems + 1) / 2;     // two items per pass
@@ -199,7 +199,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
   //    scalars (M = 1) or to the LDS tables.
   float sb[MT == 1 ? kBlocks : 1];
   int eu[MT == 1 ? kUnits : 1];
-  float sq = 0.f;  // RMS: sum of A^2 over this lane's valid values
+  float sq[MT];  // RMS: per row, the sum of A^2 over this lane's valid values
+#pragma unroll
+  for (int r = 0; r < MT; ++r) sq[r] = 0.f;
 #pragma unroll
   for (int p = 0; p < kPasses; ++p) {
     if constexpr (RMS) {
@@ -210,7 +212,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
         va[p][0][i] *= vg[p][0][i];
         va[p][1][i] *= vg[p][1][i];
       }
-      sq += 2 * p + (lane >> 5) < kItems ? q2 : 0.f;
+      const int itv = 2 * p + (lane >> 5);
+#pragma unroll
+      for (int r = 0; r < MT; ++r) sq[r] += itv < kItems && itv % MT == r ? q2 : 0.f;
     }
     float amax = 0.f;
 #pragma unroll
@@ -264,11 +268,16 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     }
   }
   if constexpr (RMS) {
-    // the wavefront's sum of squares (fixed butterfly), to LDS for the end
+    // the wavefront's sums of squares per row (fixed butterfly), to LDS
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o, 64);
-    if (lane == 0) sq_lds[wave] = sq;
+    for (int r = 0; r < MT; ++r) {
+      float t = sq[r];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o, 64);
+      if (lane == 0) sq_lds[wave * MT + r] = t;
+    }
   }
+
   // The image writes above precede the operand reads below.
   __asm__ volatile("" ::: "memory");
 
@@ -356,18 +365,17 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     for (int j = 0; j < 4; ++j) red[(wave * MT + (lane >> 4)) * 64 + 16 * j + c] = acc[j];
   }
   __syncthreads();
-  float inv_rms = 1.0f;
-  if constexpr (RMS) {
-    float tot = 0.0f;
-    for (int w = 0; w < waves; ++w) tot += sq_lds[w];
-    inv_rms = 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
-  }
   // whole wavefronts per iteration (M * 64 and the block are multiples of 64)
   for (int idx = static_cast<int>(threadIdx.x); idx < M * 64; idx += static_cast<int>(blockDim.x)) {
     const int m = idx >> 6, r = idx & 63;
     float y = red[m * 64 + r];
     for (int w = 1; w < waves; ++w) y += red[(w * MT + m) * 64 + r];
-    if constexpr (RMS) y *= inv_rms;
+    if constexpr (RMS) {
+      // row m's 1 / rms: its sum of squares over the wavefronts, in order
+      float tot = 0.0f;
+      for (int w = 0; w < waves; ++w) tot += sq_lds[w * MT + m];
+      y *= 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
+    }
     const int n = 64 * g + r;
     if constexpr (!RMS) {
       // A non-finite activation: the reference's +-inf / NaN (see
@@ -417,14 +425,21 @@ hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipSt
   hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, WINV, MTV, RMSV>), grid, block, lds, s, \
                      A, w.Bp, w.Sd, w.Zd, Y, H, bias, gamma, eps, M, N, K, nb)
   if (gamma != nullptr) {
-    // RMSNorm input (M = 1, window 8, no 32-step launch with 32-k blocks:
-    // checked by the caller)
-    switch (spw) {
-    case 8: MNB_GF_LAUNCH(8, 8, 1, true); break;
-    case 16: MNB_GF_LAUNCH(16, 8, 1, true); break;
-    default:
-      if constexpr (SPB > 1) MNB_GF_LAUNCH(32, 8, 1, true);
-      break;
+    // RMSNorm input (window 8; no 32-step launch with 32-k blocks; 8 steps
+    // for M > 1, not with 32-k blocks at 4 rows: checked by the caller, see
+    // RmsSpw)
+    if (mt == 1) {
+      switch (spw) {
+      case 8: MNB_GF_LAUNCH(8, 8, 1, true); break;
+      case 16: MNB_GF_LAUNCH(16, 8, 1, true); break;
+      default:
+        if constexpr (SPB > 1) MNB_GF_LAUNCH(32, 8, 1, true);
+        break;
+      }
+    } else if (mt == 2) {
+      MNB_GF_LAUNCH(8, 8, 2, true);
+    } else {
+      if constexpr (SPB > 1) MNB_GF_LAUNCH(8, 8, 4, true);
     }
   } else if (mt > 1) {
     // more rows: window 8, 8 or 16 steps per wavefront (checked by the caller)
@@ -486,6 +501,19 @@ inline int PickSpw(const WeightView &w, int64_t M) {
   return 0;
 }
 
+// Steps per wavefront with an RMSNorm input (0: none): M = 1 as PickSpw
+// except 32 steps with 32-k blocks; M > 1 only 8 steps, and not 4 rows with
+// 32-k blocks (the other launches of the per-row sums of squares spill
+// registers under the 1024-thread bound).
+inline int RmsSpw(const WeightView &w, int64_t M) {
+  if (M == 1) {
+    const int spw = PickSpw(w, 1);
+    return spw == 32 && w.block_size == 32 ? 0 : spw;
+  }
+  if (RowsBuilt(M) == 4 && w.block_size == 32) return 0;
+  return ShapeFits(w, M, 8, 8) ? 8 : 0;
+}
+
 } // namespace gf
 
 bool GemvFragSupports(const WeightView &w, int64_t M) {
@@ -508,9 +536,9 @@ bool GemvFragShapeOk(const WeightView &w, int64_t M, int spw, int win) {
 
 bool GemvFragPreferred(const WeightView &w, int64_t M, bool rms) {
   // One workgroup per 64-row group: worth it where the groups cover most of
-  // the CUs. The RMSNorm input: M = 1, and not 32 steps per wavefront with
-  // 32-k blocks (the launch that would spill registers).
-  if (rms && (M != 1 || (gf::PickSpw(w, 1) == 32 && w.block_size == 32))) return false;
+  // the CUs. The RMSNorm input: not 32 steps per wavefront with 32-k blocks
+  // (the launch that would spill registers).
+  if (rms && gf::RmsSpw(w, M) == 0) return false;
   return GemvFragSupports(w, M) &&
          ((w.N + 63) / 64) * 100 >= static_cast<int64_t>(w.num_cus) * 85;
 }
@@ -518,11 +546,13 @@ bool GemvFragPreferred(const WeightView &w, int64_t M, bool rms) {
 hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s,
                           int spw, int win, float *H, const float *bias, const float *gamma,
                           float eps) {
-  if (spw == 0) spw = gf::PickSpw(w, M);
+  if (spw == 0) spw = gamma != nullptr ? gf::RmsSpw(w, M) : gf::PickSpw(w, M);
   if (win == 0) win = 8;
   if (!GemvFragSupports(w, M) || !gf::ShapeFits(w, M, spw, win)) return hipErrorInvalidValue;
-  if (gamma != nullptr && (M != 1 || win != 8 || (spw == 32 && w.block_size == 32) ||
-                           (reinterpret_cast<uintptr_t>(gamma) % 16) != 0))
+  if (gamma != nullptr &&
+      (win != 8 || (spw == 32 && w.block_size == 32) ||
+       (M > 1 && (spw != 8 || (gf::RowsBuilt(M) == 4 && w.block_size == 32))) ||
+       (reinterpret_cast<uintptr_t>(gamma) % 16) != 0))
     return hipErrorInvalidValue;
   const int m = static_cast<int>(M);
   return w.zp != nullptr ? gf::LaunchZp<true>(w, m, A, Y, s, spw, win, H, bias, gamma, eps)

@@ -115,7 +115,7 @@ hipError_t LaunchGemvSmallMShape(const WeightView &w, int64_t M, const float *A,
 // group, `steps_per_wave` (8, 16 or 32; 8 or 16 when M > 1) 32-k steps per
 // wavefront with `window` (4 or 8; 8 when M > 1) weight records in flight; 0
 // picks either. Needs Bp / Sd (/ Zd) and 32 <= block_size <= 256. H, bias and
-// the RMSNorm input (gamma, M = 1, window 8) as below.
+// the RMSNorm input (gamma, window 8) as below.
 bool GemvFragSupports(const WeightView &w, int64_t M);
 bool GemvFragShapeOk(const WeightView &w, int64_t M, int steps_per_wave, int window);
 // Whether the auto path takes it: its groups cover most CUs (with `rms`, for
@@ -135,7 +135,8 @@ hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float 
 // y[m][2n + 1]) instead of the product y; Y is then scratch (M x N floats)
 // for the launches that need an intermediate sum, unused by the others.
 //
-// RMSNorm input (M = 1 GEMV, GEMM): with gamma (K floats, 16-byte aligned)
+// RMSNorm input (M = 1 GEMV, the M <= 4 fragment GEMV, the small-M MFMA
+// decode on the fragment-ordered copy, GEMM): with gamma (K floats, 16-byte aligned)
 // the launch multiplies RMSNorm(A) = A / sqrt(mean_k(A^2) + eps) * gamma
 // instead of A; both compute the rows' mean squares themselves.
 // bias (N floats, MatMulNBits input 5, not with H) is added to each row's sum
@@ -164,20 +165,26 @@ hipError_t LaunchGemvMfmaShape(const WeightView &w, int64_t M, const float *A, f
 // plan's fragment-ordered weights (Bp) and re-laid block scales / zero points
 // (Sd, Zd); K % 256 == 0, power-of-two block_size >= 32. `work` holds
 // DecodeFragWorkspaceBytes(w, M, 0, 0) bytes: the split activation image, the
-// per-unit exponents and the partial sums of runs 1.. (one pre-pass kernel,
-// the main kernel, and the ordered partial-sum pass when K is split over
-// several workgroups). wpg (wavefronts per workgroup, 1 to 8) and
-// units_per_wave (1 or 2; a unit is 256 k): 0 picks. bias (N floats, not
-// with H) is added by the main kernel's stores or the partial-sum pass.
+// per-unit exponents, the per-unit sums of squares of an RMSNorm input and
+// the partial sums of runs 1.. (one pre-pass kernel, the main kernel, and the
+// ordered partial-sum pass when K is split over several workgroups). wpg
+// (wavefronts per workgroup, 1 to 8) and units_per_wave (1 or 2; a unit is
+// 256 k): 0 picks. bias (N floats, not with H) is added by the main kernel's
+// stores or the partial-sum pass. gamma: the RMSNorm input as above (the
+// pre-pass multiplies by gamma and sums A^2 per unit; each run scales its
+// sums by 1 / rms).
 bool DecodeFragLayoutWanted(const WeightView &w);
 size_t DecodeFragScaleBytes(const WeightView &w, size_t *zd_bytes);
 hipError_t LaunchDecodeFragRelayout(const WeightView &w, float *Sd, uint32_t *Zd, hipStream_t s);
 bool DecodeFragSupports(const WeightView &w, int64_t M);
+// Whether the launch takes an RMSNorm input (gamma): K <= 16384.
+bool DecodeFragTakesRms(const WeightView &w);
 size_t DecodeFragWorkspaceBytes(const WeightView &w, int64_t M, int wpg = 0,
                                 int units_per_wave = 0);
 hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                             hipStream_t s, float *H = nullptr, int wpg = 0,
-                            int units_per_wave = 0, const float *bias = nullptr);
+                            int units_per_wave = 0, const float *bias = nullptr,
+                            const float *gamma = nullptr, float eps = 0.0f);
 // Y += P[0] + ... + P[parts - 1] over mn elements, in that order (then the
 // gate/up activation into H when H is not null).
 hipError_t LaunchSumPartials(float *Y, const float *P, int64_t mn, int parts, float *H,

@@ -1,10 +1,13 @@
 """GPU parity of RMSNorm fused into the projection input (mnb_run_rmsnorm).
 
 Y = MatMulNBits(RMSNormalization(X)) for plain and gate/up plans, on every
-route: the M = 1 GEMV that reduces the row itself, the GEMM with 1/rms and
-gamma folded into its fp16 conversion of A, and the other paths after a
-normalization pass. Checked against the fp64 oracle (rmsnorm_f64, then
-matmul_nbits_f64 / gate_up_silu_f64) at the decode bound (normwise max
+route: the M = 1 GEMV and the M <= 4 fragment-ordered GEMV that reduce the
+rows themselves, the small-M MFMA decode whose activation split multiplies
+by gamma and sums x^2 per unit (one run, and K split over several runs), the
+GEMM with 1/rms and gamma folded into its fp16 conversion of A, and the
+fp32-FMA decode fallbacks after a normalization pass. Checked against the
+fp64 oracle (rmsnorm_f64, then matmul_nbits_f64 / gate_up_silu_f64) at the
+decode bound (normwise max
 2e-5: the 1e-5 decode bound plus the fp32 rounding of the normalized input)
 and the GEMM bound (L2 2e-3), and against the unfused run of the same plan
 on X normalized by torch in fp32.
@@ -27,7 +30,8 @@ def _torch_rms(torch, X, g, eps):
 @pytest.mark.parametrize("K,N,bs,zp,Ms,eps", [
     (4096, 768, 128, True, (1, 3, 8, 40, 512), 1e-5),
     (1024, 200, 32, False, (1, 16, 33), 1e-6),
-    (4096, 14336, 128, True, (1, 3), 1e-5),   # wide: GemvFragKernel with the RMSNorm input at M = 1
+    (4096, 14336, 128, True, (1, 2, 3, 4, 5, 16), 1e-5),  # wide: GemvFragKernel (M <= 4), DecodeFrag
+    (14336, 512, 32, True, (8, 16), 1e-5),    # long K: DecodeFragKernel over several runs
     (2048, 14336, 32, False, (1,), 1e-5),     # wide, a block scale per step, 16 steps per wavefront
 ])
 def test_rmsnorm_plain_plan(pkg, orc, cuda, K, N, bs, zp, Ms, eps):
@@ -44,8 +48,10 @@ def test_rmsnorm_plain_plan(pkg, orc, cuda, K, N, bs, zp, Ms, eps):
         X = (rng.standard_normal((M, K)) * rng.uniform(0.1, 10, (M, 1))).astype(np.float32)
         dX = torch.from_numpy(X).to(cuda)
         Y = op.run_rmsnorm(dX, dg, eps).cpu().numpy()
-        if N >= 14336:
+        if N >= 14336 and M <= 4:
             assert op.kernel_name(M) == "GemvFragKernel"
+        elif K == 14336 or (N >= 14336 and M <= 16):
+            assert op.kernel_name(M) == "DecodeFragKernel"
         Yu = op(_torch_rms(torch, dX, dg, eps).contiguous()).cpu().numpy()
         An = orc.rmsnorm_f64(X, gamma, eps).astype(np.float32)
         y64 = orc.matmul_nbits_f64(An, B, S, Z, K, N, bs)
@@ -73,7 +79,7 @@ def test_rmsnorm_gate_up_plan(pkg, orc, cuda):
     rng = np.random.default_rng(9)
     gamma = rng.uniform(0.5, 1.5, K).astype(np.float32)
     dg = torch.from_numpy(gamma).to(cuda)
-    for M in (1, 5, 100):
+    for M in (1, 3, 5, 100):
         print(f"case rmsnorm gate-up K={K} I={I} M={M}", flush=True)
         X = (rng.standard_normal((M, K)) * 3.0).astype(np.float32)
         H = op.run_rmsnorm(torch.from_numpy(X).to(cuda), dg, eps).cpu().numpy()
