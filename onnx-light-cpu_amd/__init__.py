@@ -15,6 +15,7 @@ current, every compute call raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 
 import numpy as np
@@ -23,8 +24,11 @@ from . import workloads  # noqa: F401  (re-exported for bench and tests)
 
 HERE = pathlib.Path(__file__).resolve().parent
 ROOT = HERE.parent
-LIB_PATH = HERE / "libmnb.so"
-HOST_LIB_PATH = HERE / "libolc_amd.so"
+# The built libraries: in-tree, or the directory ONNX_LIGHT_CPU_AMD_LIB_DIR
+# names (the host-sanitizer build of `make -C onnx-light-cpu_amd sanitize`).
+LIB_DIR = pathlib.Path(os.environ.get("ONNX_LIGHT_CPU_AMD_LIB_DIR", str(HERE)))
+LIB_PATH = LIB_DIR / "libmnb.so"
+HOST_LIB_PATH = LIB_DIR / "libolc_amd.so"
 HEADER_PATH = ROOT / "include" / "mnb.h"
 
 KERNEL_PREFIX = "onnx_light_cpu_amd::MatMulNBits"

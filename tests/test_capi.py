@@ -156,3 +156,30 @@ def test_python_operator_validates_sizes(pkg):
     bad = pkg.MatMulNBits(256, 64, 3, 32)
     with pytest.raises(ValueError, match="unsupported"):
         bad.prepare(np.zeros(64 * 8 * 16, np.uint8), np.zeros(64 * 8, np.float32))
+
+
+@pytest.mark.parametrize("K,N,bs,zp", [(96, 5, 32, True), (256, 3, 64, False), (160, 7, 32, True)])
+def test_gate_up_interleave_reads_exactly_the_inputs(pkg, K, N, bs, zp):
+    """Without a GPU, mnb_plan_create_gate_up still interleaves the two weights
+    on the host before the device check: on exactly-sized inputs (odd block
+    counts, an odd number of rows) it reports MNB_ERR_NO_DEVICE. Under the
+    host-sanitizer build (`make -C onnx-light-cpu_amd sanitize-test`) any read
+    past an input or write past the interleaved copies aborts the run."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    L = pkg.library()
+    nb = (K + bs - 1) // bs
+    rng = np.random.default_rng(K + N)
+    mk = lambda n, dt: (rng.integers(0, 256, n).astype(dt) if dt == np.uint8
+                        else rng.random(n).astype(dt))
+    Bg, Bu = mk(N * nb * bs // 2, np.uint8), mk(N * nb * bs // 2, np.uint8)
+    Sg, Su = mk(N * nb, np.float32), mk(N * nb, np.float32)
+    Zg = mk(N * ((nb + 1) // 2), np.uint8) if zp else None
+    Zu = mk(N * ((nb + 1) // 2), np.uint8) if zp else None
+    d = pkg.MnbDesc(K, N, 4, bs, 0, 1 if zp else 0)
+    plan = ctypes.c_void_p()
+    P = lambda a: None if a is None else a.ctypes.data
+    assert L.mnb_plan_create_gate_up(ctypes.byref(d), P(Bg), P(Sg), P(Zg), P(Bu), P(Su), P(Zu),
+                                     ctypes.byref(plan)) == NODEV
+    assert not plan.value
