@@ -333,6 +333,12 @@ def plan_create_leg(torch, pkg, dev):
             op = fn()
             torch.cuda.synchronize()
             r[name] = (time.perf_counter() - t0) * 1e3
+            # device memory the plan owns: with host weights its own copies
+            # (compact plans keep only the re-laid ones), with borrowed
+            # device weights the derived copies alone
+            key = "host_plan" if name == "host_ms" else "device_plan"
+            r[key + "_device_bytes"] = op.device_bytes()
+            r[key + "_ratio"] = r[key + "_device_bytes"] / p.weight_bytes()
             op.release()
         out.append(r)
     p = W.Projection("gate_up", 4096, 14336, 128, True)
@@ -344,7 +350,9 @@ def plan_create_leg(torch, pkg, dev):
     torch.cuda.synchronize()
     out.append({"projection": "gate_up plan (two 14336-row weights interleaved)", "K": p.K,
                 "N": 2 * p.N, "weight_bytes": 2 * p.weight_bytes(),
-                "host_ms": (time.perf_counter() - t0) * 1e3})
+                "host_ms": (time.perf_counter() - t0) * 1e3,
+                "host_plan_device_bytes": op.device_bytes(),
+                "host_plan_ratio": op.device_bytes() / (2 * p.weight_bytes())})
     op.release()
     torch.cuda.empty_cache()
     return out
@@ -836,7 +844,8 @@ def main():
     if "plan" in legs:
         plans = plan_create_leg(torch, pkg, dev)
         for r in plans:
-            print(f"# plan create {r['projection']}: host {r['host_ms']:.1f} ms"
+            print(f"# plan create {r['projection']}: host {r['host_ms']:.1f} ms "
+                  f"({r['host_plan_ratio']:.2f}x the weights in device memory)"
                   + (f", device {r['device_ms']:.1f} ms" if "device_ms" in r else ""),
                   file=sys.stderr, flush=True)
     copy = None

@@ -107,6 +107,16 @@ int mnb_plan_create_gate_up(const mnb_desc *desc, const uint8_t *Bg, const float
 /* Releases the plan and the device memory it owns. NULL is accepted. */
 int mnb_plan_destroy(mnb_plan *plan);
 
+/* Device bytes the plan owns: its copy of the constants where it keeps one
+ * (not borrowed buffers), the per-row scale exponents and the re-laid copies.
+ * A plan created from host weights whose every path runs on the re-laid
+ * copies (wide weights: N / 64 row groups covering most CUs, K % 256 == 0,
+ * K <= 8192, 32 <= block_size <= 256) keeps no original layout ("compact":
+ * about 1.24x the constants' bytes at block_size 128 with zero points);
+ * others keep both (about 2.2x). No counterpart in the reference (whose
+ * constant B stays in host memory): for callers planning device memory. */
+int mnb_plan_device_bytes(const mnb_plan *plan, size_t *bytes);
+
 /* Device workspace (16-byte aligned) that mnb_run and mnb_run_path need for M
  * rows, whichever path serves them (0 when none): the larger of
  *  - the prefill GEMM's: A scaled per row by a power of two and rounded to

@@ -69,6 +69,7 @@ def library():
         L.mnb_rmsnorm_workspace_bytes.argtypes = [vp, i64, ctypes.POINTER(sz)]
         L.mnb_run_rmsnorm.argtypes = [vp, i64, vp, vp, ctypes.c_float, vp, vp, sz, vp]
         L.mnb_plan_destroy.argtypes = [vp]
+        L.mnb_plan_device_bytes.argtypes = [vp, ctypes.POINTER(sz)]
         L.mnb_workspace_bytes.argtypes = [vp, i64, ctypes.POINTER(sz)]
         L.mnb_run.argtypes = [vp, i64, vp, vp, vp, sz, vp]
         L.mnb_run_path.argtypes = [vp, i64, vp, vp, vp, sz, vp, ctypes.c_int]
@@ -95,7 +96,7 @@ def library():
                      "mnb_weight_bytes", "mnb_run_ex", "mnb_qdq_repack",
                      "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes",
                      "mnb_run_rmsnorm", "mnb_run_no_alloc", "mnb_kernel_workspace_bytes",
-                     "mnb_run_kernel", "mnb_stream_read"):
+                     "mnb_run_kernel", "mnb_stream_read", "mnb_plan_device_bytes"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib
@@ -303,6 +304,12 @@ class MatMulNBits:
                                         ctypes.c_void_p(s.cuda_stream), kernel, p0, p1),
                "run_kernel")
         return out
+
+    def device_bytes(self) -> int:
+        """Device memory the plan owns (mnb_plan_device_bytes)."""
+        n = ctypes.c_size_t()
+        _check(library().mnb_plan_device_bytes(self._plan, ctypes.byref(n)), "device_bytes")
+        return n.value
 
     def workspace_bytes(self, M: int) -> int:
         n = ctypes.c_size_t()

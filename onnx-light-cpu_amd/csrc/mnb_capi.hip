@@ -103,6 +103,7 @@ void FillView(mnb_plan *p) {
   p->view.B = p->dB;
   p->view.scales = p->dS;
   p->view.zp = p->desc.has_zero_points ? p->dZ : nullptr;
+  p->view.has_zp = p->desc.has_zero_points;
   p->view.col_exp = p->dColExp;
   p->view.Bp = p->dBp;
   p->view.Sp = p->dSp;
@@ -137,6 +138,21 @@ void FreePlanMemory(mnb_plan *p) {
   p->dColExp = nullptr;
   p->dBp = nullptr;
   p->dSp = nullptr;
+}
+
+// Whether a plan can serve every path from the re-laid copies alone: the
+// fragment-ordered GEMV for every M <= 4 (the decode path without a
+// workspace runs it on groups of up to 4 rows) and as the M = 1 choice (its
+// 64-row groups cover most CUs), the small-M MFMA decode up to 16 rows, and
+// the prefill kernel for the GEMM path. Plans whose M = 1 decode is faster on
+// the original layout (narrow weights: GemvM1Kernel) keep both copies.
+bool CompactEligible(const mnb::WeightView &w) {
+  if (w.Bp == nullptr || w.Sp == nullptr || w.Sd == nullptr || (w.has_zp && w.Zd == nullptr))
+    return false;
+  for (int64_t m = 1; m <= 4; ++m)
+    if (!mnb::GemvFragSupports(w, m)) return false;
+  return mnb::GemvFragPreferred(w, 1) && mnb::DecodeFragSupports(w, 16) &&
+         mnb::PrefillSupports(w, 1);
 }
 
 // Plan-time constants derived from the device copies of the weights (run
@@ -194,6 +210,18 @@ int DerivePlanConstants(mnb_plan *p) {
       }
       FillView(p);
     }
+  }
+  // Compact plan: where every automatic route reads only the re-laid copies,
+  // a plan that owns its weights drops the original layout (about 2.2x the
+  // weights' bytes become 1.24x at bs = 128 with zero points).
+  if (p->owns && CompactEligible(p->view)) {
+    (void)hipFree(p->dB);
+    (void)hipFree(p->dS);
+    if (p->dZ) (void)hipFree(p->dZ);
+    p->dB = nullptr;
+    p->dS = nullptr;
+    p->dZ = nullptr;
+    FillView(p);
   }
   return MNB_OK;
 }
@@ -515,6 +543,27 @@ int mnb_plan_destroy(mnb_plan *plan) {
   return MNB_OK;
 }
 
+int mnb_plan_device_bytes(const mnb_plan *plan, size_t *bytes) {
+  if (plan == nullptr || bytes == nullptr) return MNB_ERR_NULL_POINTER;
+  int64_t nb, row_bytes, zp_row_bytes;
+  Sizes(&plan->desc, &nb, &row_bytes, &zp_row_bytes);
+  const size_t N = static_cast<size_t>(plan->desc.N);
+  size_t total = N * sizeof(int32_t);  // the per-row scale exponents
+  if (plan->owns && plan->dB != nullptr)
+    total += N * static_cast<size_t>(row_bytes) + N * static_cast<size_t>(nb) * sizeof(float) +
+             (plan->dZ != nullptr ? N * static_cast<size_t>(zp_row_bytes) : 0);
+  if (plan->dBp != nullptr) {
+    size_t sp = 0;
+    total += mnb::PrefillLayoutBytes(plan->view, &sp) + sp;
+  }
+  if (plan->dSd != nullptr) {
+    size_t zd = 0;
+    total += mnb::DecodeFragScaleBytes(plan->view, &zd) + (plan->dZd != nullptr ? zd : 0);
+  }
+  *bytes = total;
+  return MNB_OK;
+}
+
 // Rows from which the decode path multiplies on the original-layout MFMA
 // kernel (GemvMfmaKernel), for plans without the fragment-ordered weight copy
 // (N % 4 != 0 or N >= 2^22; when the caller passes the workspace): below it
@@ -561,7 +610,9 @@ static bool UsesFragDecode(const mnb_plan *plan, int64_t M) {
 
 // The decode kernel path 1 launches for M rows with `work_bytes` of workspace
 // at `work` (M <= 16).
-enum DecodeKernel { kDecM1, kDecGemvFrag, kDecFrag, kDecMfma, kDecSmallM, kDecGemv };
+// kDecFragGroups: a compact plan without the small-M kernel's workspace runs
+// the fragment-ordered GEMV on consecutive groups of up to 4 rows.
+enum DecodeKernel { kDecM1, kDecGemvFrag, kDecFrag, kDecMfma, kDecSmallM, kDecGemv, kDecFragGroups };
 
 // Rows per launch of the exact route (path 4): the decode kernels' limit.
 constexpr int64_t kExactGroupRows = 16;
@@ -585,7 +636,16 @@ static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void
   if (!mnb::DecodeFragSupports(plan->view, M) && UsesMfmaDecode(plan, M) &&
       HasWorkspace(work, work_bytes, mnb::GemvMfmaWorkspaceBytes(plan->view, M)))
     return kDecMfma;
+  if (plan->view.B == nullptr) return kDecFragGroups;
   return mnb::GemvSmallMSupports(plan->view, M) ? kDecSmallM : kDecGemv;
+}
+
+// Whether the decode path (path 1) serves M <= 16 rows: the original-layout
+// kernels, or on a compact plan the fragment-ordered GEMV (groups of 4 rows).
+static bool DecodeSupported(const mnb_plan *plan, int64_t M) {
+  if (M < 1 || M > 16) return false;
+  return plan->view.B != nullptr ? mnb::GemvSupports(plan->view, M)
+                                 : mnb::GemvFragSupports(plan->view, std::min<int64_t>(M, 4));
 }
 
 // Decode kernels that multiply a fused RMSNorm input themselves.
@@ -641,12 +701,12 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
 static bool Fp32ActivationsOnly(const mnb_plan *plan) { return plan->desc.accuracy_level == 1; }
 
 static bool ExactGroupsSupported(const mnb_plan *plan, bool a_aligned) {
-  return a_aligned && mnb::GemvSupports(plan->view, kExactGroupRows);
+  return a_aligned && DecodeSupported(plan, kExactGroupRows);
 }
 
 static int SelectPath(const mnb_plan *plan, int64_t M, const float *dA) {
   const bool a_aligned = (reinterpret_cast<uintptr_t>(dA) % 16) == 0;
-  if (a_aligned && M <= 16 && mnb::GemvSupports(plan->view, M)) return 1;
+  if (a_aligned && DecodeSupported(plan, M)) return 1;
   if (Fp32ActivationsOnly(plan)) return ExactGroupsSupported(plan, a_aligned) ? 4 : 3;
   if (a_aligned && mnb::GemmSupports(plan->view, M)) return 2;
   return 3;
@@ -690,8 +750,7 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
   if (path < 0 || path > 5) return MNB_ERR_UNSUPPORTED;
   const bool a_aligned = (reinterpret_cast<uintptr_t>(dA) % 16) == 0;
   if (path == 0) path = SelectPath(plan, M, dA);
-  if (path == 1 && !(a_aligned && M <= 16 && mnb::GemvSupports(plan->view, M)))
-    return MNB_ERR_UNSUPPORTED;
+  if (path == 1 && !(a_aligned && DecodeSupported(plan, M))) return MNB_ERR_UNSUPPORTED;
   if (path == 2 && !(a_aligned && mnb::GemmSupports(plan->view, M))) return MNB_ERR_UNSUPPORTED;
   if (path == 4 && !ExactGroupsSupported(plan, a_aligned)) return MNB_ERR_UNSUPPORTED;
   if (path == 5 && !(a_aligned && mnb::PrefillSupports(plan->view, M))) return MNB_ERR_UNSUPPORTED;
@@ -769,6 +828,18 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
       fused = true;
       break;
     case kDecSmallM: e = mnb::LaunchGemvSmallM(plan->view, M, dA, Ys, s); break;
+    case kDecFragGroups: {
+      // consecutive groups of up to 4 rows, in stream order
+      const int64_t K = plan->view.K, N = plan->view.N;
+      for (int64_t m0 = 0; m0 < M && e == hipSuccess; m0 += 4) {
+        const int64_t mg = std::min<int64_t>(4, M - m0);
+        e = mnb::LaunchGemvFrag(plan->view, mg, dA + m0 * K, Ys + m0 * N, s, 0, 0,
+                                H != nullptr ? H + m0 * (N / 2) : nullptr, dBias);
+      }
+      fused = true;
+      bias_done = dBias != nullptr;
+      break;
+    }
     default: e = mnb::LaunchGemv(plan->view, M, dA, Ys, s); break;
     }
     break;
@@ -883,6 +954,7 @@ const char *mnb_kernel_name(const mnb_plan *plan, int64_t M, size_t workspace_by
     case kDecFrag: return "DecodeFragKernel";
     case kDecMfma: return "GemvMfmaKernel";
     case kDecSmallM: return "GemvSmallMKernel";
+    case kDecFragGroups: return "GemvFragKernel";
     default: return "GemvKernel";
     }
   case 2:
@@ -903,7 +975,7 @@ static bool KernelServes(const mnb::WeightView &w, int64_t M, int kernel) {
   case MNB_KERNEL_GEMV_SMALL_M: return M >= 2 && mnb::GemvSmallMSupports(w, M);
   case MNB_KERNEL_GEMV_MFMA: return mnb::GemvMfmaSupports(w, M);
   case MNB_KERNEL_DECODE_FRAG: return mnb::DecodeFragSupports(w, M);
-  case MNB_KERNEL_GEMM: return mnb::GemmSupports(w, M);
+  case MNB_KERNEL_GEMM: return mnb::GemmKernelSupports(w, M);
   case MNB_KERNEL_PREFILL: return mnb::PrefillSupports(w, M);
   case MNB_KERNEL_STREAM: return mnb::StreamSupports(w, M);
   case MNB_KERNEL_GEMV: return M <= 16 && mnb::GemvSupports(w, M);

@@ -488,7 +488,7 @@ bool DecodeFragLayoutWanted(const WeightView &w) {
 
 size_t DecodeFragScaleBytes(const WeightView &w, size_t *zd_bytes) {
   const int64_t items = (w.N + 63) / 64 * w.nb * 16;
-  if (zd_bytes != nullptr) *zd_bytes = w.zp != nullptr ? static_cast<size_t>(items) * 4 : 0;
+  if (zd_bytes != nullptr) *zd_bytes = w.has_zp ? static_cast<size_t>(items) * 4 : 0;
   return static_cast<size_t>(items) * 16;
 }
 
@@ -501,7 +501,7 @@ hipError_t LaunchDecodeFragRelayout(const WeightView &w, float *Sd, uint32_t *Zd
 
 bool DecodeFragSupports(const WeightView &w, int64_t M) {
   return M >= 2 && M <= 16 && w.Bp != nullptr && w.Sd != nullptr &&
-         (w.zp == nullptr || w.Zd != nullptr) && DecodeFragLayoutWanted(w) &&
+         (!w.has_zp || w.Zd != nullptr) && DecodeFragLayoutWanted(w) &&
          M * w.K * 4 + 4096 < (int64_t{1} << 31) && M * w.N * 4 < (int64_t{1} << 31) &&
          (w.K / 32) * df::kStepBytes < (int64_t{1} << 31);
 }
@@ -542,7 +542,7 @@ hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, floa
   float *Hk = sh.segs == 1 ? H : nullptr;
   const float *bk = sh.segs == 1 ? bias : nullptr;
   const df::Work wk{img, exps, gamma != nullptr ? sq : nullptr, P, eps};
-  e = w.zp != nullptr ? df::LaunchZp<true>(w, M, wk, Y, Hk, bk, sh, s)
+  e = w.has_zp ? df::LaunchZp<true>(w, M, wk, Y, Hk, bk, sh, s)
                       : df::LaunchZp<false>(w, M, wk, Y, Hk, bk, sh, s);
   if (e != hipSuccess || sh.segs == 1) return e;
   return LaunchSumPartials(Y, P, M * w.N, sh.segs - 1, H, s, bias, w.N);

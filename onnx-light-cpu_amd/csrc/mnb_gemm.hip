@@ -1486,7 +1486,7 @@ size_t StreamPartialBytes(const WeightView &w, int64_t M, int segs) {
 } // namespace
 
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M) {
-  size_t partial = PartialBytes(w, M, PickShape(w, M));
+  size_t partial = w.B != nullptr ? PartialBytes(w, M, PickShape(w, M)) : 0;
   if (PrefillSupportsM(w, M)) partial = std::max(partial, PrefillPartialBytes(w, M));
   if (StreamSupportsM(w, M))
     partial = std::max(partial, StreamPartialBytes(w, M, PickStreamShape(w, 0, 0).segs));
@@ -1529,7 +1529,7 @@ hipError_t LaunchStream(const WeightView &w, int64_t M, const float *A, float *Y
   float *Hk = sh.segs == 1 ? H : nullptr;
   const float *bk = sh.segs == 1 ? bias : nullptr;
   const float *Ak = cvt ? A : nullptr;
-  e = w.zp != nullptr ? LaunchStreamZp<true>(w, M, Ah, Ak, Y, P, Hk, row_exp, bk, sh, s)
+  e = w.has_zp ? LaunchStreamZp<true>(w, M, Ah, Ak, Y, P, Hk, row_exp, bk, sh, s)
                       : LaunchStreamZp<false>(w, M, Ah, Ak, Y, P, Hk, row_exp, bk, sh, s);
   if (e != hipSuccess || sh.segs == 1) return e;
   return DispatchReduce(sh.segs - 1, Y, P, M * w.N, s, H,
@@ -1583,7 +1583,7 @@ static hipError_t LaunchPrefillGemm(const WeightView &w, int64_t M, const float 
   // bias. Several: the ordered reduction does, after the partial sums.
   float *Hk = splits == 1 ? H : nullptr;
   const float *bk = splits == 1 ? bias : nullptr;
-  const bool zp = w.zp != nullptr, bs32 = w.block_size == 32;
+  const bool zp = w.has_zp != 0, bs32 = w.block_size == 32;
   if (zp)
     e = bs32 ? LaunchPrefillT<true, true>(w, M, Ah, Y, partials, splits, s, Hk, row_exp, bk)
              : LaunchPrefillT<true, false>(w, M, Ah, Y, partials, splits, s, Hk, row_exp, bk);
@@ -1600,10 +1600,15 @@ size_t GemmShapeWorkspaceBytes(const WeightView &w, int64_t M, int splits) {
 }
 
 bool GemmSupports(const WeightView &w, int64_t M) {
+  return GemmKernelSupports(w, M) || PrefillSupportsM(w, M);
+}
+
+bool GemmKernelSupports(const WeightView &w, int64_t M) {
   // Buffer offsets are 32-bit within one tile of 128 weight rows; up to 16
   // splits of the BM = 32 tiling must fit one grid.
   const int64_t tiles = ((M + 31) / 32) * ((w.N + kBN - 1) / kBN) * 16;
-  return M >= 1 && (w.K % kBK) == 0 && w.block_size >= 32 && tiles < (int64_t{1} << 31) &&
+  return w.B != nullptr && M >= 1 && (w.K % kBK) == 0 && w.block_size >= 32 &&
+         tiles < (int64_t{1} << 31) &&
          int64_t{kBN} * w.row_bytes < (int64_t{1} << 31) &&
          int64_t{kBN} * w.nb * 4 < (int64_t{1} << 31) && (w.row_bytes % 16) == 0 &&
          (reinterpret_cast<uintptr_t>(w.B) % 16) == 0 && M <= (int64_t{1} << 30) &&
@@ -1627,6 +1632,7 @@ hipError_t LaunchGemmShape(const WeightView &w, int64_t M, const float *A, float
     const int per = (ktiles + splits - 1) / splits;
     return LaunchPrefillGemm(w, M, A, Y, work, s, H, gamma, eps, nullptr, (ktiles + per - 1) / per);
   }
+  if (w.B == nullptr) return hipErrorInvalidValue;  // GemmKernel reads the original layout
   Shape sh = PickShape(w, M);
   if (bm > 0) sh = MakeShape(w, bm, splits > 0 ? splits : 1);
   switch (sh.bm) {
@@ -1645,14 +1651,15 @@ hipError_t LaunchGemm(const WeightView &w, int64_t M, const float *A, float *Y, 
     if (bias_done != nullptr) *bias_done = bias != nullptr;
     return LaunchStream(w, M, A, Y, work, s, H, gamma, eps, bias, 0, 0);
   }
-  if (UsePrefill(w, M)) {
+  // A compact plan (no original layout) always takes the prefill kernel.
+  if (UsePrefill(w, M) || w.B == nullptr) {
     if (bias_done != nullptr) *bias_done = bias != nullptr;
     return LaunchPrefillGemm(w, M, A, Y, work, s, H, gamma, eps, bias, PrefillSplits(w, M));
   }
   return LaunchGemmShape(w, M, A, Y, work, s, 0, 0, H, gamma, eps);
 }
 
-bool GemmUsesPrefill(const WeightView &w, int64_t M) { return UsePrefill(w, M); }
+bool GemmUsesPrefill(const WeightView &w, int64_t M) { return UsePrefill(w, M) || w.B == nullptr; }
 
 bool GemmUsesStream(const WeightView &w, int64_t M) { return StreamSupportsM(w, M); }
 

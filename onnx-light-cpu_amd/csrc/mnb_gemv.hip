@@ -182,6 +182,38 @@ __global__ __launch_bounds__(256) void GenericKernel(const float *__restrict__ A
   }
 }
 
+// GenericKernel over a compact plan's fragment-ordered copy: row n = 64 g +
+// 16 j + c is word j of lane (q, c) in the 1 KiB record of (g, 32-k step s),
+// k = 32 s + 8 q + i its nibble i; its block scale and zero point sit at
+// [g][b][c][j] of Sd and byte j of Zd[g][b][c]. Same arithmetic and order
+// as GenericKernel.
+__global__ __launch_bounds__(256) void GenericFragKernel(const float *__restrict__ A,
+                                                         const uint32_t *__restrict__ Bp,
+                                                         const float *__restrict__ Sd,
+                                                         const uint32_t *__restrict__ Zd,
+                                                         float *__restrict__ Y, int64_t M,
+                                                         int64_t K, int64_t N, int64_t nb,
+                                                         int log2_bs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (n >= N) return;
+  const int64_t g = n >> 6, T = K >> 5;
+  const int j = static_cast<int>((n >> 4) & 3), c = static_cast<int>(n & 15);
+  for (int64_t m = 0; m < M; ++m) {
+    const float *a = A + m * K;
+    float acc = 0.f;
+    for (int64_t k = lane; k < K; k += 64) {
+      const int64_t s = k >> 5, q = (k >> 3) & 3, b = k >> log2_bs;
+      const uint32_t word = Bp[((g * T + s) * 64 + q * 16 + c) * 4 + j];
+      const int qv = static_cast<int>((word >> (4 * (k & 7))) & 0xFu);
+      const int z = Zd ? static_cast<int>((Zd[(g * nb + b) * 16 + c] >> (8 * j)) & 0xFFu) : 8;
+      acc = fmaf(a[k], static_cast<float>(qv - z) * Sd[((g * nb + b) * 16 + c) * 4 + j], acc);
+    }
+    acc = WaveSum(acc);
+    if (lane == 0) Y[m * N + n] = acc;
+  }
+}
+
 template <int MT, int R, bool HAS_ZP>
 hipError_t LaunchGemvT(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s) {
   const int64_t waves = (w.N + R - 1) / R;
@@ -206,7 +238,7 @@ hipError_t LaunchGemvZ(const WeightView &w, int64_t M, const float *A, float *Y,
 } // namespace
 
 bool GemvSupports(const WeightView &w, int64_t M) {
-  return M >= 1 && M <= 16 && (w.K % 32) == 0 && w.block_size >= 32 &&
+  return w.B != nullptr && M >= 1 && M <= 16 && (w.K % 32) == 0 && w.block_size >= 32 &&
          w.K <= (int64_t{1} << 30) && w.N <= (int64_t{1} << 30) &&
          w.row_bytes <= (int64_t{1} << 30) && (w.row_bytes % 16) == 0 &&
          (reinterpret_cast<uintptr_t>(w.B) % 16) == 0;
@@ -219,6 +251,15 @@ hipError_t LaunchGemv(const WeightView &w, int64_t M, const float *A, float *Y, 
 hipError_t LaunchGeneric(const WeightView &w, int64_t M, const float *A, float *Y,
                          hipStream_t s) {
   const int64_t blocks = (w.N + 3) / 4;
+  if (w.B == nullptr) {
+    // a compact plan: the same over the fragment-ordered copy
+    if (w.Bp == nullptr || w.Sd == nullptr || (w.has_zp && w.Zd == nullptr))
+      return hipErrorInvalidValue;
+    hipLaunchKernelGGL(GenericFragKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, A,
+                       reinterpret_cast<const uint32_t *>(w.Bp), w.Sd, w.has_zp ? w.Zd : nullptr,
+                       Y, M, w.K, w.N, w.nb, w.log2_bs);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(GenericKernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, A, w.B,
                      w.scales, w.zp, Y, M, w.K, w.N, w.nb, static_cast<int64_t>(w.block_size),
                      w.row_bytes, w.zp_row_bytes);

@@ -522,7 +522,7 @@ bool GemvFragSupports(const WeightView &w, int64_t M) {
   // whole units per wavefront for some SPW with the image in LDS; 32-bit
   // buffer offsets.
   return M >= 1 && M <= 4 && w.Bp != nullptr && w.Sd != nullptr &&
-         (w.zp == nullptr || w.Zd != nullptr) && w.block_size >= 32 && w.block_size <= 256 &&
+         (!w.has_zp || w.Zd != nullptr) && w.block_size >= 32 && w.block_size <= 256 &&
          (w.block_size & (w.block_size - 1)) == 0 && (w.K % gf::kUnitK) == 0 &&
          gf::PickSpw(w, M) > 0 && (w.K / 32) * 1024 < (int64_t{1} << 31) &&
          w.nb * 256 < (int64_t{1} << 31) && M * w.K * 4 < (int64_t{1} << 31) &&
@@ -555,7 +555,7 @@ hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float 
        (reinterpret_cast<uintptr_t>(gamma) % 16) != 0))
     return hipErrorInvalidValue;
   const int m = static_cast<int>(M);
-  return w.zp != nullptr ? gf::LaunchZp<true>(w, m, A, Y, s, spw, win, H, bias, gamma, eps)
+  return w.has_zp ? gf::LaunchZp<true>(w, m, A, Y, s, spw, win, H, bias, gamma, eps)
                          : gf::LaunchZp<false>(w, m, A, Y, s, spw, win, H, bias, gamma, eps);
 }
 

@@ -514,8 +514,8 @@ bool GemvM1Supports(const WeightView &w) {
   // lane (the largest CPL instantiated) and A within 64 KiB of LDS; the
   // 16-byte scale loads need 16-byte aligned scales, the 2-byte zero-point
   // loads 2-byte aligned zero points.
-  return (w.K % 32) == 0 && w.K <= 16384 && w.block_size >= 32 && (w.row_bytes % 16) == 0 &&
-         (reinterpret_cast<uintptr_t>(w.B) % 16) == 0 &&
+  return w.B != nullptr && (w.K % 32) == 0 && w.K <= 16384 && w.block_size >= 32 &&
+         (w.row_bytes % 16) == 0 && (reinterpret_cast<uintptr_t>(w.B) % 16) == 0 &&
          (reinterpret_cast<uintptr_t>(w.scales) % 16) == 0 &&
          (reinterpret_cast<uintptr_t>(w.zp) % 2) == 0 &&
          w.row_bytes * w.N < (int64_t{1} << 31) && w.nb * 4 * w.N < (int64_t{1} << 31);

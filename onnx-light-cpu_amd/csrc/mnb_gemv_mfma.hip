@@ -527,7 +527,8 @@ hipError_t LaunchBsc(const WeightView &w, int64_t M, const float *A, float *Y, f
 bool GemvMfmaSupports(const WeightView &w, int64_t M) {
   // K in whole 512-k ranges (at most 64); power-of-two blocks of 32 or more;
   // every buffer offset (including one past the end) below 2^31.
-  return M >= 2 && M <= 16 && (w.K % mf::kKR) == 0 && w.K / mf::kKR <= mf::kMaxSplits &&
+  return w.B != nullptr && M >= 2 && M <= 16 && (w.K % mf::kKR) == 0 &&
+         w.K / mf::kKR <= mf::kMaxSplits &&
          w.block_size >= 32 && (w.block_size & (w.block_size - 1)) == 0 &&
          w.row_bytes * w.N + w.K < (int64_t{1} << 31) && w.nb * 4 * w.N < (int64_t{1} << 31) &&
          M * w.K * 4 + 512 < (int64_t{1} << 31) && M * w.N * 4 < (int64_t{1} << 31);

@@ -343,7 +343,8 @@ hipError_t LaunchGroup(const WeightView &w, int mt, const float *A, float *Y, hi
 bool GemvSmallMSupports(const WeightView &w, int64_t M) {
   // 32-bit buffer offsets; 16-byte scale loads (nb % 4 == 0 path) and 2-byte
   // zero-point loads need aligned bases; the default shape must fit the LDS.
-  if (M < 2 || M > 16 || (w.K % 32) != 0 || w.block_size < 32 || (w.row_bytes % 16) != 0)
+  if (w.B == nullptr || M < 2 || M > 16 || (w.K % 32) != 0 || w.block_size < 32 ||
+      (w.row_bytes % 16) != 0)
     return false;
   if ((reinterpret_cast<uintptr_t>(w.B) % 16) != 0 ||
       (reinterpret_cast<uintptr_t>(w.scales) % 16) != 0 ||

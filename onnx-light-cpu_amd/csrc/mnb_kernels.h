@@ -75,10 +75,13 @@ constexpr int kScaleExpTarget = 11;
 constexpr int kRowExpTarget = 14;
 
 // Everything a kernel needs to address one plan's constants.
+// B, scales and zp are null on a compact plan, which keeps only the re-laid
+// copies (see the plan's description in mnb_capi.hip); kernels on the
+// original layout then report themselves unsupported.
 struct WeightView {
-  const uint8_t *B;       // [N, nb, bs/2] packed nibbles, low nibble first
-  const float *scales;    // [N, nb]
-  const uint8_t *zp;      // [N, zp_row_bytes] packed nibbles, or nullptr (zp = 8)
+  const uint8_t *B;       // [N, nb, bs/2] packed nibbles, low nibble first, or nullptr
+  const float *scales;    // [N, nb], or nullptr
+  const uint8_t *zp;      // [N, zp_row_bytes] packed nibbles, or nullptr (zp = 8 or compact)
   const int32_t *col_exp; // [N] RangeExponent(max_b |scales[n][b]|, kScaleExpTarget)
   const uint8_t *Bp;      // the prefill kernel's fragment-ordered weights, or nullptr
   const uint8_t *Sp;      // its per-step scale / zero-point words, or nullptr
@@ -92,6 +95,7 @@ struct WeightView {
   int32_t block_size;
   int32_t log2_bs;
   int32_t num_cus;        // compute units of the plan's device
+  int32_t has_zp;         // MatMulNBits input 3 present (Zd holds it on a compact plan)
 };
 
 // Decode GEMV, M in [1, 16], K % 32 == 0, block_size >= 32.
@@ -230,7 +234,11 @@ hipError_t LaunchStream(const WeightView &w, int64_t M, const float *A, float *Y
 bool PrefillLayoutWanted(const WeightView &w);
 size_t PrefillLayoutBytes(const WeightView &w, size_t *sp_bytes);
 hipError_t LaunchPrefillRelayout(const WeightView &w, uint8_t *Bp, uint8_t *Sp, hipStream_t s);
+// The GEMM path (path 2): GemmKernel on the original layout, or the prefill
+// / streaming kernels on the re-laid copy.
 bool GemmSupports(const WeightView &w, int64_t M);
+// GemmKernel itself (the original layout).
+bool GemmKernelSupports(const WeightView &w, int64_t M);
 size_t GemmWorkspaceBytes(const WeightView &w, int64_t M);
 // Same with an explicit tile height (32, 64 or 128; 0 picks both;
 // kPrefillTileCode = the prefill kernel) and split count (1..16), for

@@ -22,6 +22,7 @@ def test_library_exports_every_header_function(pkg):
         "mnb_last_error", "mnb_weight_bytes", "mnb_version", "mnb_qdq_repack",
         "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes", "mnb_run_rmsnorm",
         "mnb_run_no_alloc", "mnb_kernel_name", "mnb_kernel_workspace_bytes", "mnb_run_kernel",
+        "mnb_plan_device_bytes",
         "mnb_stream_read"])
     for name in names:
         assert hasattr(L, name), name
@@ -101,6 +102,7 @@ def test_run_and_queries_reject_null_plan(pkg):
     assert L.mnb_select_path(None, 1, ctypes.byref(p)) == NULLP
     assert L.mnb_run_no_alloc(None, 1, None, None, None) == NULLP
     assert L.mnb_plan_destroy(None) == MNB_OK
+    assert L.mnb_plan_device_bytes(None, ctypes.byref(x)) == NULLP
     assert L.mnb_run_rmsnorm(None, 1, None, None, 1e-5, None, None, 0, None) == NULLP
     assert L.mnb_rmsnorm_workspace_bytes(None, 1, ctypes.byref(x)) == NULLP
 

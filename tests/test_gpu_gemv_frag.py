@@ -38,7 +38,10 @@ def test_m1_frag_vs_oracle_and_m1(pkg, orc, cuda, K, N, bs, zp, spws):
     import torch
     B, S, Z = _weights(pkg, K, N, bs, zp, seed=K + N + bs)
     A = pkg.workloads.make_activations(1, K, 1.0, seed=K + 5)
-    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    # a plan over borrowed device weights keeps the original layout that
+    # GemvM1Kernel reads (a host-created plan of c2's shape is compact)
+    dev = [None if x is None else torch.from_numpy(x).to(cuda) for x in (B, S, Z)]
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare_device(*dev)
     dA = torch.from_numpy(A).to(cuda)
     y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
     y32 = orc.matmul_nbits_ref_f32(A, B, S, Z, K, N, bs)
