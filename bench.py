@@ -40,12 +40,12 @@ METRIC = "MatMulNBits 4-bit: M=1 achieved HBM GB/s; M=2048 TFLOP/s; % roofline"
 ROTATION_BYTES = 1 << 30
 
 # HBM bytes per launch of the headline kernel (GemvFragKernel on c2 M=1),
-# from two rocprofv3 --pmc passes over `bench.py --only decode,gemm,sweep,copy --eager
-# --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15580.1 KiB and
+# from two rocprofv3 --pmc passes over `bench.py --only decode,gemm,sweep,copy,lm_head
+# --eager --steps 3 --warmup 1 --cpu-seconds 0`: FETCH_SIZE 15584.6 KiB and
 # WRITE_SIZE 56.0 KiB per dispatch, each scaled by what the same counter reads
 # for the copy leg's 512 MiB device copy (FETCH_SIZE 262155.5 KiB -> x1.99992,
 # WRITE_SIZE 524288.0 KiB -> x1.00000). Re-measure when the kernel changes.
-GEMV_M1_C2_TRAFFIC_BYTES = round((15580.1 * (524288.0 / 262155.5) + 56.0) * 1024)
+GEMV_M1_C2_TRAFFIC_BYTES = round((15584.6 * (524288.0 / 262155.5) + 56.0) * 1024)
 
 
 def parse_args():
@@ -56,8 +56,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline sampling budget over its four modes (0 disables)")
     ap.add_argument("--only", default="",
-                    help="comma list of legs: decode,ceiling,gemm,sweep,c5,gate_up,rmsnorm,plan,"
-                         "cpu,copy (default: all but copy)")
+                    help="comma list of legs: decode,ceiling,gemm,sweep,lm_head,c5,gate_up,rmsnorm,"
+                         "plan,cpu,copy,gemm_shapes (default: all but copy and gemm_shapes)")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step directly instead of replaying a HIP graph "
                          "(for counter collection, which serialises dispatches)")
@@ -229,14 +229,19 @@ def gpu_metadata(torch, dev):
             md["hip_driver_version"] = v.value
     except (OSError, StopIteration, AttributeError) as e:
         md["hip_versions_error"] = str(e)
-    try:
-        r = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True,
-                           text=True, timeout=30)
-        clocks = json.loads(r.stdout) if r.returncode == 0 else {}
-        md["clocks_after_run"] = {card: {k: v for k, v in vals.items() if "clk" in k.lower()}
-                        for card, vals in clocks.items() if isinstance(vals, dict)}
-    except (OSError, subprocess.SubprocessError, ValueError) as e:
-        md["clocks_error"] = str(e)
+    # the current clock levels (the line marked *) from the driver's sysfs
+    # tables, read as files (no helper process)
+    clocks = {}
+    for dev_dir in sorted(pathlib.Path("/sys/class/drm").glob("card*/device")):
+        for table in ("pp_dpm_sclk", "pp_dpm_mclk", "pp_dpm_fclk"):
+            try:
+                cur = [ln.strip() for ln in (dev_dir / table).read_text().splitlines()
+                       if ln.strip().endswith("*")]
+            except OSError:
+                continue
+            if cur:
+                clocks.setdefault(dev_dir.parent.name, {})[table] = cur[0]
+    md["clocks_after_run"] = clocks
     return md
 
 
@@ -430,6 +435,46 @@ def gemm_leg(torch, pkg, dev, p, M, steps, warmup, seed, stream):
            "validation": validate(torch, p, A, sets[0], Y, op.select_path(M), seed=seed)}
     op.release()
     return res
+
+
+def gemm_shapes_leg(torch, pkg, dev, Ms, steps, warmup, stream):
+    """The GEMM path's kernel choice, measured (not run by default): per c5
+    projection and c4 at each M, us per call of the automatic path against
+    GemmKernel's own shape choice and the prefill kernel with 1, 2 and 4 K
+    splits and with its own choice (mnb_run_kernel), CALLS_PER_STEP calls per
+    graph replay on one weight copy."""
+    W = pkg.workloads
+    out = []
+    projections = list(W.CONFIGS["c5"].projections) + [W.CONFIGS["c4"].projections[0]]
+    for p in projections:
+        B, S, Z = W.make_weights(p, 41)
+        op = pkg.MatMulNBits(p.K, p.N, 4, p.block_size).prepare(B, S, Z)
+        for M in Ms:
+            A = torch.randn((M, p.K), device=dev)
+            Y = torch.empty((M, p.N), device=dev)
+            r = {"projection": p.name, "K": p.K, "N": p.N, "M": M, "auto_kernel": op.kernel_name(M)}
+            variants = [("auto", lambda: op(A, out=Y, stream=torch.cuda.current_stream())),
+                        ("gemm_kernel", lambda: op.run_kernel(A, pkg.KERNEL_GEMM, out=Y,
+                                                              stream=torch.cuda.current_stream())),
+                        ("prefill_auto_splits", lambda: op.run_kernel(
+                            A, pkg.KERNEL_PREFILL, out=Y, stream=torch.cuda.current_stream()))]
+            for sp in (1, 2, 4):
+                variants.append((f"prefill_{sp}_splits", lambda sp=sp: op.run_kernel(
+                    A, pkg.KERNEL_PREFILL, sp, out=Y, stream=torch.cuda.current_stream())))
+            for name, fn in variants:
+                try:
+                    ms, _, _, _ = time_graph(torch, lambda fn=fn: [fn() for _ in range(CALLS_PER_STEP)],
+                                             steps, warmup, stream)
+                    r[name + "_us"] = ms * 1e3 / CALLS_PER_STEP
+                except pkg.MatMulNBitsError:
+                    r[name + "_us"] = None  # not served by this plan (compact: no original layout)
+            r["auto_TFLOPs"] = p.flops(M) / (r["auto_us"] * 1e-6) / 1e12
+            out.append(r)
+            print(f"# gemm shapes {p.name} M={M}: " + " ".join(
+                f"{k[:-3]}={v:.1f}" for k, v in r.items() if k.endswith("_us") and v is not None),
+                file=sys.stderr, flush=True)
+        op.release()
+    return out
 
 
 def gate_up_leg(torch, pkg, dev, Ms, steps, warmup, stream):
@@ -791,6 +836,10 @@ def main():
                                                  "us_per_launch_iqr", "GBps", "path", "kernel")})
                 print(f"# decode {cname} M={M}: {r['us_per_launch']:.2f} us, {r['GBps']:.0f} GB/s",
                       file=sys.stderr, flush=True)
+    gemm_shapes = None
+    if "gemm_shapes" in legs:
+        gemm_shapes = gemm_shapes_leg(torch, pkg, dev, (128, 256, 512, 1024), max(3, args.steps // 4),
+                                      2, stream)
     lm_head = None
     if "lm_head" in legs:
         # Llama-3-8B's LM head at decode: the one decode launch large enough
@@ -896,6 +945,7 @@ def main():
         "read_ceilings": ceilings,
         "launch_floor": floor,
         "lm_head_decode": lm_head,
+        "gemm_shapes": gemm_shapes,
         "headline_samples_us_per_launch": head["us_per_launch_samples"] if head else None,
         "plan_create": plans,
         "rmsnorm_fusion": rms,
