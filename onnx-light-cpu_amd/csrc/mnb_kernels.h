@@ -32,19 +32,20 @@ __device__ __forceinline__ void CopyToLds16(const void *gsrc, uint32_t lds_base)
 }
 #pragma clang diagnostic pop
 
-// Gated-MLP activation of one gate/up pair: silu(g) * u = g * sigmoid(g) * u,
-// with sigmoid(g) = 1 / (1 + exp(-g)) from the hardware exp2 and reciprocal
-// (v_exp_f32, v_rcp_f32, 1 ulp each): a few instructions instead of the
-// libm-exact expf and division, which made the GEMM's fused epilogue cost
-// more than the pass it removes. Relative error about 3e-7 + |g| * 6e-8
-// (the rounding of -g * log2(e)). Large |g| saturate cleanly: exp2 of a
-// large argument is +inf and its reciprocal 0, of a very negative one 0.
-// Every kernel that applies the activation (fused epilogues and the separate
-// SiluMulKernel) uses this one expression, so a fused result equals the
-// unfused one bit for bit.
+// Gated-MLP activation of one gate/up pair, in the order of the ONNX subgraph
+// it replaces: s = Sigmoid(g) = 1 / (1 + exp(-g)), then Mul(g, s), then
+// Mul(., u), each rounded to fp32. exp is the device library's expf (at most
+// 1 ulp, arguments reduced in extended precision, so its error does not grow
+// with |g|) and the reciprocal v_rcp_f32 (1 ulp). Error contract, against the
+// exact g * sigmoid(g) * u of the fp32 g and u: at most 2^-20 relative, plus
+// 2^-126 * |g * u| absolute where sigmoid(g) falls below fp32's normal range
+// (g < -87). Special values follow the subgraph: g = +inf gives +-inf * u,
+// g = -inf gives NaN (-inf * 0), NaN propagates. Every kernel that applies
+// the activation (fused epilogues and the separate SiluMulKernel) uses this
+// one expression, so a fused result equals the unfused one bit for bit.
 __device__ __forceinline__ float SiluMul(float g, float u) {
-  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
-  return g * u * __builtin_amdgcn_rcpf(1.0f + e);
+  const float s = __builtin_amdgcn_rcpf(1.0f + expf(-g));
+  return (g * s) * u;
 }
 
 // The value of lane ^ 1 (DPP quad_perm [1,0,3,2]: one VALU move, no LDS

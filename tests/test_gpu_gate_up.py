@@ -14,7 +14,8 @@ Every route is covered: the M = 1 kernel's fused epilogue, M = 2..4 with the
 separate SiLU pass, the MFMA decode with the activation in its partial-sum
 pass (and with one 512-k range, where the pass is separate), the GEMM with
 one split (fused into its stores) and several (fused into the reduction),
-and the generic path.
+and the generic path. test_silu_error_contract pins the activation itself on
+every route, with products made exact.
 """
 import ctypes
 
@@ -134,5 +135,58 @@ def test_gate_up_fused_gemv_needs_no_workspace(pkg, cuda):
             assert L.mnb_run_ex(op._plan, M, P(dA), None, P(out), None, 0, stream, 0) == 0
             torch.cuda.synchronize()
             np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    finally:
+        op.release()
+
+
+def _selector(K, I, col, scale):
+    """Weights with one nonzero per row, w[n, col[n]] = scale (nibble 9, no
+    zero points: implicit 8), and 0 elsewhere: the product is one activation
+    times scale, exactly, on every kernel when the activations are
+    multiples of 2^-6 below 32 in magnitude (11 significant bits, all partial
+    sums below 2^24 units)."""
+    q = np.full((I, K), 8, np.uint8)
+    q[np.arange(I), col] = 9
+    bs = 32
+    B = (q[:, 0::2] | (q[:, 1::2] << 4)).reshape(I, K // bs, bs // 2)
+    return np.ascontiguousarray(B), np.full((I, K // bs), scale, np.float32), None
+
+
+@pytest.mark.parametrize("I", [1024, 8192])   # 2048 rows (GemvM1, GemvSmallM) / 16384 (GemvFrag)
+def test_silu_error_contract(pkg, orc, cuda, I):
+    """The activation itself, on every route, against the exact
+    g * sigmoid(g) * u of the products (ONNX Sigmoid -> Mul -> Mul): selector
+    weights make the gate and up products exact (g = 4 a[k_g], u = a[k_u]), so
+    H's only error is the activation's. Contract (SiluMul): at most 2^-20
+    relative, plus 2^-126 |g u| where sigmoid(g) is below fp32's normal range,
+    for g over [-128, 128] (most in [-20, 20])."""
+    import torch
+    K = 512
+    n = np.arange(I)
+    kg, ku = n % K, (7 * n + 3) % K
+    Bg, Sg, Zg = _selector(K, I, kg, 4.0)
+    Bu, Su, Zu = _selector(K, I, ku, 1.0)
+    op = pkg.GateUpSiLU(K, I, 4, 32).prepare(Bg, Sg, Zg, Bu, Su, Zu)
+    rng = np.random.default_rng(I)
+    routes = [(M, pkg.PATH_AUTO) for M in (1, 2, 3, 4, 5, 8, 16, 17, 32, 64, 100, 300)]
+    routes += [(4, pkg.PATH_GENERIC), (8, pkg.PATH_EXACT), (16, pkg.PATH_GEMM),
+               (100, pkg.PATH_PREFILL)]
+    try:
+        for M, path in routes:
+            j = np.where(rng.random((M, K)) < 0.5, rng.integers(-2047, 2048, (M, K)),
+                         rng.integers(-320, 321, (M, K)))
+            A = (j / 64.0).astype(np.float32)
+            H = op(torch.from_numpy(A).to(cuda), path=path).cpu().numpy()
+            g = 4.0 * A[:, kg].astype(np.float64)
+            u = A[:, ku].astype(np.float64)
+            h64 = orc.silu_mul_f64(g, u)
+            err = np.abs(H.astype(np.float64) - h64)
+            bound = 2.0 ** -20 * np.abs(h64) + 2.0 ** -126 * np.abs(g * u) + 2.0 ** -149
+            worst = np.unravel_index(np.argmax(err / bound), err.shape)
+            rel = np.max(np.where(np.abs(h64) > 2.0 ** -126, err / np.maximum(np.abs(h64), 1e-300), 0))
+            print(f"case silu contract I={I} M={M} path={path} kernel={op.kernel_name(M)}: "
+                  f"max rel error {rel:.2e} (bound {2.0 ** -20:.2e})", flush=True)
+            assert np.all(err <= bound), (M, path, worst, float(g[worst]), float(u[worst]),
+                                          float(H[worst]), float(h64[worst]))
     finally:
         op.release()
