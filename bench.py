@@ -155,21 +155,29 @@ def copy_leg(torch, dev, steps, warmup, stream):
             "GBps": 2 * n / (ms * 1e-3) / 1e9, "wall_s": wall}
 
 
-def stream_ceiling_leg(torch, pkg, dev, nbytes, steps, warmup, stream):
+def stream_ceiling_leg(torch, pkg, dev, nbytes, steps, warmup, stream, grid=None):
     """The HBM read ceiling for one launch of nbytes: mnb_stream_read (loads
     only, 8 KiB contiguous records per wavefront) over as many rotated
-    buffers as the headline leg, one launch each, graph-replayed."""
+    buffers as the headline leg, one launch each, graph-replayed. With grid =
+    (workgroups, threads): mnb_stream_read_grid, the same reads on that grid
+    (one contiguous share per wavefront)."""
     import ctypes
     rot = max(2, -(-ROTATION_BYTES // nbytes))
     bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(i & 0xFF) for i in range(rot)]
-    out = torch.empty(2048, dtype=torch.int32, device=dev)  # MNB_STREAM_OUT_WORDS
+    words = 2048 if grid is None else grid[0] * grid[1] // 64  # one per wavefront
+    out = torch.empty(words, dtype=torch.int32, device=dev)
     L = pkg.library()
 
     def launches():
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         for b in bufs:
-            rc = L.mnb_stream_read(ctypes.c_void_p(b.data_ptr()), nbytes,
-                                   ctypes.c_void_p(out.data_ptr()), out.numel(), st)
+            if grid is None:
+                rc = L.mnb_stream_read(ctypes.c_void_p(b.data_ptr()), nbytes,
+                                       ctypes.c_void_p(out.data_ptr()), out.numel(), st)
+            else:
+                rc = L.mnb_stream_read_grid(ctypes.c_void_p(b.data_ptr()), nbytes,
+                                            ctypes.c_void_p(out.data_ptr()), out.numel(),
+                                            grid[0], grid[1], st)
             if rc != 0:
                 raise RuntimeError(f"mnb_stream_read: status {rc}")
 
@@ -177,7 +185,9 @@ def stream_ceiling_leg(torch, pkg, dev, nbytes, steps, warmup, stream):
     us = ms * 1e3 / rot
     del bufs
     torch.cuda.empty_cache()
-    return {"kernel": "StreamReadKernel (mnb_stream_read)", "bytes_per_launch": nbytes,
+    kernel = ("StreamReadKernel (mnb_stream_read)" if grid is None else
+              f"StreamChunkKernel (mnb_stream_read_grid, {grid[0]} x {grid[1]} threads)")
+    return {"kernel": kernel, "bytes_per_launch": nbytes,
             "rotation_copies": rot, "us_per_launch": us, "us_per_launch_median": med * 1e3 / rot,
             "us_per_launch_samples": last_samples(rot), "GBps": nbytes / (us * 1e-6) / 1e9,
             "frac_of_peak": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
@@ -442,7 +452,8 @@ def gemm_shapes_leg(torch, pkg, dev, Ms, steps, warmup, stream):
     projection and c4 at each M, us per call of the automatic path against
     GemmKernel's own shape choice and the prefill kernel with 1, 2 and 4 K
     splits and with its own choice (mnb_run_kernel), CALLS_PER_STEP calls per
-    graph replay on one weight copy."""
+    graph replay on one weight copy; beside them hipBLASLt's dense fp16 GEMM
+    of the shape (fp16_gemm_reference)."""
     W = pkg.workloads
     out = []
     projections = list(W.CONFIGS["c5"].projections) + [W.CONFIGS["c4"].projections[0]]
@@ -468,6 +479,9 @@ def gemm_shapes_leg(torch, pkg, dev, Ms, steps, warmup, stream):
                     r[name + "_us"] = ms * 1e3 / CALLS_PER_STEP
                 except pkg.MatMulNBitsError:
                     r[name + "_us"] = None  # not served by this plan (compact: no original layout)
+            # the vendor's dense fp16 GEMM on the shape (no 4-bit decode, no input conversion)
+            r["hipblaslt_fp16_us"] = fp16_gemm_reference(torch, dev, p, M, steps, warmup,
+                                                         stream)["us_per_launch"]
             r["auto_TFLOPs"] = p.flops(M) / (r["auto_us"] * 1e-6) / 1e12
             out.append(r)
             print(f"# gemm shapes {p.name} M={M}: " + " ".join(
@@ -838,7 +852,8 @@ def main():
                       file=sys.stderr, flush=True)
     gemm_shapes = None
     if "gemm_shapes" in legs:
-        gemm_shapes = gemm_shapes_leg(torch, pkg, dev, (128, 256, 512, 1024), max(3, args.steps // 4),
+        gemm_shapes = gemm_shapes_leg(torch, pkg, dev, (128, 256, 512, 1024, 2048),
+                                      max(3, args.steps // 4),
                                       2, stream)
     lm_head = None
     if "lm_head" in legs:
@@ -880,8 +895,14 @@ def main():
                  ("c3 M=1", W.CONFIGS["c3"].projections[0].algorithmic_bytes(1)),
                  ("LM head M=1", W.Projection("lm_head", 4096, 128256, 128, True)
                   .algorithmic_bytes(1))]
-        for name, nbytes in sizes:
-            r = stream_ceiling_leg(torch, pkg, dev, nbytes, args.steps, args.warmup, stream)
+        # and c2's bytes read on GemvFragKernel's own grid: one workgroup of 8
+        # wavefronts per 64-row group, 224 workgroups (the CUs it can use)
+        c2 = W.CONFIGS["c2"].projections[0]
+        sizes.append(("c2 M=1 on GemvFragKernel's grid", c2.algorithmic_bytes(1),
+                      ((c2.N + 63) // 64, 64 * min(16, c2.K // 512))))
+        for name, nbytes, *grid in sizes:
+            r = stream_ceiling_leg(torch, pkg, dev, nbytes, args.steps, args.warmup, stream,
+                                   grid[0] if grid else None)
             r["for"] = name
             ceilings.append(r)
             print(f"# read ceiling {name}, {nbytes} B per launch: {r['us_per_launch']:.2f} us, "
@@ -924,6 +945,9 @@ def main():
             roof["ceiling"] = ceiling["frac_of_peak"]
             roof["ceiling_GBps"] = ceiling["GBps"]
             roof["frac_of_ceiling"] = head["GBps"] / ceiling["GBps"]
+            grid_ceiling = ceilings[-1]
+            roof["grid_ceiling_GBps"] = grid_ceiling["GBps"]
+            roof["frac_of_grid_ceiling"] = head["GBps"] / grid_ceiling["GBps"]
         workload = ("c2: MatMulNBits M=1 K=4096 N=14336 bits=4 block_size=128 zero_points; "
                     f"{head['rotation_copies']} rotated weight copies per step")
     else:

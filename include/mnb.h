@@ -271,6 +271,16 @@ int mnb_run_kernel(const mnb_plan *plan, int64_t M, const float *dA, float *dY, 
 int mnb_stream_read(const void *dSrc, size_t bytes, uint32_t *dOut, size_t out_words,
                     void *stream);
 
+/* The same probe on a given grid: `workgroups` workgroups of `threads`
+ * threads (a multiple of 64, at most 1024), each wavefront reading one
+ * contiguous share of the bytes (rounded up to 1 KiB) with eight 16-byte
+ * loads in flight, one word per wavefront into dOut (out_words >= the
+ * wavefront count, at most 65536). It gives the read rate a decode kernel's
+ * own grid allows, e.g. one workgroup of 8 wavefronts per 64-row group. No
+ * counterpart in the reference. */
+int mnb_stream_read_grid(const void *dSrc, size_t bytes, uint32_t *dOut, size_t out_words,
+                         int workgroups, int threads, void *stream);
+
 /* Text for a status code (static storage). */
 const char *mnb_status_str(int status);
 

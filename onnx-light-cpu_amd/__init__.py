@@ -91,12 +91,14 @@ def library():
         L.mnb_run_kernel.argtypes = [vp, i64, vp, vp, vp, sz, vp, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_int]
         L.mnb_stream_read.argtypes = [vp, sz, vp, sz, vp]
+        L.mnb_stream_read_grid.argtypes = [vp, sz, vp, sz, ctypes.c_int, ctypes.c_int, vp]
         for name in ("mnb_plan_create", "mnb_plan_create_device", "mnb_plan_destroy",
                      "mnb_workspace_bytes", "mnb_run", "mnb_run_path", "mnb_select_path",
                      "mnb_weight_bytes", "mnb_run_ex", "mnb_qdq_repack",
                      "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes",
                      "mnb_run_rmsnorm", "mnb_run_no_alloc", "mnb_kernel_workspace_bytes",
-                     "mnb_run_kernel", "mnb_stream_read", "mnb_plan_device_bytes"):
+                     "mnb_run_kernel", "mnb_stream_read", "mnb_stream_read_grid",
+                     "mnb_plan_device_bytes"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib

@@ -1444,10 +1444,10 @@ bool PrefillSupportsM(const WeightView &w, int64_t M) {
 }
 
 // The prefill kernel serves the automatic GEMM path
-// - when its 128 x 256 tiles alone fill the CUs in whole waves (the last
-//   wave at least 85% full): no split-K, one workgroup per CU busy to the
-//   end; a half-empty last wave (c5 qkv at M = 2048, 1.5 waves: 146 against
-//   156 us) stays with GemmKernel;
+// - when its 128 x 256 tiles alone fill at least one wave of CUs and the
+//   last wave is at least half full: no split-K, one workgroup per CU (c5
+//   qkv at M = 2048, 1.5 waves: 121.4 against GemmKernel's 130.6 us in one
+//   process; a last wave below half stays with GemmKernel's smaller tiles);
 // - when they do not fill one wave, with K split (PrefillSplits) as long as
 //   each split keeps at least 12 k-tiles (shorter splits spend most of their
 //   time in the prologue and the epilogue).
@@ -1466,8 +1466,8 @@ bool UsePrefill(const WeightView &w, int64_t M) {
     const int64_t splits = std::min<int64_t>(cus / tiles, kPrefillMaxSplits);
     return w.K / kBK >= 12 * splits;
   }
-  const int64_t waves = (tiles + cus - 1) / cus;
-  return tiles * 100 >= waves * cus * 85;
+  const int64_t last = tiles - (tiles - 1) / cus * cus;  // workgroups in the last wave
+  return last * 2 >= cus;
 }
 
 size_t PrefillPartialBytes(const WeightView &w, int64_t M) {

@@ -447,8 +447,10 @@ hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipSt
       if (spw == 8) MNB_GF_LAUNCH(8, 8, 2, false);
       else MNB_GF_LAUNCH(16, 8, 2, false);
     } else {
+      // 16 steps at 4 rows only above 32-k blocks (ShapeFits; that launch
+      // with 32-k blocks spills registers and is not built)
       if (spw == 8) MNB_GF_LAUNCH(8, 8, 4, false);
-      else MNB_GF_LAUNCH(16, 8, 4, false);
+      else if constexpr (SPB > 1) MNB_GF_LAUNCH(16, 8, 4, false);
     }
   } else if (win == 8) {
     switch (spw) {

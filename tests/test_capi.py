@@ -23,7 +23,7 @@ def test_library_exports_every_header_function(pkg):
         "mnb_plan_create_gate_up", "mnb_rmsnorm_workspace_bytes", "mnb_run_rmsnorm",
         "mnb_run_no_alloc", "mnb_kernel_name", "mnb_kernel_workspace_bytes", "mnb_run_kernel",
         "mnb_plan_device_bytes",
-        "mnb_stream_read"])
+        "mnb_stream_read", "mnb_stream_read_grid"])
     for name in names:
         assert hasattr(L, name), name
 
@@ -105,6 +105,22 @@ def test_run_and_queries_reject_null_plan(pkg):
     assert L.mnb_plan_device_bytes(None, ctypes.byref(x)) == NULLP
     assert L.mnb_run_rmsnorm(None, 1, None, None, 1e-5, None, None, 0, None) == NULLP
     assert L.mnb_rmsnorm_workspace_bytes(None, 1, ctypes.byref(x)) == NULLP
+
+
+def test_stream_probes_validate_before_the_device(pkg):
+    """The read probes reject null buffers, empty or oversized reads, bad
+    grids and a short output before any HIP call (fake non-null pointers are
+    never dereferenced on these paths)."""
+    L = pkg.library()
+    fake = ctypes.c_void_p(0x1000)
+    assert L.mnb_stream_read(None, 1024, fake, 2048, None) == NULLP
+    assert L.mnb_stream_read(fake, 0, fake, 2048, None) == SHAPE
+    assert L.mnb_stream_read(fake, 1024, fake, 100, None) == WORK
+    assert L.mnb_stream_read_grid(fake, 1024, None, 2048, 224, 512, None) == NULLP
+    assert L.mnb_stream_read_grid(fake, 1 << 31, fake, 2048, 224, 512, None) == SHAPE
+    for wgs, threads in ((224, 500), (224, 0), (224, 2048), (0, 512), (70000, 64)):
+        assert L.mnb_stream_read_grid(fake, 1024, fake, 1 << 20, wgs, threads, None) == SHAPE
+    assert L.mnb_stream_read_grid(fake, 1024, fake, 1791, 224, 512, None) == WORK
 
 
 def test_gate_up_plan_validates_before_the_device(pkg):
