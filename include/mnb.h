@@ -69,7 +69,9 @@ typedef struct mnb_plan mnb_plan;
  * the device copies. Replaces the reference's prepared plan with a constant B
  * (MatMulPlan constant_b, onnx_light_cpu/impl/math/gemm/gemm_plan.h:161-195;
  * GemmPlanOptions::constant_b, gemm_plan.h:34-38). zero_points must be NULL
- * when desc->has_zero_points == 0. */
+ * when desc->has_zero_points == 0. Plan creation allocates device memory and
+ * waits for its own copies and re-layout kernels: create plans before, not
+ * during, the capture of a stream of the device into a HIP graph. */
 int mnb_plan_create(const mnb_desc *desc, const uint8_t *B, const float *scales,
                     const uint8_t *zero_points, mnb_plan **out_plan);
 
