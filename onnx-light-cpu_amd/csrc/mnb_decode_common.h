@@ -86,6 +86,44 @@ __device__ __forceinline__ float DppAdd(float v) {
   return v + __int_as_float(moved);
 }
 
+template <int CTRL>
+__device__ __forceinline__ float DppMax(float v) {
+  const int moved = __builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true);
+  return fmaxf(v, __int_as_float(moved));
+}
+
+// The value of lane ^ 16 (ds_swizzle, bit mode: and 0x1F, or 0, xor 0x10;
+// no memory access).
+__device__ __forceinline__ float Xor16(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+
+// Largest value over each 32-lane half of the wavefront, every lane of the
+// half holding it: the xor butterfly over 1, 2, 4, 8 and 16 lanes with DPP
+// moves (row_half_mirror and row_mirror pair the same lanes' values as xor 4
+// and xor 8 once the smaller groups agree) instead of LDS permutes.
+__device__ __forceinline__ float HalfMax(float v) {
+  v = DppMax<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = DppMax<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = DppMax<0x141>(v);  // row_half_mirror
+  v = DppMax<0x140>(v);  // row_mirror
+  return fmaxf(v, Xor16(v));
+}
+
+// Sum over aligned groups of LANES (4, 8, 16 or 32) lanes, every lane of a
+// group holding it: the same additions, in the same order, as the xor
+// butterfly over 1, 2, ... LANES / 2 (so bit-identical to it).
+template <int LANES>
+__device__ __forceinline__ float GroupSum(float v) {
+  static_assert(LANES == 4 || LANES == 8 || LANES == 16 || LANES == 32, "group size");
+  v = DppAdd<0xB1>(v);
+  v = DppAdd<0x4E>(v);
+  if constexpr (LANES >= 8) v = DppAdd<0x141>(v);
+  if constexpr (LANES >= 16) v = DppAdd<0x140>(v);
+  if constexpr (LANES >= 32) v += Xor16(v);
+  return v;
+}
+
 // Sum over the 64 lanes; the result is wave-uniform.
 __device__ __forceinline__ float WaveTotal(float v) {
   v = DppAdd<0xB1>(v);   // quad_perm [1,0,3,2]

@@ -137,8 +137,7 @@ __global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A
     float q = 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) q += v0[c] * v0[c] + v1[c] * v1[c];
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) q += __shfl_xor(q, o);
+    q = GroupSum<32>(q);
     if (ch == 0) sq[u * kTok + t] = q;
     v0 *= floatx4{g0.x, g0.y, g0.z, g0.w};
     v1 *= floatx4{g1.x, g1.y, g1.z, g1.w};
@@ -146,8 +145,7 @@ __global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A
   float amax = 0.f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) amax = fmaxf(amax, fmaxf(fabsf(v0[c]), fabsf(v1[c])));
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  amax = HalfMax(amax);
   // The largest magnitude times 2^e in [2^14, 2^15); ldexp is exact for
   // every e this gives (|e| <= 163), subnormal inputs included. A zero, inf
   // or NaN maximum gives e = 0 (inf and NaN then propagate).

@@ -219,8 +219,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fmaxf(fabsf(va[p][0][i]), fabsf(va[p][1][i])));
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    amax = HalfMax(amax);
     const int e = RangeExponent(amax, 14);
     half8 h[kTerms];
     float ssum = 0.f;
@@ -238,8 +237,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
       h[1][o] = t1;
       h[2][o] = t2;
     }
-#pragma unroll
-    for (int o = 1; o < 4 * SPB; o <<= 1) ssum += __shfl_xor(ssum, o, 64);
+    ssum = GroupSum<4 * SPB>(ssum);
     ssum *= 5.9604644775390625e-8f;  // 2^-24 (exact), before the block sums leave the lanes
     const int it = 2 * p + (lane >> 5);
     const int ul = it / MT, m = it % MT;
