@@ -92,10 +92,13 @@ __device__ __forceinline__ float DppMax(float v) {
   return fmaxf(v, __int_as_float(moved));
 }
 
-// The value of lane ^ 16 (ds_swizzle, bit mode: and 0x1F, or 0, xor 0x10;
-// no memory access).
-__device__ __forceinline__ float Xor16(float v) {
-  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+// Largest value over each aligned 16-lane row, every lane of the row holding
+// it (the xor butterfly over 1, 2, 4 and 8 lanes with DPP moves).
+__device__ __forceinline__ float RowMax16(float v) {
+  v = DppMax<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = DppMax<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = DppMax<0x141>(v);  // row_half_mirror
+  return DppMax<0x140>(v);  // row_mirror
 }
 
 // Largest value over each 32-lane half of the wavefront, every lane of the
@@ -103,10 +106,7 @@ __device__ __forceinline__ float Xor16(float v) {
 // moves (row_half_mirror and row_mirror pair the same lanes' values as xor 4
 // and xor 8 once the smaller groups agree) instead of LDS permutes.
 __device__ __forceinline__ float HalfMax(float v) {
-  v = DppMax<0xB1>(v);   // quad_perm [1,0,3,2]
-  v = DppMax<0x4E>(v);   // quad_perm [2,3,0,1]
-  v = DppMax<0x141>(v);  // row_half_mirror
-  v = DppMax<0x140>(v);  // row_mirror
+  v = RowMax16(v);
   return fmaxf(v, Xor16(v));
 }
 

@@ -1178,7 +1178,7 @@ __global__ __launch_bounds__(512) void StreamKernel(
 #pragma unroll
         for (int c = 0; c < 4; ++c)
           amax = fmaxf(amax, fmaxf(fabsf(alo[i][tg][c]), fabsf(ahi[i][tg][c])));
-      amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+      amax = fmaxf(amax, Xor16(amax));
       amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
       const int f = RangeExponent(amax, kRowExpTarget);
       fw[tg] = f;

@@ -262,8 +262,7 @@ __global__ __launch_bounds__(64 * kWaves) void GemvMfmaKernel(
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int c = 0; c < 4; ++c) amax = fmaxf(amax, fabsf(av[i][c]));
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = RowMax16(amax);
     // e puts the largest magnitude in [2^14, 2^15); applied with ldexp, which
     // is exact for every e this gives (|e| <= 163), subnormal inputs included.
     int e = 0;

@@ -55,6 +55,12 @@ __device__ __forceinline__ float PairSwap(float v) {
       float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
 }
 
+// The value of lane ^ 16 (ds_swizzle, bit mode: and 0x1F, or 0, xor 0x10;
+// no memory access, a shorter path than an LDS permute).
+__device__ __forceinline__ float Xor16(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+
 // Power-of-two exponent f that brings a largest magnitude amax into
 // [2^target, 2^(target+1)), so that values up to amax times 2^f stay in fp16's
 // range; the scaling itself is exact in fp32. 0 for a zero, infinite or NaN
