@@ -591,17 +591,23 @@ static bool UsesMfmaDecode(const mnb_plan *plan, int64_t M) {
 // decode scales) take DecodeFragKernel, when the caller passes its
 // workspace; the fp32-FMA kernels serve fewer. DecodeFragKernel's cost barely
 // changes with M (its pre-pass and, for long K, its partial-sum pass add a
-// fixed few us), the FMA kernel's grows by about one M = 1 pass per token.
-// Measured on MI355X (c1-c5 shapes, HIP-graph replay, us, FMA against
-// DecodeFragKernel): M = 2 c2 13.4 / 14.4, c5 gate+up 23.3 / 22.7, the others
-// 5.3-12.7 against 10.0-18.7; M = 4 c2 20.2 / 13.6, gate+up 32.5 / 22.3, c1
-// 7.3 / 10.3, c5 qkv 10.9 / 11.8, c3 18.2 / 18.4; from M = 5 it is ahead
-// of both the FMA and the original-layout MFMA kernel everywhere except c5
-// qkv (5-7% behind the latter).
+// fixed few us), the FMA kernel's grows by about one M = 1 pass per token, so
+// the larger the weights the earlier the crossover. Measured on MI355X
+// (HIP-graph replay, us, FMA against DecodeFragKernel with both terms of up
+// to 8 tokens in one operand): M = 2 c1 5.3 / 8.7, c3 12.8 / 14.3, c5 qkv
+// 7.4 / 9.9, o 5.3 / 8.7, down 11.0 / 13.0; M = 3 c1 6.4 / 8.9, c3 15.9 /
+// 14.8, qkv 9.1 / 10.0, o 6.4 / 8.7, down 14.4 / 13.3; M = 4 c1 7.2 / 8.9,
+// c3 18.4 / 14.7, qkv 10.6 / 9.9, o 7.2 / 8.8, down 17.0 / 13.3. Wide
+// weights (N >= 3K) take the fragment-ordered GEMV up to 4 rows when their
+// groups cover the CUs; the thresholds by N / K serve the others (before the
+// one-operand split: M = 2 c2 13.4 / 14.4, c5 gate+up 23.3 / 22.7; M = 4 c2
+// 20.2 / 13.6, gate+up 32.5 / 22.3).
 static int64_t FragDecodeMinRows(const mnb::WeightView &w) {
+  const int64_t kn = w.K * w.N;
   if (w.N >= 6 * w.K) return 2;
-  if (w.N >= 3 * w.K) return 3;
-  return 5;
+  if (w.N >= 3 * w.K || kn >= (int64_t{48} << 20)) return 3;  // c3, c5 down: 58.7 M
+  if (kn >= (int64_t{20} << 20)) return 4;                     // c5 qkv: 25.2 M
+  return 5;                                                    // c1, c5 o: 16.8 M
 }
 
 static bool UsesFragDecode(const mnb_plan *plan, int64_t M) {

@@ -43,6 +43,11 @@
 //      end the tile is multiplied by the rows' fp32 block scales into the
 //      unit's sum, at each unit's end the unit's sum is scaled by 2^-e
 //      (exact) into the wavefront's sum.
+//    - Up to 8 tokens (TOKS = 8) the two terms of token t are rows 2 t and
+//      2 t + 1 of one A operand: a step reads 1 KiB of operands instead of
+//      2 (the operand loads bound the kernel at 16 tokens) and issues 4
+//      MFMAs; the two terms' rows are added at each block's end. c2 M = 5 /
+//      8 14.0 / 14.1 -> 11.5 / 11.6 us, c3 17.6 / 17.9 -> 14.4 / 15.0.
 //    - The wavefronts' sums meet in LDS and are added in wavefront order;
 //      a run that does not cover K writes a partial sum, added in run order
 //      by the ordered partial-sum pass. Results do not depend on scheduling.
@@ -73,7 +78,12 @@ constexpr int kUnitSteps = kUnitK / 32;
 constexpr int kTok = 16;               // tokens per MFMA tile (M padded)
 constexpr int kMaxWaves = 8;
 constexpr int kTerms = 2;              // fp16 terms per activation
-constexpr int kStepBytes = kTerms * 1024;  // image bytes per 32-k step
+constexpr int kStepBytes = kTerms * 1024;  // image bytes per 32-k step (16 tokens)
+// Up to 8 tokens: the two terms of each token are rows 2 t and 2 t + 1 of
+// one MFMA A operand, so a step's image is 1 KiB and one MFMA per slice
+// multiplies both terms.
+template <int TOKS>
+constexpr int StepBytesT() { return TOKS == 16 ? kStepBytes : 1024; }
 constexpr int kMaxSqUnits = 64;            // RMSNorm input: K <= 64 units (16384)
 
 __device__ __forceinline__ uint32_t PkAddF16(uint32_t a, uint32_t b) {
@@ -110,20 +120,23 @@ __device__ __forceinline__ half8 DecodeQ(uint32_t w, uint32_t neg_lo, uint32_t n
 // + 7 of token t = 2 pair + (lane >> 5), so each token's unit spans 32 lanes
 // and its largest magnitude is a 5-step butterfly within them. Writes
 // img[((u * 8 + ch / 4) * kTerms + term) * 64 + 16 (ch % 4) + t] and
-// exps[u * 16 + t]. (One 128-thread workgroup per unit, each thread taking 32
-// values, kept 16 workgroups busy for about 4 us at M = 16.)
+// exps[u * 16 + t]; with TOKS = 8 (M <= 8) TOKS / 2 workgroups per unit and
+// img[(u * 8 + ch / 4) * 64 + 16 (ch % 4) + 2 t + term]. (One 128-thread
+// workgroup per unit, each thread taking 32 values, kept 16 workgroups busy
+// for about 4 us at M = 16.)
 // RMS (RMSNorm fused into the input): the values split are a * gamma, and
 // sq[u * 16 + t] receives the token's sum of a^2 over the unit (a fixed
 // butterfly), from which the main kernel forms 1 / rms.
-template <bool RMS>
+template <bool RMS, int TOKS>
 __global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A,
                                                      uint4 *__restrict__ img,
                                                      int *__restrict__ exps,
                                                      float *__restrict__ sq,
                                                      const float *__restrict__ gamma, int M,
                                                      int K) {
-  const int u = static_cast<int>(blockIdx.x) >> 3;
-  const int t = (static_cast<int>(blockIdx.x) & 7) * 2 + static_cast<int>(threadIdx.x >> 5);
+  constexpr int kPairs = TOKS / 2;  // workgroups per unit
+  const int u = static_cast<int>(blockIdx.x) / kPairs;
+  const int t = (static_cast<int>(blockIdx.x) % kPairs) * 2 + static_cast<int>(threadIdx.x >> 5);
   const int ch = threadIdx.x & 31;
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, M * K * 4, 0x00020000);
@@ -161,9 +174,14 @@ __global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A
     h[1][o] = static_cast<_Float16>(__builtin_isfinite(x) ? x - static_cast<float>(h0) : 0.f);
   }
 #pragma unroll
-  for (int term = 0; term < kTerms; ++term)
-    img[((u * kUnitSteps + (ch >> 2)) * kTerms + term) * 64 + 16 * (ch & 3) + t] =
-        __builtin_bit_cast(uint4, h[term]);
+  for (int term = 0; term < kTerms; ++term) {
+    if constexpr (TOKS == 16)
+      img[((u * kUnitSteps + (ch >> 2)) * kTerms + term) * 64 + 16 * (ch & 3) + t] =
+          __builtin_bit_cast(uint4, h[term]);
+    else  // lane 16 quarter + 2 t + term of the step's one operand
+      img[(u * kUnitSteps + (ch >> 2)) * 64 + 16 * (ch & 3) + 2 * t + term] =
+          __builtin_bit_cast(uint4, h[term]);
+  }
 }
 
 // Group g of 64 weight rows, run `seg` of WPG * U units. SPB = 32-k steps
@@ -171,7 +189,7 @@ __global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A
 // RMS: the image holds A * gamma; every run scales its sums by each token's
 // 1 / rms = 1 / sqrt(sum_k A^2 / K + eps), from SplitActKernel's per-unit
 // sums of squares added in unit order.
-template <bool HAS_ZP, int SPB, int U, int WIN, bool RMS>
+template <bool HAS_ZP, int SPB, int U, int WIN, bool RMS, int TOKS>
 __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
     const uint8_t *__restrict__ Bp, const float *__restrict__ Sd, const uint32_t *__restrict__ Zd,
     const uint4 *__restrict__ img, const int *__restrict__ exps, float *__restrict__ Y,
@@ -182,6 +200,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
   __shared__ float rinv[kTok];                // RMS: each token's 1 / rms
   __shared__ float sqs[RMS ? kMaxSqUnits * kTok : 1];  // RMS: the per-unit sums of squares
   constexpr int kSteps = U * kUnitSteps;
+  constexpr int kSB = StepBytesT<TOKS>();
+  constexpr int kTPL = TOKS / 4;     // tokens per lane in the MFMA result
+  constexpr int kItems = 4 * kTPL;   // (slice, token) results per lane
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int c = lane & 15, qd = lane >> 4;
@@ -195,7 +216,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(Bp + static_cast<size_t>(g) * T * 1024), 0, T * 1024, 0x00020000);
   const __amdgpu_buffer_rsrc_t ri =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4 *>(img), 0, T * kStepBytes, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4 *>(img), 0, T * kSB, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float *>(Sd + static_cast<size_t>(g) * nb * 64), 0, nb * 256, 0x00020000);
   const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
@@ -216,14 +237,21 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
     }
   }
 
-  // Each unit's token exponents: lane quarter qd holds tokens 4 qd .. 4 qd + 3.
+  // Each unit's token exponents: lane quarter qd holds tokens kTPL qd ..
+  // kTPL qd + kTPL - 1.
   int4 ue[U];
+  const __amdgpu_buffer_rsrc_t re = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int *>(exps), 0, (T / kUnitSteps) * 64, 0x00020000);
 #pragma unroll
-  for (int uu = 0; uu < U; ++uu)
-    ue[uu] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(
-                                          __builtin_amdgcn_make_buffer_rsrc(const_cast<int *>(exps), 0,
-                                                                            (T / kUnitSteps) * 64, 0x00020000),
-                                          (u0 + uu) * 64 + 16 * qd, 0, 0));
+  for (int uu = 0; uu < U; ++uu) {
+    if constexpr (TOKS == 16) {
+      ue[uu] = __builtin_bit_cast(int4, __builtin_amdgcn_raw_buffer_load_b128(re, (u0 + uu) * 64 + 16 * qd, 0, 0));
+    } else {
+      typedef int i32x2 __attribute__((ext_vector_type(2)));
+      const i32x2 e2 = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(re, (u0 + uu) * 64 + 8 * qd, 0, 0));
+      ue[uu] = int4{e2[0], e2[1], 0, 0};
+    }
+  }
 
   struct Slot {
     u32x4 w, a0, a1;
@@ -236,8 +264,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
     const int s = s0 + i;
     sl.w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, s * 1024 + 16 * lane, 0,
                                                                            kNonTemporal));
-    sl.a0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ri, s * kStepBytes + 16 * lane, 0, 0));
-    sl.a1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ri, s * kStepBytes + 1024 + 16 * lane, 0, 0));
+    sl.a0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ri, s * kSB + 16 * lane, 0, 0));
+    if constexpr (TOKS == 16)
+      sl.a1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ri, s * kSB + 1024 + 16 * lane, 0, 0));
     if (i % SPB == 0) {
       const int blk = (s * 32) >> log2_bs;
       sl.s = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, blk * 256 + 16 * c, 0, 0));
@@ -287,16 +316,21 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) q[j] = DecodeQ(sl.w[j], neg_lo[j], neg_hi[j], mk);
     const half8 a0 = __builtin_bit_cast(half8, sl.a0);
-    const half8 a1 = __builtin_bit_cast(half8, sl.a1);
 #pragma unroll
     for (int j = 0; j < 4; ++j) tmp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, q[j], tmp[j], 0, 0, 0);
+    if constexpr (TOKS == 16) {
+      const half8 a1 = __builtin_bit_cast(half8, sl.a1);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) tmp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, q[j], tmp[j], 0, 0, 0);
+      for (int j = 0; j < 4; ++j) tmp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, q[j], tmp[j], 0, 0, 0);
+    }
     if ((i + 1) % SPB == 0) {
+      // TOKS = 8: result rows 4 qd + v hold term v & 1 of token 2 qd + v / 2
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) racc[j][v] = fmaf(bsc[j], tmp[j][v], racc[j][v]);
+        for (int v = 0; v < kTPL; ++v)
+          racc[j][v] = fmaf(bsc[j], TOKS == 16 ? tmp[j][v] : tmp[j][2 * v] + tmp[j][2 * v + 1],
+                            racc[j][v]);
     }
     if ((i + 1) % kUnitSteps == 0) {
       const int4 e4 = ue[i / kUnitSteps];
@@ -304,7 +338,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[j][v] += __builtin_amdgcn_ldexpf(racc[j][v], -ev[v]);
+        for (int v = 0; v < kTPL; ++v) acc[j][v] += __builtin_amdgcn_ldexpf(racc[j][v], -ev[v]);
     }
   };
   // Straight-line code (no loop, no branch around a load) keeps the
@@ -323,7 +357,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) red[(wave * 16 + j * 4 + v) * 64 + lane] = acc[j][v];
+    for (int v = 0; v < kTPL; ++v) red[(wave * kItems + j * kTPL + v) * 64 + lane] = acc[j][v];
   if constexpr (RMS) {
     if (wave == 0) {
       // the copies have landed (vmcnt counts them), then lane t adds token
@@ -341,12 +375,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
   float *out = seg == 0 ? Y : partials + static_cast<size_t>(seg - 1) * M * N;
   const int y_end = M * N * 4;
   const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(out, 0, y_end, 0x00020000);
-  for (int x = wave; x < 16; x += wpg) {
+  for (int x = wave; x < kItems; x += wpg) {
     float sum = red[x * 64 + lane];
-    for (int w = 1; w < wpg; ++w) sum += red[(w * 16 + x) * 64 + lane];
-    const int j = x >> 2, v = x & 3;
+    for (int w = 1; w < wpg; ++w) sum += red[(w * kItems + x) * 64 + lane];
+    const int j = x / kTPL, v = x % kTPL;
     const int n = 64 * g + 16 * j + c;
-    const int tok = 4 * qd + v;
+    const int tok = kTPL * qd + v;
     if constexpr (RMS) sum *= rinv[tok];
     if (H != nullptr) {
       // gate/up pairs (rows 2 n', 2 n' + 1 in lanes c, c ^ 1; N even)
@@ -439,7 +473,7 @@ struct Work {
   float eps;
 };
 
-template <bool HAS_ZP, int SPB, int U>
+template <bool HAS_ZP, int SPB, int U, int TOKS>
 hipError_t LaunchMain(const WeightView &w, int64_t M, const Work &wk, float *Y, float *H,
                       const float *bias, const Shape &sh, hipStream_t s) {
   const int64_t groups = (w.N + 63) / 64;
@@ -448,11 +482,11 @@ hipError_t LaunchMain(const WeightView &w, int64_t M, const Work &wk, float *Y, 
   const int m = static_cast<int>(M), n = static_cast<int>(w.N), k = static_cast<int>(w.K),
             nb = static_cast<int>(w.nb);
   if (wk.sq != nullptr)
-    hipLaunchKernelGGL((DecodeFragKernel<HAS_ZP, SPB, U, kWin, true>), grid, block, 0, s, w.Bp,
+    hipLaunchKernelGGL((DecodeFragKernel<HAS_ZP, SPB, U, kWin, true, TOKS>), grid, block, 0, s, w.Bp,
                        w.Sd, w.Zd, wk.img, wk.exps, Y, wk.P, H, bias, m, n, k, nb, w.log2_bs,
                        sh.segs, sh.wpg, wk.sq, wk.eps);
   else
-    hipLaunchKernelGGL((DecodeFragKernel<HAS_ZP, SPB, U, kWin, false>), grid, block, 0, s, w.Bp,
+    hipLaunchKernelGGL((DecodeFragKernel<HAS_ZP, SPB, U, kWin, false, TOKS>), grid, block, 0, s, w.Bp,
                        w.Sd, w.Zd, wk.img, wk.exps, Y, wk.P, H, bias, m, n, k, nb, w.log2_bs,
                        sh.segs, sh.wpg, nullptr, 0.0f);
   return hipGetLastError();
@@ -461,8 +495,11 @@ hipError_t LaunchMain(const WeightView &w, int64_t M, const Work &wk, float *Y, 
 template <bool HAS_ZP, int SPB>
 hipError_t LaunchU(const WeightView &w, int64_t M, const Work &wk, float *Y, float *H,
                    const float *bias, const Shape &sh, hipStream_t s) {
-  return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2>(w, M, wk, Y, H, bias, sh, s)
-                                : LaunchMain<HAS_ZP, SPB, 1>(w, M, wk, Y, H, bias, sh, s);
+  if (M <= 8)
+    return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2, 8>(w, M, wk, Y, H, bias, sh, s)
+                                  : LaunchMain<HAS_ZP, SPB, 1, 8>(w, M, wk, Y, H, bias, sh, s);
+  return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2, 16>(w, M, wk, Y, H, bias, sh, s)
+                                : LaunchMain<HAS_ZP, SPB, 1, 16>(w, M, wk, Y, H, bias, sh, s);
 }
 
 template <bool HAS_ZP>
@@ -527,12 +564,20 @@ hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, floa
   int *exps = reinterpret_cast<int *>(base + df::ImageBytes(w));
   float *sq = reinterpret_cast<float *>(base + df::ImageBytes(w) + df::ExpBytes(w));
   float *P = reinterpret_cast<float *>(base + df::ImageBytes(w) + df::ExpBytes(w) + df::SqBytes(w));
-  const dim3 sgrid(static_cast<unsigned>(units * 8)), sblock(64);
-  if (gamma != nullptr)
-    hipLaunchKernelGGL(df::SplitActKernel<true>, sgrid, sblock, 0, s, A, img, exps, sq, gamma,
+  // up to 8 rows: both terms of a token in one MFMA operand (half the image)
+  const bool t8 = M <= 8;
+  const dim3 sgrid(static_cast<unsigned>(units * (t8 ? 4 : 8))), sblock(64);
+  if (gamma != nullptr && t8)
+    hipLaunchKernelGGL((df::SplitActKernel<true, 8>), sgrid, sblock, 0, s, A, img, exps, sq, gamma,
                        static_cast<int>(M), static_cast<int>(w.K));
+  else if (gamma != nullptr)
+    hipLaunchKernelGGL((df::SplitActKernel<true, 16>), sgrid, sblock, 0, s, A, img, exps, sq, gamma,
+                       static_cast<int>(M), static_cast<int>(w.K));
+  else if (t8)
+    hipLaunchKernelGGL((df::SplitActKernel<false, 8>), sgrid, sblock, 0, s, A, img, exps, nullptr,
+                       nullptr, static_cast<int>(M), static_cast<int>(w.K));
   else
-    hipLaunchKernelGGL(df::SplitActKernel<false>, sgrid, sblock, 0, s, A, img, exps, nullptr,
+    hipLaunchKernelGGL((df::SplitActKernel<false, 16>), sgrid, sblock, 0, s, A, img, exps, nullptr,
                        nullptr, static_cast<int>(M), static_cast<int>(w.K));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

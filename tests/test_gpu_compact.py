@@ -32,8 +32,9 @@ def _weights(pkg, K, N, bs, zp, seed):
 def _plan_bytes(torch, make):
     """The plan and its device bytes (mnb_plan_device_bytes), cross-checked
     against the device's free memory before and after (allocation granularity
-    aside; a first small plan loads the library's code and static device
-    memory beforehand)."""
+    aside, and small buffers the runtime may place in memory it already holds
+    from earlier frees; a first small plan loads the library's code and
+    static device memory beforehand)."""
     import __graft_entry__
     pkg = __graft_entry__.load_package()
     warm = pkg.workloads.Projection("warm", 256, 64, 32, False)
@@ -44,7 +45,7 @@ def _plan_bytes(torch, make):
     torch.cuda.synchronize()
     seen = free0 - torch.cuda.mem_get_info()[0]
     owned = op.device_bytes()
-    assert owned <= seen + (1 << 20) and seen <= owned + (24 << 20), (owned, seen)
+    assert owned <= seen + (4 << 20) and seen <= owned + (24 << 20), (owned, seen)
     return op, owned
 
 
