@@ -114,8 +114,8 @@ int mnb_plan_destroy(mnb_plan *plan);
  * A plan created from host weights whose every path runs on the re-laid
  * copies (wide weights: N / 64 row groups covering most CUs, K % 256 == 0,
  * K <= 8192, 32 <= block_size <= 256) keeps no original layout ("compact":
- * about 1.24x the constants' bytes at block_size 128 with zero points);
- * others keep both (about 2.2x). No counterpart in the reference (whose
+ * about 1.07x the constants' bytes at block_size 128 with zero points);
+ * others keep both (about 2.07x). No counterpart in the reference (whose
  * constant B stays in host memory): for callers planning device memory. */
 int mnb_plan_device_bytes(const mnb_plan *plan, size_t *bytes);
 

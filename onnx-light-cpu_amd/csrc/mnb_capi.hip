@@ -158,7 +158,8 @@ bool CompactEligible(const mnb::WeightView &w) {
 // Plan-time constants derived from the device copies of the weights (run
 // once, synchronously, on the null stream): the per-row scale exponents and,
 // for shapes the prefill kernel serves, its fragment-ordered copy of the
-// weights with per-step scale / zero-point words (1.25x the packed B bytes).
+// weights with per-block scale / zero-point words (1.06x the packed B bytes
+// at block size 128, 1.25x at 32).
 // Fills the plan's view.
 int DerivePlanConstants(mnb_plan *p) {
   FillView(p);
@@ -212,8 +213,8 @@ int DerivePlanConstants(mnb_plan *p) {
     }
   }
   // Compact plan: where every automatic route reads only the re-laid copies,
-  // a plan that owns its weights drops the original layout (about 2.2x the
-  // weights' bytes become 1.24x at bs = 128 with zero points).
+  // a plan that owns its weights drops the original layout (about 2.07x the
+  // weights' bytes become 1.07x at bs = 128 with zero points).
   if (p->owns && CompactEligible(p->view)) {
     (void)hipFree(p->dB);
     (void)hipFree(p->dS);

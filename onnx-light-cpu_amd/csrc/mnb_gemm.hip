@@ -743,9 +743,10 @@ inline Shape PickShape(const WeightView &w, int64_t M) {
 // the 1 KiB record Bp[g][s][lane][j] holds in lane l's 16 bytes the packed
 // word (8 nibbles, original order) of weight row 64g + 16j + (l & 15) at k =
 // 32s + 8(l >> 4): exactly lane l's MFMA operand for the 16 rows of slice j.
-// The 256-byte record Sp[g][s][c][j] holds, per step, the fp16 scale (times
-// the row's 2^e) in the low half and the zero point in the high half, for
-// row 64g + 16j + c and the step's block. Rows past N are zero (scale 0).
+// The 256-byte record Sp[g][b][c][j] holds, per quantization block b, the
+// fp16 scale (times the row's 2^e) in the low half and the zero point in the
+// high half, for row 64g + 16j + c. Rows past N are zero (scale 0). One record
+// per block, not per step: every step of a block reads the same record.
 //
 // A workgroup of 8 wavefronts (two per SIMD, one workgroup per CU) computes a
 // 128 x 256 output tile. Wavefronts w and w + 4 own columns 64(w % 4) ..
@@ -804,7 +805,7 @@ template <bool HAS_ZP, bool BS32>
 __global__ __launch_bounds__(kPThreads, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 PrefillKernel(const uint4 *__restrict__ Ah, const uint8_t *__restrict__ Bp,
               const uint8_t *__restrict__ Sp, float *__restrict__ Y, int M, int N, int K,
-              int kt_per_split, float *__restrict__ partials, float *__restrict__ H,
+              int log2_bs, int kt_per_split, float *__restrict__ partials, float *__restrict__ H,
               const int *__restrict__ row_exp, const int *__restrict__ col_exp,
               const float *__restrict__ bias) {
   extern __shared__ uint4 lds[];
@@ -845,23 +846,30 @@ PrefillKernel(const uint4 *__restrict__ Ah, const uint8_t *__restrict__ Bp,
   constexpr int sg = decltype(sg_c)::value;
   // Copies per k-tile: A instruction i of wavefront w takes units
   // i * 512 + 64 w + lane; wavefront w the weight record of (g, step sg);
-  // wavefronts 0-3 the scale record of g (both steps; lanes 32-63 repeat
-  // lanes 0-31).
-  const uint4 *a_src = Ah + (static_cast<size_t>(tm) * (K / kBK) + kt0) * kPAU + wave * 64 + lane;
-  const uint8_t *b_src = Bp + (static_cast<size_t>(g) * T + 2 * kt0 + sg) * 1024 + lane * 16;
-  const uint8_t *s_src = Sp + (static_cast<size_t>(g) * T + 2 * kt0) * 256 + (lane & 31) * 16;
+  // wavefronts 0-3 the scale records of g for both steps (lanes 16-31 the
+  // second step's, lanes 32-63 repeat lanes 0-31). 32-k blocks: one record per
+  // step; larger blocks hold both steps of a 64-k tile, whose record repeats.
+  // Sources as a wave-uniform base (SGPRs) plus the lane's byte offset.
+  const int nb = (K + (1 << log2_bs) - 1) >> log2_bs;
+  const uint4 *a_base = Ah + (static_cast<size_t>(tm) * (K / kBK) + kt0) * kPAU + wave * 64;
+  const uint8_t *b_base = Bp + (static_cast<size_t>(g) * T + 2 * kt0 + sg) * 1024;
+  const uint8_t *s_base = Sp + static_cast<size_t>(g) * nb * 256;
+  const uint32_t a_off = static_cast<uint32_t>(lane) * 16;
+  const uint32_t s_off = static_cast<uint32_t>(lane & (BS32 ? 31 : 15)) * 16;
+  const int bt_shift = BS32 ? 0 : log2_bs - 6;  // 64-k tiles per block, log2
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
   auto issue = [&](int kt, int st) {
     const uint32_t base = lds0 + static_cast<uint32_t>(st * kPStage * 16);
 #pragma unroll
     for (int i = 0; i < kPAU / kPThreads; ++i)
-      CopyToLds16(a_src + static_cast<size_t>(kt) * kPAU + i * kPThreads,
-                  base + static_cast<uint32_t>((i * kPThreads + wave * 64) * 16));
-    CopyToLds16(b_src + static_cast<size_t>(kt) * 2048,
-                base + static_cast<uint32_t>((kPAU + cg * kPBU + sg * 64) * 16));
+      CopyToLds16S(a_base + static_cast<size_t>(kt) * kPAU + i * kPThreads, a_off,
+                   base + static_cast<uint32_t>((i * kPThreads + wave * 64) * 16));
+    CopyToLds16S(b_base + static_cast<size_t>(kt) * 2048, a_off,
+                 base + static_cast<uint32_t>((kPAU + cg * kPBU + sg * 64) * 16));
     if constexpr (sg == 0)
-      CopyToLds16(s_src + static_cast<size_t>(kt) * 512,
-                  base + static_cast<uint32_t>((kPAU + 4 * kPBU + cg * kPSU) * 16));
+      CopyToLds16S(s_base + (BS32 ? static_cast<size_t>(2 * (kt0 + kt)) * 256
+                                  : static_cast<size_t>((kt0 + kt) >> bt_shift) * 256),
+                   s_off, base + static_cast<uint32_t>((kPAU + 4 * kPBU + cg * kPSU) * 16));
   };
   // Tile t + 1 has landed once only the copies of tiles t + 2 .. t + kPSA - 1
   // (issued at the tops of the iterations since) are outstanding.
@@ -1084,7 +1092,7 @@ __global__ __launch_bounds__(512) void StreamKernel(
     const uint4 *__restrict__ Ah, const float *__restrict__ A, const uint8_t *__restrict__ Bp,
     const uint8_t *__restrict__ Sp, float *__restrict__ Y, float *__restrict__ partials,
     float *__restrict__ H, const int *__restrict__ row_exp, const int *__restrict__ col_exp,
-    const float *__restrict__ bias, int M, int N, int K, int segs, int wpg) {
+    const float *__restrict__ bias, int M, int N, int K, int log2_bs, int segs, int wpg) {
   extern __shared__ floatx4 sred[];  // [wave][tg * 4 + j][lane]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -1094,8 +1102,10 @@ __global__ __launch_bounds__(512) void StreamKernel(
   const int s0 = (seg * wpg + wave) * SPW;  // first step of this wavefront
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(Bp + static_cast<size_t>(g) * T * 1024), 0, T * 1024, 0x00020000);
+  const int nb = (K + (1 << log2_bs) - 1) >> log2_bs;
+  const int sb_shift = log2_bs - 5;  // 32-k steps per block, log2
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t *>(Sp + static_cast<size_t>(g) * T * 256), 0, T * 256, 0x00020000);
+      const_cast<uint8_t *>(Sp + static_cast<size_t>(g) * nb * 256), 0, nb * 256, 0x00020000);
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint4 *>(Ah), 0, (K / kBK) * AUnits<kSGroupRows>() * 16, 0x00020000);
   // Lane l's activation fragment tg of step s: row 16 tg + (l & 15), unit
@@ -1135,7 +1145,8 @@ __global__ __launch_bounds__(512) void StreamKernel(
     Slot &sl = ring[i % WIN];
     const int s = s0 + i;
     sl.w = __builtin_bit_cast(u32x4e, __builtin_amdgcn_raw_buffer_load_b128(rb, s * 1024 + 16 * lane, 0, 2));
-    sl.sz = __builtin_bit_cast(u32x4e, __builtin_amdgcn_raw_buffer_load_b128(rs, s * 256 + 16 * (lane & 15), 0, 0));
+    sl.sz = __builtin_bit_cast(u32x4e, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rs, (s >> sb_shift) * 256 + 16 * (lane & 15), 0, 0));
     if constexpr (!CVT) {
       const int kt = s >> 1;
 #pragma unroll
@@ -1334,12 +1345,12 @@ hipError_t LaunchStreamT(const WeightView &w, int64_t M, const uint4 *Ah, const 
   if (A != nullptr) {
     if constexpr (TG * SPW <= 16)
       hipLaunchKernelGGL((StreamKernel<HAS_ZP, TG, SPW, 4, true>), grid, block, lds, s, Ah, A, w.Bp,
-                         w.Sp, Y, P, H, row_exp, w.col_exp, bias, m, n, k, sh.segs, sh.wpg);
+                         w.Sp, Y, P, H, row_exp, w.col_exp, bias, m, n, k, w.log2_bs, sh.segs, sh.wpg);
     else
       return hipErrorInvalidValue;
   } else {
     hipLaunchKernelGGL((StreamKernel<HAS_ZP, TG, SPW, 4, false>), grid, block, lds, s, Ah, A, w.Bp,
-                       w.Sp, Y, P, H, row_exp, w.col_exp, bias, m, n, k, sh.segs, sh.wpg);
+                       w.Sp, Y, P, H, row_exp, w.col_exp, bias, m, n, k, w.log2_bs, sh.segs, sh.wpg);
   }
   return hipGetLastError();
 }
@@ -1390,7 +1401,7 @@ hipError_t LaunchPrefillT(const WeightView &w, int64_t M, const uint4 *Ah, float
   const int tiles = static_cast<int>((M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN));
   hipLaunchKernelGGL((PrefillKernel<HAS_ZP, BS32>), dim3(tiles * splits), dim3(kPThreads), kPLds, s, Ah,
                      w.Bp, w.Sp, Y, static_cast<int>(M), static_cast<int>(w.N),
-                     static_cast<int>(w.K), per, partials, H, row_exp, w.col_exp, bias);
+                     static_cast<int>(w.K), w.log2_bs, per, partials, H, row_exp, w.col_exp, bias);
   return hipGetLastError();
 }
 
@@ -1415,15 +1426,14 @@ __global__ __launch_bounds__(256) void RelayoutSKernel(const float *__restrict__
                                                        const int32_t *__restrict__ col_exp,
                                                        uint32_t *__restrict__ Sp, int64_t N,
                                                        int64_t nb, int64_t zp_row_bytes,
-                                                       int log2_bs, int64_t T, int64_t words) {
+                                                       int64_t words) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= words) return;
   const int j = static_cast<int>(idx & 3);
   const int c = static_cast<int>((idx >> 2) & 15);
-  const int64_t gs = idx >> 6;
-  const int64_t s = gs % T, g = gs / T;
+  const int64_t gb = idx >> 6;
+  const int64_t b = gb % nb, g = gb / nb;
   const int64_t n = 64 * g + 16 * j + c;
-  const int64_t b = (32 * s) >> log2_bs;
   uint32_t v = 8u << 16;  // rows past N: scale 0
   if (n < N) {
     const _Float16 h = static_cast<_Float16>(__builtin_amdgcn_ldexpf(S[n * nb + b], col_exp[n]));
@@ -1542,7 +1552,7 @@ bool PrefillSupports(const WeightView &w, int64_t M) { return PrefillSupportsM(w
 size_t PrefillLayoutBytes(const WeightView &w, size_t *sp_bytes) {
   const int64_t groups = (w.N + kPTN - 1) / kPTN * (kPTN / 64);
   const int64_t steps = w.K / 32;
-  if (sp_bytes != nullptr) *sp_bytes = static_cast<size_t>(groups * steps * 256);
+  if (sp_bytes != nullptr) *sp_bytes = static_cast<size_t>(groups * w.nb * 256);
   return static_cast<size_t>(groups * steps * 1024);
 }
 
@@ -1563,7 +1573,7 @@ hipError_t LaunchPrefillRelayout(const WeightView &w, uint8_t *Bp, uint8_t *Sp, 
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(RelayoutSKernel, dim3(static_cast<unsigned>((sw + 255) / 256)), dim3(256), 0,
                      s, w.scales, w.zp, w.col_exp, reinterpret_cast<uint32_t *>(Sp), w.N, w.nb,
-                     w.zp_row_bytes, w.log2_bs, T, sw);
+                     w.zp_row_bytes, sw);
   return hipGetLastError();
 }
 

@@ -30,6 +30,15 @@ __device__ __forceinline__ void CopyToLds16(const void *gsrc, uint32_t lds_base)
                    : "s"(lds_base), "v"(gsrc)
                    : "memory", "m0");
 }
+// The same copy from sbase + voff: a wave-uniform 64-bit base in SGPRs and a
+// per-lane 32-bit byte offset, so the address costs no 64-bit VGPR pair and
+// no vector arithmetic per copy.
+__device__ __forceinline__ void CopyToLds16S(const void *sbase, uint32_t voff, uint32_t lds_base) {
+  __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :
+                   : "s"(lds_base), "v"(voff), "s"(sbase)
+                   : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Gated-MLP activation of one gate/up pair, in the order of the ONNX subgraph
@@ -91,7 +100,7 @@ struct WeightView {
   const uint8_t *zp;      // [N, zp_row_bytes] packed nibbles, or nullptr (zp = 8 or compact)
   const int32_t *col_exp; // [N] RangeExponent(max_b |scales[n][b]|, kScaleExpTarget)
   const uint8_t *Bp;      // the prefill kernel's fragment-ordered weights, or nullptr
-  const uint8_t *Sp;      // its per-step scale / zero-point words, or nullptr
+  const uint8_t *Sp;      // its per-block scale / zero-point words, or nullptr
   const float *Sd;        // DecodeFragKernel's block scales per 64-row group, or nullptr
   const uint32_t *Zd;     // its zero points per 64-row group, or nullptr
   int64_t K;

@@ -3,8 +3,9 @@
 A plan created from host weights whose every automatic route runs on the
 fragment-ordered copy (wide weights: the M <= 4 GEMV's 64-row groups cover
 most CUs) frees the original layout after deriving the copies. Checked here:
-- its device memory is at most 1.3x the operator's constant bytes (B,
-  scales, zero points), against about 2.2x when both layouts are kept;
+- its device memory is at most 1.15x the operator's constant bytes (B,
+  scales, zero points; about 1.07x at block size 128 with zero points, 1.11x
+  at 64 without), against about 2.1x when both layouts are kept;
 - every path still serves every M at its bound against the fp64 oracle:
   the decode path with the small-M kernel's workspace and without it (the
   fragment-ordered GEMV over groups of up to 4 rows), the exact route, the
@@ -57,7 +58,7 @@ def test_compact_plan_memory_and_every_path(pkg, orc, cuda, K, N, bs, zp):
     wbytes = pkg.weight_bytes(K, N, bs, zp)
     print(f"case compact K={K} N={N} bs={bs} zp={zp}: plan {used} B for {wbytes} B of weights "
           f"({used / wbytes:.2f}x)", flush=True)
-    assert used <= 1.3 * wbytes
+    assert used <= 1.15 * wbytes
     L = pkg.library()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())
@@ -140,7 +141,7 @@ def test_compact_gate_up_plan(pkg, orc, cuda):
     wbytes = 2 * pkg.weight_bytes(K, I, bs, True)
     print(f"case compact gate/up K={K} I={I}: plan {used} B for {wbytes} B ({used / wbytes:.2f}x)",
           flush=True)
-    assert used <= 1.3 * wbytes
+    assert used <= 1.15 * wbytes
     try:
         for M in (1, 4, 7, 40):
             A = pkg.workloads.make_activations(M, K, 1.0, seed=M + 20)
