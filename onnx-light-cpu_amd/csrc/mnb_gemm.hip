@@ -782,7 +782,10 @@ constexpr int kPOps0 = kPAU / kPThreads + 2;          // copies per k-tile, wave
 constexpr int kPOps1 = kPAU / kPThreads + 1;          // wavefronts 4-7 (no scale copy)
 // Cache policy of the output stores: non-temporal. Y is not read again by
 // this kernel; streaming it out keeps the L2 for the operand tiles (measured:
-// c5 gate+up M = 2048, 224 MiB of Y, 472 -> 445 us; c4 unchanged).
+// c5 gate+up M = 2048, 224 MiB of Y, 472 -> 445 us; c4 unchanged). With K
+// split, the split reduction reads Y and the partial sums straight back, and
+// plain stores serve it better (c4 and c5 o at M = 512, 4 splits: 37.1 ->
+// 35.4 and 38.0 -> 36.3 us per call; qkv at M = 256 33.2 -> 32.2).
 constexpr int kStoreNT = 2;
 
 // (scale fp16 | zp << 16) -> the operands of DequantWord.
@@ -1045,7 +1048,10 @@ PrefillKernel(const uint4 *__restrict__ Ah, const uint8_t *__restrict__ Bp,
                          __float_as_uint(__builtin_amdgcn_ldexpf(x3, -(er[q] + e3)) + b3)};
         const int row = (4 * S + q) * 16 + (lane & 15);
         const int off = n < N ? (row * N + n) * 4 : 0x7FFFFFF0;
-        __builtin_amdgcn_raw_buffer_store_b128(v, yr, off, 0, kStoreNT);
+        if (kt_per_split < K / kBK)  // split K: read back by the reduction
+          __builtin_amdgcn_raw_buffer_store_b128(v, yr, off, 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b128(v, yr, off, 0, kStoreNT);
       }
     }
   }
