@@ -31,6 +31,8 @@ def _prepare(pkg, K, N, bs, zp, seed):
     (8192, 256, 256, True, 17),      # one column tile, 16 splits, M below one tile
     (4096, 4096, 128, True, 512),    # 64 tiles, 4 splits
     (1024, 2048, 1024, False, 1000), # block size 1024, 8 x 8 tiles, 2 splits
+    (1344, 512, 128, True, 200),     # ragged last block (64 of 128 k): one scale record per block
+    (2560, 768, 1024, True, 150),    # ragged last block (512 of 1024 k), 16 k-tiles per block
 ])
 def test_prefill_kernel_forced(pkg, orc, cuda, K, N, bs, zp, M):
     import torch

@@ -33,6 +33,7 @@ def _weights(pkg, K, N, bs, zp, seed):
     (2048, 512, 256, False, 40, 4, 4),     # 4 segments, blocks spanning several steps
     (14336, 256, 32, True, 24, 7, 8),      # long K, 7 segments
     (2048, 512, 64, True, 32, 4, 4),       # 4 wavefronts per workgroup (the fewest served)
+    (2560, 512, 1024, True, 40, 5, 4),     # ragged last block (512 of 1024 k), 5 segments
 ])
 def test_stream_kernel_parity(pkg, orc, cuda, K, N, bs, zp, M, segs, spw):
     import torch
