@@ -9,7 +9,9 @@ do not take). A seeded sweep over shapes no parametrized test names checks
 that every choice stays within its path's bound: max|y - y64| / max|y64| <=
 1e-5 on the decode, exact and generic paths (fp32 accumulation), ||Y - Y64||
 / ||Y64|| <= 2e-3 on the fp16 GEMM paths. Every case prints its shape, path
-and kernel before touching the GPU.
+and kernel before touching the GPU. The same generator drives the GEMM and
+generic paths forced on other shapes, and RMSNorm fused into the input
+(K % 4 == 0, which the fused entry point requires).
 """
 import numpy as np
 import pytest
@@ -65,3 +67,63 @@ def test_random_shape_auto_path(pkg, orc, cuda, K, N, bs, zp, M, seed):
         err = orc.normwise_max_error(Y, y64)
         print(f"  normwise error vs fp64 {err:.2e}")
         assert err <= GEMV_TOL
+
+
+@pytest.mark.parametrize("K,N,bs,zp,M,seed", _cases(24, 20261203))
+def test_random_shape_forced_paths(pkg, orc, cuda, K, N, bs, zp, M, seed):
+    """The GEMM path (fp16 MFMA) and the generic path (one wavefront per
+    output, fp32) forced on the same seeded shapes, each at its bound; a path
+    that does not take the shape reports it (MNB_ERR_UNSUPPORTED)."""
+    import torch
+    p = pkg.workloads.Projection("rand", K, N, bs, zp, 1.0, 0.005, 0.02)
+    B, S, Z = pkg.workloads.make_weights(p, seed)
+    A = pkg.workloads.make_activations(M, K, 1.0, seed + 1)
+    y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    try:
+        dA = torch.from_numpy(A).to(cuda)
+        for path, tol, metric in ((pkg.PATH_GEMM, GEMM_TOL, orc.l2_rel_error),
+                                  (pkg.PATH_GENERIC, GEMV_TOL, orc.normwise_max_error)):
+            print(f"case random forced K={K} N={N} bs={bs} zp={zp} M={M} path={path}", flush=True)
+            try:
+                Y = op(dA, path=path).cpu().numpy()
+            except pkg.MatMulNBitsError as e:
+                assert "unsupported" in str(e), e
+                continue
+            err = metric(Y, y64)
+            print(f"  error vs fp64 {err:.2e}")
+            assert err <= tol
+    finally:
+        op.release()
+
+
+@pytest.mark.parametrize("K,N,bs,zp,M,seed", [c for c in _cases(40, 20261204) if c[0] % 4 == 0][:24])
+def test_random_shape_rmsnorm(pkg, orc, cuda, K, N, bs, zp, M, seed):
+    """RMSNorm fused into the projection input on seeded shapes, against the
+    fp64 RMSNormalization followed by the fp64 product, at the bound of the
+    path the plan takes for M rows."""
+    import torch
+    p = pkg.workloads.Projection("rand", K, N, bs, zp, 1.0, 0.005, 0.02)
+    B, S, Z = pkg.workloads.make_weights(p, seed)
+    X = pkg.workloads.make_activations(M, K, 1.0, seed + 1)
+    gamma = np.random.default_rng(seed + 2).uniform(0.5, 1.5, K).astype(np.float32)
+    Xn = orc.rmsnorm_f64(X.astype(np.float64), gamma.astype(np.float64), 1e-5)
+    y64 = orc.matmul_nbits_f64(Xn.astype(np.float32), B, S, Z, K, N, bs)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    try:
+        path = op.select_path(M)
+        print(f"case random rmsnorm K={K} N={N} bs={bs} zp={zp} M={M} path={path}", flush=True)
+        Y = op.run_rmsnorm(torch.from_numpy(X).to(cuda), torch.from_numpy(gamma).to(cuda),
+                           1e-5).cpu().numpy()
+    finally:
+        op.release()
+    # decode bound: the 1e-5 of the product plus the fp32 rounding of the
+    # normalized input (as in the RMSNorm parity tests)
+    if path in (pkg.PATH_GEMM, pkg.PATH_PREFILL):
+        err = orc.l2_rel_error(Y, y64)
+        print(f"  l2 error vs fp64 {err:.2e}")
+        assert err <= GEMM_TOL
+    else:
+        err = orc.normwise_max_error(Y, y64)
+        print(f"  normwise error vs fp64 {err:.2e}")
+        assert err <= 2 * GEMV_TOL
