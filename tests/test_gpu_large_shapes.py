@@ -1,0 +1,53 @@
+"""GPU: parity at the largest shapes the configurations reach.
+
+Llama-3-8B's LM head (K = 4096, N = 128256: 2004 row groups, 282 MB of
+constants) at decode and prefill row counts, and a long K (65536, 256 units
+per row) on narrow weights. Output column n of MatMulNBits depends only on
+weight row n, so each case checks a seeded sample of columns against the
+fp64 oracle run on the same rows of B, scales and zero points, at the bound
+of the path that serves the row count. Every case prints its shape and
+kernel before touching the GPU.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL, GEMM_TOL = 1e-5, 2e-3
+
+
+def _check_sampled(pkg, orc, cuda, K, N, bs, zp, Ms, seed, ncols=512):
+    import torch
+    p = pkg.workloads.Projection("large", K, N, bs, zp, 1.0, 0.005, 0.02)
+    B, S, Z = pkg.workloads.make_weights(p, seed)
+    cols = np.sort(np.random.default_rng(seed).choice(N, size=min(ncols, N), replace=False))
+    Bc, Sc = B[cols], S[cols]
+    Zc = Z[cols] if Z is not None else None
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    try:
+        for M in Ms:
+            A = pkg.workloads.make_activations(M, K, 1.0, seed + M)
+            path = op.select_path(M)
+            print(f"case large K={K} N={N} bs={bs} zp={zp} M={M} path={path} "
+                  f"kernel={op.kernel_name(M)}", flush=True)
+            Y = op(torch.from_numpy(A).to(cuda)).cpu().numpy()
+            assert Y.shape == (M, N) and np.isfinite(Y).all()
+            y64 = orc.matmul_nbits_f64(A, Bc, Sc, Zc, K, len(cols), bs)
+            if path in (pkg.PATH_GEMM, pkg.PATH_PREFILL):
+                err = orc.l2_rel_error(Y[:, cols], y64)
+                print(f"  l2 error vs fp64 over {len(cols)} columns {err:.2e}")
+                assert err <= GEMM_TOL
+            else:
+                err = orc.normwise_max_error(Y[:, cols], y64)
+                print(f"  normwise error vs fp64 over {len(cols)} columns {err:.2e}")
+                assert err <= GEMV_TOL
+    finally:
+        op.release()
+
+
+def test_lm_head_shape(pkg, orc, cuda):
+    _check_sampled(pkg, orc, cuda, 4096, 128256, 128, True, (1, 3, 16, 130), seed=8128)
+
+
+def test_long_k_narrow_weights(pkg, orc, cuda):
+    _check_sampled(pkg, orc, cuda, 65536, 320, 64, True, (1, 2, 8, 40, 100), seed=6553)
