@@ -131,6 +131,9 @@ int mnb_plan_device_bytes(const mnb_plan *plan, size_t *bytes);
  *    exact route serves larger M 16 rows at a time), its split activation
  *    image and fp32 partial sums (none where the fragment-ordered M <= 4
  *    GEMV serves them);
+ *  - for 1 or 2 rows too long for one workgroup per 64-row group (K > 16384
+ *    at M = 1, K > 8192 at M = 2; plain plans), the fragment-ordered GEMV
+ *    with K split into S segments: (S - 1)*M*N*4 bytes of partial sums;
  *  - on a gate/up plan, plus the M x 2N fp32 scratch sum.
  * Without it (NULL or smaller) the decode path runs its fp32-FMA kernels. */
 int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);

@@ -615,11 +615,22 @@ static bool UsesFragDecode(const mnb_plan *plan, int64_t M) {
   return M >= FragDecodeMinRows(plan->view) && mnb::DecodeFragSupports(plan->view, M);
 }
 
+// The K-segmented fragment-ordered GEMV (1 or 2 rows too long for one
+// workgroup): plain plans (its sums pass has no gate/up pairing), no RMSNorm
+// input (a segment sees only its part of each row's sum of squares).
+static bool UsesFragSegments(const mnb_plan *plan, int64_t M, bool rms) {
+  return !rms && !plan->gate_up && mnb::GemvFragSegSupports(plan->view, M);
+}
+
 // The decode kernel path 1 launches for M rows with `work_bytes` of workspace
 // at `work` (M <= 16).
 // kDecFragGroups: a compact plan without the small-M kernel's workspace runs
 // the fragment-ordered GEMV on consecutive groups of up to 4 rows.
-enum DecodeKernel { kDecM1, kDecGemvFrag, kDecFrag, kDecMfma, kDecSmallM, kDecGemv, kDecFragGroups };
+// kDecGemvFragSeg: the fragment-ordered GEMV with K split into segments, for
+// 1 or 2 rows too long for one workgroup (and for GemvM1Kernel).
+enum DecodeKernel {
+  kDecM1, kDecGemvFrag, kDecFrag, kDecMfma, kDecSmallM, kDecGemv, kDecFragGroups, kDecGemvFragSeg
+};
 
 // Rows per launch of the exact route (path 4): the decode kernels' limit.
 constexpr int64_t kExactGroupRows = 16;
@@ -632,7 +643,9 @@ static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
 // Without the kernel's workspace, M >= 2 falls back to the fp32-FMA kernels.
 // M <= 4 takes the LDS-staged MFMA kernel on the fragment-ordered copy where
 // its 64-row groups cover most CUs (a fused RMSNorm input at M = 1 too); M = 1
-// otherwise GemvM1Kernel.
+// otherwise GemvM1Kernel. Rows too long for both (K > 16384 at M = 1, K >
+// 8192 at M = 2) take that MFMA kernel with K segments when the workspace
+// holds their partial sums (plain plans, no RMSNorm input).
 static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void *work,
                                      size_t work_bytes, bool rms = false) {
   if (mnb::GemvFragPreferred(plan->view, M, rms)) return kDecGemvFrag;
@@ -640,6 +653,9 @@ static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void
   if (UsesFragDecode(plan, M) &&
       HasWorkspace(work, work_bytes, mnb::DecodeFragWorkspaceBytes(plan->view, M)))
     return kDecFrag;
+  if (UsesFragSegments(plan, M, rms) &&
+      HasWorkspace(work, work_bytes, mnb::GemvFragSegWorkspaceBytes(plan->view, M)))
+    return kDecGemvFragSeg;
   if (!mnb::DecodeFragSupports(plan->view, M) && UsesMfmaDecode(plan, M) &&
       HasWorkspace(work, work_bytes, mnb::GemvMfmaWorkspaceBytes(plan->view, M)))
     return kDecMfma;
@@ -666,6 +682,7 @@ static size_t DecodeNeed(const mnb_plan *plan, int64_t M, bool rms = false) {
   if (mnb::GemvFragPreferred(plan->view, M, rms)) return 0;
   if (M == 1 && mnb::GemvM1Supports(plan->view)) return 0;
   if (UsesFragDecode(plan, M)) return mnb::DecodeFragWorkspaceBytes(plan->view, M);
+  if (UsesFragSegments(plan, M, rms)) return mnb::GemvFragSegWorkspaceBytes(plan->view, M);
   if (!mnb::DecodeFragSupports(plan->view, M) && UsesMfmaDecode(plan, M))
     return mnb::GemvMfmaWorkspaceBytes(plan->view, M);
   return 0;
@@ -834,6 +851,10 @@ static int RunImpl(const mnb_plan *plan, int64_t M, const float *dA, const float
       e = mnb::LaunchGemvMfma(plan->view, M, dA, Ys, work, s, H);
       fused = true;
       break;
+    case kDecGemvFragSeg:
+      e = mnb::LaunchGemvFragSeg(plan->view, M, dA, Ys, work, s, dBias);
+      bias_done = dBias != nullptr;
+      break;
     case kDecSmallM: e = mnb::LaunchGemvSmallM(plan->view, M, dA, Ys, s); break;
     case kDecFragGroups: {
       // consecutive groups of up to 4 rows, in stream order
@@ -962,6 +983,7 @@ const char *mnb_kernel_name(const mnb_plan *plan, int64_t M, size_t workspace_by
     case kDecMfma: return "GemvMfmaKernel";
     case kDecSmallM: return "GemvSmallMKernel";
     case kDecFragGroups: return "GemvFragKernel";
+    case kDecGemvFragSeg: return "GemvFragKernel (K segments)";
     default: return "GemvKernel";
     }
   case 2:

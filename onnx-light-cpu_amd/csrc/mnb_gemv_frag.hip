@@ -47,8 +47,10 @@
 // with the 2^(24 - e) applied once per unit (exact). No workgroup barrier
 // precedes the stream: a wavefront only reads the operands it wrote itself.
 //
-// Mapping. One workgroup per group g of 64 weight rows and the whole of K; its
-// wavefront w takes SPW consecutive 32-k steps (whole units and blocks), i.e.
+// Mapping. One workgroup per group g of 64 weight rows and the whole of K (or,
+// for rows too long for one workgroup, one per group and K segment: see K
+// segments below); its wavefront w takes SPW consecutive 32-k steps (whole
+// units and blocks), i.e.
 // SPW records of the plan's fragment-ordered copy Bp (1 KiB each: lane l holds
 // the words of rows 64 g + 16 j + (l & 15), j = 0..3, at k = 32 s + 8 (l >> 4),
 // the B operands of four 16-row slices), with 16-byte non-temporal loads kept
@@ -59,6 +61,21 @@
 // points). The wavefronts' row sums meet in LDS and are added in wavefront
 // order by one thread per output. No workspace; results do not depend on
 // scheduling.
+//
+// K segments. Rows longer than 16 wavefronts of 32 steps (K > 16384) do not
+// fit one workgroup, and GemvM1Kernel (whose activation row must fit its LDS)
+// does not take them either. For up to 2 rows the launch then splits K into
+// `segs` segments of whole units: workgroup (g, seg) stages and streams only
+// its segment (its LDS image indexed from the segment's first step), segment
+// 0 writes Y and segment s > 0 the partial sums P[s - 1], and
+// SumPartialsKernel adds them in segment order (with the bias). A row with a
+// non-finite activation gets, per segment, the reference's sum over that
+// segment, so the ordered total is the reference's +-inf or NaN. Measured on
+// MI355X at K = 28672, N = 8192 (2 segments): M = 1 25.8 us against 43.9 for
+// the fp32-FMA GemvKernel the shape took before, M = 2 28.5 against 40.6 for
+// GemvSmallMKernel; K = 24576, N = 4096 (4 segments) at M = 1 13.5 against
+// 26.8. Shorter rows stay with their kernels (the segmented launch is slower
+// there: c3 M = 1 11.5 against GemvM1Kernel's 10.0 us, c1 7.2 against 4.4).
 #include "mnb_decode_common.h"
 
 #include <algorithm>
@@ -109,12 +126,12 @@ __host__ __device__ inline LdsLayout Layout(int K, int nb, int waves, int mt) {
 // staging multiplies by gamma and sums A^2 per row over the wavefront's
 // units, and each row's 1 / rms scales its final sums (it is common to
 // every product of the row).
-template <bool HAS_ZP, int SPB, int SPW, int WIN, int MT, bool RMS>
+template <bool HAS_ZP, int SPB, int SPW, int WIN, int MT, bool RMS, bool SEG = false>
 __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     const float *__restrict__ A, const uint8_t *__restrict__ Bp, const float *__restrict__ Sd,
     const uint32_t *__restrict__ Zd, float *__restrict__ Y, float *__restrict__ H,
     const float *__restrict__ bias, const float *__restrict__ gamma, float eps, int M, int N,
-    int K, int nb) {
+    int K, int nb, int segs, float *__restrict__ P) {
   constexpr int kUnits = SPW / kUnitSteps;      // units of this wavefront
   constexpr int kItems = kUnits * MT;           // (unit, row) staging items, 32 lanes each
   constexpr int kPasses = (kItems + 1) / 2;     // two items per pass
@@ -126,12 +143,19 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int waves = static_cast<int>(blockDim.x) >> 6;
-  const int g = blockIdx.x;
+  // SEG: workgroup (g, seg) of `segs` K segments; otherwise one per group
+  // (every segment term below folds away).
+  const int nseg = SEG ? segs : 1;
+  const int g = SEG ? static_cast<int>(blockIdx.x) / nseg : static_cast<int>(blockIdx.x);
+  const int seg = SEG ? static_cast<int>(blockIdx.x) - g * nseg : 0;
   const int T = K >> 5;
+  const int sbase = SEG ? seg * (T / nseg) : 0;  // first step of this workgroup's K segment
+  const int ubase = sbase / kUnitSteps;
   const int c = lane & 15;
-  const int s0 = wave * SPW;           // first step of this wavefront
+  const int s0 = sbase + wave * SPW;   // first step of this wavefront
   const int u0 = s0 / kUnitSteps;      // its first unit
-  const LdsLayout L = Layout(K, nb, waves, MT);
+  // The LDS image and tables cover the segment (steps from sbase).
+  const LdsLayout L = SEG ? Layout(K / nseg, nb / nseg, waves, MT) : Layout(K, nb, waves, MT);
   float *sums = reinterpret_cast<float *>(lds + L.sums);
   int *exps = reinterpret_cast<int *>(lds + L.exps);
   float *red = reinterpret_cast<float *>(lds + L.red);
@@ -243,14 +267,14 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     const int ul = it / MT, m = it % MT;
     const int q = lane & 31;  // quarter of the unit
     if (it < kItems && m < M) {
-      uint4 *dst = reinterpret_cast<uint4 *>(lds + ((u0 + ul) * kUnitSteps + (q >> 2)) * kStepBytes +
+      uint4 *dst = reinterpret_cast<uint4 *>(lds + ((u0 + ul - ubase) * kUnitSteps + (q >> 2)) * kStepBytes +
                                              (q & 3) * (MT * kOpBytes) + m * kOpBytes);
 #pragma unroll
       for (int t = 0; t < kTerms; ++t) dst[t] = __builtin_bit_cast(uint4, h[t]);
       if constexpr (MT > 1) {
-        if (q == 0) exps[(u0 + ul) * MT + m] = e;
+        if (q == 0) exps[(u0 + ul - ubase) * MT + m] = e;
         if ((q & (4 * SPB - 1)) == 0)
-          sums[((u0 + ul) * kBlocksPerUnit + q / (4 * SPB)) * MT + m] = ssum;
+          sums[((u0 + ul - ubase) * kBlocksPerUnit + q / (4 * SPB)) * MT + m] = ssum;
       }
     }
     if constexpr (MT == 1) {
@@ -285,7 +309,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
   //    computed and not stored).
   const int ma = min((lane & 15) >> 2, M - 1), ta = (lane & 3) == 3 ? 0 : (lane & 3);
   const int mc = min(lane >> 4, M - 1);
-  const int a16 = (s0 * kStepBytes + (lane >> 4) * (MT * kOpBytes) + ma * kOpBytes + ta * 16) >> 4;
+  const int a16 =
+      ((s0 - sbase) * kStepBytes + (lane >> 4) * (MT * kOpBytes) + ma * kOpBytes + ta * 16) >> 4;
   const floatx4 zero4 = floatx4{0.f, 0.f, 0.f, 0.f};
   floatx4 tmp[4];
   float racc[4], acc[4];  // per slice: the unit's sum, the wavefront's sum
@@ -311,10 +336,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     if (i % SPB == 0) {
       bsc = sl.s;
       if constexpr (HAS_ZP) zw = sl.z;
-      if constexpr (MT > 1) sbv = sums[((s0 + i) / SPB) * MT + mc];
+      if constexpr (MT > 1) sbv = sums[((s0 - sbase + i) / SPB) * MT + mc];
     }
     if constexpr (MT > 1) {
-      if (i % kUnitSteps == 0) ev = exps[((s0 + i) / kUnitSteps) * MT + mc];
+      if (i % kUnitSteps == 0) ev = exps[((s0 - sbase + i) / kUnitSteps) * MT + mc];
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -377,16 +402,18 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     const int n = 64 * g + r;
     if constexpr (!RMS) {
       // A non-finite activation: the reference's +-inf / NaN (see
-      // ReferenceRowDot). Row r of the group is slice j = r >> 4, lane
-      // column r & 15 of the fragment-ordered records.
+      // ReferenceRowDot) over this workgroup's K segment. Row r of the group
+      // is slice j = r >> 4, lane column r & 15 of the fragment-ordered
+      // records.
       if (!__builtin_isfinite(y) && n < N) {
         constexpr int kLog2Bs = 5 + (SPB == 1 ? 0 : (SPB == 2 ? 1 : (SPB == 4 ? 2 : 3)));
         const int j = r >> 4, cc = r & 15;
-        const uint8_t *grp = Bp + static_cast<size_t>(g) * T * 1024;
-        const float *sg = Sd + static_cast<size_t>(g) * nb * 64;
-        const uint32_t *zg = HAS_ZP ? Zd + static_cast<size_t>(g) * nb * 16 : Zd;
+        // the segment's first step, 8-k word and block
+        const uint8_t *grp = Bp + (static_cast<size_t>(g) * T + sbase) * 1024;
+        const float *sg = Sd + (static_cast<size_t>(g) * nb + sbase / SPB) * 64;
+        const uint32_t *zg = HAS_ZP ? Zd + (static_cast<size_t>(g) * nb + sbase / SPB) * 16 : Zd;
         y = ReferenceRowDot(
-            A + static_cast<size_t>(m) * K, K, kLog2Bs,
+            A + static_cast<size_t>(m) * K + 32 * sbase, K / nseg, kLog2Bs,
             [&](int k8) {
               return *reinterpret_cast<const uint32_t *>(grp + (k8 >> 2) * 1024 +
                                                          16 * ((k8 & 3) * 16 + cc) + 4 * j);
@@ -403,25 +430,48 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
       const float other = PairSwap(y);
       if ((r & 1) == 0 && n < N) H[m * (N >> 1) + (n >> 1)] = SiluMul(y, other);
     } else if (n < N) {
-      if (bias != nullptr) y += bias[n];  // MatMulNBits input 5
-      Y[m * N + n] = y;
+      // MatMulNBits input 5 (segments: added after their sum)
+      if (bias != nullptr && !SEG) y += bias[n];
+      (seg == 0 ? Y : P + static_cast<size_t>(seg - 1) * M * N)[m * N + n] = y;
     }
   }
 }
 
 inline int RowsBuilt(int64_t M) { return M == 1 ? 1 : (M == 2 ? 2 : 4); }
 
+// segs > 1: K segments with their partial sums at P (no H, no RMSNorm input:
+// checked by the caller); the sum pass follows in LaunchGemvFragSeg.
 template <bool HAS_ZP, int SPB>
 hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipStream_t s, int spw,
-                     int win, float *H, const float *bias, const float *gamma, float eps) {
+                     int win, float *H, const float *bias, const float *gamma, float eps,
+                     int segs = 1, float *P = nullptr) {
   const int K = static_cast<int>(w.K), N = static_cast<int>(w.N), nb = static_cast<int>(w.nb);
-  const int waves = K / 32 / spw;
+  const int waves = K / 32 / segs / spw;
   const int mt = RowsBuilt(M);
-  const int lds = Layout(K, nb, waves, mt).bytes;
-  const dim3 grid(static_cast<unsigned>((w.N + 63) / 64)), block(static_cast<unsigned>(64 * waves));
+  const int lds = Layout(K / segs, nb / segs, waves, mt).bytes;
+  const dim3 grid(static_cast<unsigned>((w.N + 63) / 64 * segs)),
+      block(static_cast<unsigned>(64 * waves));
 #define MNB_GF_LAUNCH(SPWV, WINV, MTV, RMSV)                                                    \
   hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, WINV, MTV, RMSV>), grid, block, lds, s, \
-                     A, w.Bp, w.Sd, w.Zd, Y, H, bias, gamma, eps, M, N, K, nb)
+                     A, w.Bp, w.Sd, w.Zd, Y, H, bias, gamma, eps, M, N, K, nb, segs, P)
+  if (segs > 1) {
+    // K segments: 1 or 2 rows, window 8, no RMSNorm input (checked by the caller)
+#define MNB_GF_LAUNCH_SEG(SPWV, MTV)                                                         \
+  hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, 8, MTV, false, true>), grid, block, lds, \
+                     s, A, w.Bp, w.Sd, w.Zd, Y, nullptr, nullptr, nullptr, 0.0f, M, N, K, nb, segs, P)
+    if (mt == 1) {
+      switch (spw) {
+      case 8: MNB_GF_LAUNCH_SEG(8, 1); break;
+      case 16: MNB_GF_LAUNCH_SEG(16, 1); break;
+      default: MNB_GF_LAUNCH_SEG(32, 1); break;
+      }
+    } else {
+      if (spw == 8) MNB_GF_LAUNCH_SEG(8, 2);
+      else MNB_GF_LAUNCH_SEG(16, 2);
+    }
+#undef MNB_GF_LAUNCH_SEG
+    return hipGetLastError();
+  }
   if (gamma != nullptr) {
     // RMSNorm input (window 8; no 32-step launch with 32-k blocks; 8 steps
     // for M > 1, not with 32-k blocks at 4 rows: checked by the caller, see
@@ -469,25 +519,29 @@ hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipSt
 
 template <bool HAS_ZP>
 hipError_t LaunchZp(const WeightView &w, int M, const float *A, float *Y, hipStream_t s, int spw,
-                    int win, float *H, const float *bias, const float *gamma, float eps) {
+                    int win, float *H, const float *bias, const float *gamma, float eps,
+                    int segs = 1, float *P = nullptr) {
   switch (w.block_size / 32) {
-  case 1: return LaunchSpw<HAS_ZP, 1>(w, M, A, Y, s, spw, win, H, bias, gamma, eps);
-  case 2: return LaunchSpw<HAS_ZP, 2>(w, M, A, Y, s, spw, win, H, bias, gamma, eps);
-  case 4: return LaunchSpw<HAS_ZP, 4>(w, M, A, Y, s, spw, win, H, bias, gamma, eps);
-  default: return LaunchSpw<HAS_ZP, 8>(w, M, A, Y, s, spw, win, H, bias, gamma, eps);
+  case 1: return LaunchSpw<HAS_ZP, 1>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, P);
+  case 2: return LaunchSpw<HAS_ZP, 2>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, P);
+  case 4: return LaunchSpw<HAS_ZP, 4>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, P);
+  default: return LaunchSpw<HAS_ZP, 8>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, P);
   }
 }
 
-inline bool ShapeFits(const WeightView &w, int64_t M, int spw, int win) {
-  const int T = static_cast<int>(w.K / 32);
+// Whether a launch with `spw` steps per wavefront and window `win` fits the
+// kernels built, the workgroup size and the LDS, with K split into `segs`
+// segments (the LDS image then covers one segment).
+inline bool ShapeFits(const WeightView &w, int64_t M, int spw, int win, int segs = 1) {
+  const int T = static_cast<int>(w.K / 32) / segs;
   if (spw != 8 && spw != 16 && spw != 32) return false;
   if (win != 4 && win != 8) return false;
   if (M > 1 && (spw == 32 || win != 8)) return false;  // the launches built for M > 1
   if (M > 2 && w.block_size == 32 && spw != 8) return false;  // 16 steps spill registers
   if (T % spw != 0 || T / spw > kMaxWaves) return false;
-  return static_cast<size_t>(
-             Layout(static_cast<int>(w.K), static_cast<int>(w.nb), T / spw, RowsBuilt(M)).bytes) <=
-         kLdsLimit;
+  return static_cast<size_t>(Layout(static_cast<int>(w.K) / segs, static_cast<int>(w.nb) / segs,
+                                    T / spw, RowsBuilt(M))
+                                 .bytes) <= kLdsLimit;
 }
 
 // Steps per wavefront: 16 where that gives at most 16 wavefronts, else 32
@@ -495,9 +549,23 @@ inline bool ShapeFits(const WeightView &w, int64_t M, int spw, int win) {
 // (interleaved medians; steps / window): c2 16 / 8 7.31 us, 16 / 4 7.42,
 // 8 / 4 7.70, 8 / 8 7.94, 32 / 4 8.47; c5 gate+up 12.69, 12.65, 13.04,
 // 14.38, 12.76.
-inline int PickSpw(const WeightView &w, int64_t M) {
+inline int PickSpw(const WeightView &w, int64_t M, int segs = 1) {
   for (int spw : {16, 32, 8})
-    if (ShapeFits(w, M, spw, 8)) return spw;
+    if (ShapeFits(w, M, spw, 8, segs)) return spw;
+  return 0;
+}
+
+// K segments for up to 2 rows whose K is too long for one workgroup: the
+// fewest (at least 2) of whole units that fit a launch and give the groups
+// and segments 85% of the CUs (at most 16); 0 when none fits.
+inline int Segments(const WeightView &w, int64_t M) {
+  const int T = static_cast<int>(w.K / 32);
+  const int64_t groups = (w.N + 63) / 64;
+  for (int sg = 2; sg <= 16; ++sg) {
+    if (T % (sg * kUnitSteps) != 0) continue;
+    if (sg < 16 && groups * sg * 100 < static_cast<int64_t>(w.num_cus) * 85) continue;
+    if (PickSpw(w, M, sg) > 0) return sg;
+  }
   return 0;
 }
 
@@ -557,6 +625,38 @@ hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float 
   const int m = static_cast<int>(M);
   return w.has_zp ? gf::LaunchZp<true>(w, m, A, Y, s, spw, win, H, bias, gamma, eps)
                          : gf::LaunchZp<false>(w, m, A, Y, s, spw, win, H, bias, gamma, eps);
+}
+
+bool GemvFragSegSupports(const WeightView &w, int64_t M) {
+  // As GemvFragSupports, for 1 or 2 rows too long for one workgroup (no
+  // single-workgroup launch fits), K split into segments of whole units.
+  if (M < 1 || M > 2 || w.Bp == nullptr || w.Sd == nullptr || (w.has_zp && w.Zd == nullptr) ||
+      w.block_size < 32 || w.block_size > 256 || (w.block_size & (w.block_size - 1)) != 0 ||
+      (w.K % gf::kUnitK) != 0 || gf::PickSpw(w, M) > 0)
+    return false;
+  const int segs = gf::Segments(w, M);
+  return segs > 1 && (w.K / 32) * 1024 < (int64_t{1} << 31) && w.nb * 256 < (int64_t{1} << 31) &&
+         M * w.K * 4 < (int64_t{1} << 31) && segs * M * w.N < (int64_t{1} << 29);
+}
+
+size_t GemvFragSegWorkspaceBytes(const WeightView &w, int64_t M) {
+  const int segs = GemvFragSegSupports(w, M) ? gf::Segments(w, M) : 1;
+  return static_cast<size_t>(segs - 1) * static_cast<size_t>(M) * w.N * 4;
+}
+
+hipError_t LaunchGemvFragSeg(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                             hipStream_t s, const float *bias) {
+  if (!GemvFragSegSupports(w, M) || work == nullptr) return hipErrorInvalidValue;
+  const int segs = gf::Segments(w, M);
+  const int spw = gf::PickSpw(w, M, segs);
+  float *P = static_cast<float *>(work);
+  const int m = static_cast<int>(M);
+  const hipError_t e =
+      w.has_zp ? gf::LaunchZp<true>(w, m, A, Y, s, spw, 8, nullptr, nullptr, nullptr, 0.0f, segs, P)
+               : gf::LaunchZp<false>(w, m, A, Y, s, spw, 8, nullptr, nullptr, nullptr, 0.0f, segs, P);
+  if (e != hipSuccess) return e;
+  // Y += the segments' partial sums in segment order, then the bias.
+  return LaunchSumPartials(Y, P, M * w.N, segs - 1, nullptr, s, bias, w.N);
 }
 
 } // namespace mnb

@@ -144,6 +144,15 @@ bool GemvFragPreferred(const WeightView &w, int64_t M, bool rms = false);
 hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s,
                           int steps_per_wave, int window, float *H, const float *bias,
                           const float *gamma = nullptr, float eps = 0.0f);
+// The same GEMV for 1 or 2 rows too long for one workgroup per group (K >
+// 16384 at M = 1, K > 8192 at M = 2): K split into segments of whole 256-k
+// units, one workgroup per (group, segment), the segments' partial sums in
+// `work` (GemvFragSegWorkspaceBytes) added in order by SumPartialsKernel with
+// the bias. No gate/up epilogue and no RMSNorm input.
+bool GemvFragSegSupports(const WeightView &w, int64_t M);
+size_t GemvFragSegWorkspaceBytes(const WeightView &w, int64_t M);
+hipError_t LaunchGemvFragSeg(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
+                             hipStream_t s, const float *bias);
 
 // Decode GEMV for M == 1 (fp16-subnormal mixed FMA): one workgroup per band
 // of `band_rows` weight rows, `rows_per_wave` (1, 2, 4 or 8) rows per

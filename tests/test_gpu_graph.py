@@ -11,6 +11,7 @@ its output with an eager run of the same call on the same input (the same
 kernels, so bit-identical). Cases cover every launch chain: the M <= 4
 fragment-ordered GEMV, the M = 1 GEMV on narrow weights, the small-M GEMV,
 the small-M MFMA decode with and without the partial-sum pass, the
+fragment-ordered GEMV with K segments and their sum pass, the
 weight-streaming GEMM with its split reduction, the prefill GEMM, a gate/up
 plan (fused epilogues and the scratch-sum routes), a fused RMSNorm input and
 the entry point that allocates nothing.
@@ -77,6 +78,19 @@ def test_graph_narrow_plan(pkg, cuda, M):
     print(f"case graph narrow K={K} N={N} M={M} kernel={op.kernel_name(M)}", flush=True)
     try:
         _check_graph(torch, cuda, K, M, lambda A, Y: op(A, out=Y), f"narrow M={M}")
+    finally:
+        op.release()
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_graph_k_segments(pkg, cuda, M):
+    import torch
+    K, N = 20480, 512
+    op = _plan(pkg, K, N, 128, True, seed=M + 50)
+    print(f"case graph k-segments K={K} N={N} M={M} kernel={op.kernel_name(M)}", flush=True)
+    try:
+        assert op.kernel_name(M) == "GemvFragKernel (K segments)"
+        _check_graph(torch, cuda, K, M, lambda A, Y: op(A, out=Y), f"k-segments M={M}")
     finally:
         op.release()
 

@@ -51,3 +51,45 @@ def test_lm_head_shape(pkg, orc, cuda):
 
 def test_long_k_narrow_weights(pkg, orc, cuda):
     _check_sampled(pkg, orc, cuda, 65536, 320, 64, True, (1, 2, 8, 40, 100), seed=6553)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_k_segments_long_rows(pkg, orc, cuda, M):
+    """Llama-70B's down projection (K = 28672, N = 8192), rows too long for
+    one workgroup per group: the fragment-ordered GEMV with K split into
+    segments and their partial sums added in order (the bias after them),
+    bit-identical from run to run; without a workspace the fp32-FMA GEMV
+    serves it. Sampled columns against the fp64 oracle."""
+    import ctypes
+    import torch
+    K, N, bs = 28672, 8192, 128
+    p = pkg.workloads.Projection("long", K, N, bs, True, 1.0, 0.005, 0.02)
+    B, S, Z = pkg.workloads.make_weights(p, 7070)
+    A = pkg.workloads.make_activations(M, K, 1.0, 7071 + M)
+    cols = np.sort(np.random.default_rng(7072).choice(N, size=512, replace=False))
+    y64 = orc.matmul_nbits_f64(A, B[cols], S[cols], Z[cols], K, len(cols), bs)
+    bias = np.random.default_rng(7073).standard_normal(N).astype(np.float32)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    try:
+        print(f"case k-segments K={K} N={N} M={M} kernel={op.kernel_name(M)} "
+              f"(no workspace: {op.kernel_name(M, 0)})", flush=True)
+        assert op.kernel_name(M) == "GemvFragKernel (K segments)"
+        assert op.kernel_name(M, 0) in ("GemvKernel", "GemvSmallMKernel")
+        dA = torch.from_numpy(A).to(cuda)
+        Y = op(dA).cpu().numpy()
+        np.testing.assert_array_equal(op(dA).cpu().numpy(), Y)
+        err = orc.normwise_max_error(Y[:, cols], y64)
+        print(f"  normwise error vs fp64 {err:.2e}")
+        assert err <= GEMV_TOL
+        Yb = op(dA, bias=torch.from_numpy(bias).to(cuda)).cpu().numpy()
+        np.testing.assert_array_equal(Yb, Y + bias[None, :])
+        L = pkg.library()
+        Yn = torch.full((M, N), float("nan"), device=cuda)
+        assert L.mnb_run(op._plan, M, ctypes.c_void_p(dA.data_ptr()), ctypes.c_void_p(Yn.data_ptr()),
+                         None, 0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
+        torch.cuda.synchronize()
+        err0 = orc.normwise_max_error(Yn.cpu().numpy()[:, cols], y64)
+        print(f"  without workspace {err0:.2e}")
+        assert err0 <= GEMV_TOL
+    finally:
+        op.release()

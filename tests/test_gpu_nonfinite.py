@@ -12,7 +12,9 @@ must be bit-identical to the same kernel's run without the non-finite values
 (rows are computed independently).
 
 "mixed" puts +inf and -inf into one row, so that both signs and NaN occur
-among its outputs.
+among its outputs. Rows too long for one workgroup (K = 20480) take the
+fragment-ordered GEMV with K segments at M <= 2: there the +inf and the -inf
+of "mixed" fall into different segments.
 """
 import numpy as np
 import pytest
@@ -65,25 +67,18 @@ def _runs(pkg, op, A, Ab, cuda, M):
     return out
 
 
-@pytest.mark.parametrize("cfg,M", CASES)
-@pytest.mark.parametrize("bad", BADS)
-def test_non_finite_rows(pkg, orc, cuda, cfg, M, bad):
-    W = pkg.workloads
-    c = W.CONFIGS[cfg]
-    p = c.projections[0]
-    B, S, Z = W.make_weights(p, W.weight_seed(c.index) + 7)
-    A = W.make_activations(M, p.K, p.a_sigma, W.activation_seed(c.index, M) + 7)
+def _check_row(pkg, orc, cuda, K, N, bs, B, S, Z, A, M, bad, label):
     row = M // 2
     Ab = _plant(A, row, bad)
-    op = pkg.MatMulNBits(p.K, p.N, 4, p.block_size).prepare(B, S, Z)
-    print(f"case non-finite {cfg} M={M} value={bad} row={row} kernel={op.kernel_name(M)}",
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    print(f"case non-finite {label} M={M} value={bad} row={row} kernel={op.kernel_name(M)}",
           flush=True)
     try:
         runs = _runs(pkg, op, A, Ab, cuda, M)
     finally:
         op.release()
     # the reference's kinds in the row (rows are computed one by one)
-    y32 = orc.matmul_nbits_ref_f32(Ab[row:row + 1], B, S, Z, p.K, p.N, p.block_size)[0]
+    y32 = orc.matmul_nbits_ref_f32(Ab[row:row + 1], B, S, Z, K, N, bs)[0]
     assert not np.isfinite(y32).any()
     if bad == "mixed":
         k = _kinds(y32).sum(axis=1)
@@ -100,3 +95,28 @@ def test_non_finite_rows(pkg, orc, cuda, cfg, M, bad):
                             f"{y32[bad_kind[0]]}")
     print("  checked " + ", ".join(r[0] for r in runs), flush=True)
     assert not failures, failures
+
+
+@pytest.mark.parametrize("cfg,M", CASES)
+@pytest.mark.parametrize("bad", BADS)
+def test_non_finite_rows(pkg, orc, cuda, cfg, M, bad):
+    W = pkg.workloads
+    c = W.CONFIGS[cfg]
+    p = c.projections[0]
+    B, S, Z = W.make_weights(p, W.weight_seed(c.index) + 7)
+    A = W.make_activations(M, p.K, p.a_sigma, W.activation_seed(c.index, M) + 7)
+    _check_row(pkg, orc, cuda, p.K, p.N, p.block_size, B, S, Z, A, M, bad, cfg)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("bad", BADS)
+def test_non_finite_rows_k_segments(pkg, orc, cuda, M, bad):
+    """Rows too long for one workgroup (K = 20480): the fragment-ordered GEMV
+    splits K into segments, each giving the reference's sum over its part of
+    the row, and the ordered sum of the segments keeps the reference's kinds
+    ("mixed" puts its +inf and -inf into different segments)."""
+    W = pkg.workloads
+    p = W.Projection("long", 20480, 512, 128, True, 1.0, 0.005, 0.02)
+    B, S, Z = W.make_weights(p, 2048)
+    A = W.make_activations(M, p.K, 1.0, 2049 + M)
+    _check_row(pkg, orc, cuda, p.K, p.N, p.block_size, B, S, Z, A, M, bad, "K=20480 N=512")

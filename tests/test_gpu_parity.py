@@ -313,7 +313,8 @@ def test_c5_layer_projections(pkg, orc, cuda, proj, M):
     (33280, 94, 128, 8, "GemvSmallMKernel"),  # one range past it: the fp32-FMA kernel serves it
     (33280, 96, 128, 8, "DecodeFragKernel"),  # the fragment-copy kernel has no such limit
     (16384, 14336, 128, 1, "GemvFragKernel"),  # its activation image's largest K at M = 1 (16 x 32 steps)
-    (16640, 14336, 128, 1, "GemvKernel"),      # past it and the M = 1 GEMV's: the fp32-FMA fallback
+    (16640, 14336, 128, 1, "GemvFragKernel (K segments)"),  # past it and the M = 1 GEMV's: K segments
+    (8448, 14336, 128, 2, "GemvFragKernel (K segments)"),   # past its largest K at M = 2 (16 x 16 steps)
 ])
 def test_decode_at_the_kernels_k_limits(pkg, orc, cuda, K, N, bs, M, kernel):
     """At and just past each decode kernel's largest K the dispatcher switches
@@ -334,10 +335,11 @@ def test_decode_at_the_kernels_k_limits(pkg, orc, cuda, K, N, bs, M, kernel):
     y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
     assert orc.normwise_max_error(Y, y64) <= GEMV_TOL
     if M == 1:
-        forced_id = {"GemvM1Kernel": pkg.KERNEL_GEMV_M1, "GemvFragKernel": pkg.KERNEL_GEMV_FRAG}.get(
-            kernel, pkg.KERNEL_GEMV)
-        forced = op.run_kernel(dA, forced_id).cpu().numpy()
-        np.testing.assert_array_equal(Y, forced)
+        forced_id = {"GemvM1Kernel": pkg.KERNEL_GEMV_M1, "GemvFragKernel": pkg.KERNEL_GEMV_FRAG,
+                     "GemvFragKernel (K segments)": None}.get(kernel, pkg.KERNEL_GEMV)
+        if forced_id is not None:
+            forced = op.run_kernel(dA, forced_id).cpu().numpy()
+            np.testing.assert_array_equal(Y, forced)
     else:
         fma = op.run_kernel(dA, pkg.KERNEL_GEMV_SMALL_M).cpu().numpy()
         assert np.array_equal(Y, fma) == (kernel == "GemvSmallMKernel")
