@@ -837,11 +837,14 @@ def main():
     if "sweep" in legs:
         # the configs, then one GPU's shard of c2 and c3 under 8-way tensor
         # parallelism (c2 column-parallel: N / 8 weight rows; c3 row-parallel:
-        # K / 8 of each row)
+        # K / 8 of each row), then rows too long for one workgroup per row
+        # group: Llama-70B's down projection (K = 28672, N = 8192), served at
+        # M <= 2 by the fragment-ordered GEMV with K segments
         tp8 = {"c2/tp8": W.Projection("c2/tp8", 4096, 14336 // 8, 128, True),
-               "c3/tp8": W.Projection("c3/tp8", 14336 // 8, 4096, 32, True, 0.5, 0.002, 0.01)}
+               "c3/tp8": W.Projection("c3/tp8", 14336 // 8, 4096, 32, True, 0.5, 0.002, 0.01),
+               "70b_down": W.Projection("70b_down", 28672, 8192, 128, True)}
         for cname, Ms in (("c1", (1,)), ("c2", (4, 16)), ("c3", (1, 2, 8, 16)),
-                          ("c2/tp8", (1, 16)), ("c3/tp8", (1, 16))):
+                          ("c2/tp8", (1, 16)), ("c3/tp8", (1, 16)), ("70b_down", (1, 2))):
             p = tp8[cname] if cname in tp8 else W.CONFIGS[cname].projections[0]
             for M in Ms:
                 r = decode_leg(torch, pkg, dev, p, M, max(3, args.steps // 4), 2, 17 + M, stream)
