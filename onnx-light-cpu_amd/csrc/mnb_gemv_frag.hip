@@ -65,17 +65,22 @@
 // K segments. Rows longer than 16 wavefronts of 32 steps (K > 16384) do not
 // fit one workgroup, and GemvM1Kernel (whose activation row must fit its LDS)
 // does not take them either. For up to 2 rows the launch then splits K into
-// `segs` segments of whole units: workgroup (g, seg) stages and streams only
-// its segment (its LDS image indexed from the segment's first step), segment
-// 0 writes Y and segment s > 0 the partial sums P[s - 1], and
+// `segs` segments of whole units, all of one length but the last (shorter
+// when the units do not divide evenly: its wavefronts past the row's end read
+// only zeros beyond the weights' buffers and add nothing): workgroup
+// (g, seg) stages and streams only its segment (its LDS image indexed from
+// the segment's first step), segment 0 writes Y and segment s > 0 the
+// partial sums P[s - 1], and
 // SumPartialsKernel adds them in segment order (with the bias). A row with a
 // non-finite activation gets, per segment, the reference's sum over that
 // segment, so the ordered total is the reference's +-inf or NaN. Measured on
 // MI355X at K = 28672, N = 8192 (2 segments): M = 1 25.8 us against 43.9 for
 // the fp32-FMA GemvKernel the shape took before, M = 2 28.5 against 40.6 for
 // GemvSmallMKernel; K = 24576, N = 4096 (4 segments) at M = 1 13.5 against
-// 26.8. Shorter rows stay with their kernels (the segmented launch is slower
-// there: c3 M = 1 11.5 against GemvM1Kernel's 10.0 us, c1 7.2 against 4.4).
+// 26.8; K = 18944, N = 3584 (74 units: 4 segments of 20, the last of 14) at
+// M = 1 11.0 against 22.5. Shorter rows stay with their kernels (the
+// segmented launch is slower there: c3 M = 1 11.5 against GemvM1Kernel's
+// 10.0 us, c1 7.2 against 4.4).
 #include "mnb_decode_common.h"
 
 #include <algorithm>
@@ -131,7 +136,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     const float *__restrict__ A, const uint8_t *__restrict__ Bp, const float *__restrict__ Sd,
     const uint32_t *__restrict__ Zd, float *__restrict__ Y, float *__restrict__ H,
     const float *__restrict__ bias, const float *__restrict__ gamma, float eps, int M, int N,
-    int K, int nb, int segs, float *__restrict__ P) {
+    int K, int nb, int segs, int seg_steps, float *__restrict__ P) {
   constexpr int kUnits = SPW / kUnitSteps;      // units of this wavefront
   constexpr int kItems = kUnits * MT;           // (unit, row) staging items, 32 lanes each
   constexpr int kPasses = (kItems + 1) / 2;     // two items per pass
@@ -143,19 +148,22 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int waves = static_cast<int>(blockDim.x) >> 6;
-  // SEG: workgroup (g, seg) of `segs` K segments; otherwise one per group
-  // (every segment term below folds away).
+  // SEG: workgroup (g, seg) of `segs` K segments of `seg_steps` steps (the
+  // last may be shorter); otherwise one per group (every segment term below
+  // folds away).
   const int nseg = SEG ? segs : 1;
   const int g = SEG ? static_cast<int>(blockIdx.x) / nseg : static_cast<int>(blockIdx.x);
   const int seg = SEG ? static_cast<int>(blockIdx.x) - g * nseg : 0;
   const int T = K >> 5;
-  const int sbase = SEG ? seg * (T / nseg) : 0;  // first step of this workgroup's K segment
+  const int sbase = SEG ? seg * seg_steps : 0;  // first step of this workgroup's K segment
+  const int send = SEG ? min(sbase + seg_steps, T) : T;
   const int ubase = sbase / kUnitSteps;
   const int c = lane & 15;
   const int s0 = sbase + wave * SPW;   // first step of this wavefront
   const int u0 = s0 / kUnitSteps;      // its first unit
-  // The LDS image and tables cover the segment (steps from sbase).
-  const LdsLayout L = SEG ? Layout(K / nseg, nb / nseg, waves, MT) : Layout(K, nb, waves, MT);
+  // The LDS image and tables cover a segment (steps from sbase).
+  const LdsLayout L = SEG ? Layout(32 * seg_steps, seg_steps / SPB, waves, MT)
+                          : Layout(K, nb, waves, MT);
   float *sums = reinterpret_cast<float *>(lds + L.sums);
   int *exps = reinterpret_cast<int *>(lds + L.exps);
   float *red = reinterpret_cast<float *>(lds + L.red);
@@ -381,6 +389,15 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  // A wavefront past the end of a shorter last segment ran on loads beyond the
+  // weights' buffers (zeros) and activations past its row: it adds nothing.
+  if constexpr (SEG) {
+    if (s0 >= send) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = 0.f;
+    }
+  }
+
   // 5. Wavefront sums in LDS (lanes 16 m + c hold rows 16 j + c of
   //    activation row m), added in wavefront order; one thread per output.
   if ((lane >> 4) < M) {
@@ -413,7 +430,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
         const float *sg = Sd + (static_cast<size_t>(g) * nb + sbase / SPB) * 64;
         const uint32_t *zg = HAS_ZP ? Zd + (static_cast<size_t>(g) * nb + sbase / SPB) * 16 : Zd;
         y = ReferenceRowDot(
-            A + static_cast<size_t>(m) * K + 32 * sbase, K / nseg, kLog2Bs,
+            A + static_cast<size_t>(m) * K + 32 * sbase, 32 * (send - sbase), kLog2Bs,
             [&](int k8) {
               return *reinterpret_cast<const uint32_t *>(grp + (k8 >> 2) * 1024 +
                                                          16 * ((k8 & 3) * 16 + cc) + 4 * j);
@@ -444,21 +461,24 @@ inline int RowsBuilt(int64_t M) { return M == 1 ? 1 : (M == 2 ? 2 : 4); }
 template <bool HAS_ZP, int SPB>
 hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipStream_t s, int spw,
                      int win, float *H, const float *bias, const float *gamma, float eps,
-                     int segs = 1, float *P = nullptr) {
+                     int segs = 1, int seg_steps = 0, float *P = nullptr) {
   const int K = static_cast<int>(w.K), N = static_cast<int>(w.N), nb = static_cast<int>(w.nb);
-  const int waves = K / 32 / segs / spw;
+  if (segs <= 1) seg_steps = K / 32;
+  const int waves = seg_steps / spw;
   const int mt = RowsBuilt(M);
-  const int lds = Layout(K / segs, nb / segs, waves, mt).bytes;
+  const int lds = segs > 1 ? Layout(32 * seg_steps, seg_steps / SPB, waves, mt).bytes
+                           : Layout(K, nb, waves, mt).bytes;
   const dim3 grid(static_cast<unsigned>((w.N + 63) / 64 * segs)),
       block(static_cast<unsigned>(64 * waves));
 #define MNB_GF_LAUNCH(SPWV, WINV, MTV, RMSV)                                                    \
   hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, WINV, MTV, RMSV>), grid, block, lds, s, \
-                     A, w.Bp, w.Sd, w.Zd, Y, H, bias, gamma, eps, M, N, K, nb, segs, P)
+                     A, w.Bp, w.Sd, w.Zd, Y, H, bias, gamma, eps, M, N, K, nb, segs, seg_steps, P)
   if (segs > 1) {
     // K segments: 1 or 2 rows, window 8, no RMSNorm input (checked by the caller)
 #define MNB_GF_LAUNCH_SEG(SPWV, MTV)                                                         \
   hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, 8, MTV, false, true>), grid, block, lds, \
-                     s, A, w.Bp, w.Sd, w.Zd, Y, nullptr, nullptr, nullptr, 0.0f, M, N, K, nb, segs, P)
+                     s, A, w.Bp, w.Sd, w.Zd, Y, nullptr, nullptr, nullptr, 0.0f, M, N, K, nb, segs,     \
+                     seg_steps, P)
     if (mt == 1) {
       switch (spw) {
       case 8: MNB_GF_LAUNCH_SEG(8, 1); break;
@@ -520,28 +540,29 @@ hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipSt
 template <bool HAS_ZP>
 hipError_t LaunchZp(const WeightView &w, int M, const float *A, float *Y, hipStream_t s, int spw,
                     int win, float *H, const float *bias, const float *gamma, float eps,
-                    int segs = 1, float *P = nullptr) {
+                    int segs = 1, int seg_steps = 0, float *P = nullptr) {
   switch (w.block_size / 32) {
-  case 1: return LaunchSpw<HAS_ZP, 1>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, P);
-  case 2: return LaunchSpw<HAS_ZP, 2>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, P);
-  case 4: return LaunchSpw<HAS_ZP, 4>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, P);
-  default: return LaunchSpw<HAS_ZP, 8>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, P);
+  case 1:
+    return LaunchSpw<HAS_ZP, 1>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, seg_steps, P);
+  case 2:
+    return LaunchSpw<HAS_ZP, 2>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, seg_steps, P);
+  case 4:
+    return LaunchSpw<HAS_ZP, 4>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, seg_steps, P);
+  default:
+    return LaunchSpw<HAS_ZP, 8>(w, M, A, Y, s, spw, win, H, bias, gamma, eps, segs, seg_steps, P);
   }
 }
 
-// Whether a launch with `spw` steps per wavefront and window `win` fits the
-// kernels built, the workgroup size and the LDS, with K split into `segs`
-// segments (the LDS image then covers one segment).
-inline bool ShapeFits(const WeightView &w, int64_t M, int spw, int win, int segs = 1) {
-  const int T = static_cast<int>(w.K / 32) / segs;
+inline bool ShapeFits(const WeightView &w, int64_t M, int spw, int win) {
+  const int T = static_cast<int>(w.K / 32);
   if (spw != 8 && spw != 16 && spw != 32) return false;
   if (win != 4 && win != 8) return false;
   if (M > 1 && (spw == 32 || win != 8)) return false;  // the launches built for M > 1
   if (M > 2 && w.block_size == 32 && spw != 8) return false;  // 16 steps spill registers
   if (T % spw != 0 || T / spw > kMaxWaves) return false;
-  return static_cast<size_t>(Layout(static_cast<int>(w.K) / segs, static_cast<int>(w.nb) / segs,
-                                    T / spw, RowsBuilt(M))
-                                 .bytes) <= kLdsLimit;
+  return static_cast<size_t>(
+             Layout(static_cast<int>(w.K), static_cast<int>(w.nb), T / spw, RowsBuilt(M)).bytes) <=
+         kLdsLimit;
 }
 
 // Steps per wavefront: 16 where that gives at most 16 wavefronts, else 32
@@ -549,24 +570,41 @@ inline bool ShapeFits(const WeightView &w, int64_t M, int spw, int win, int segs
 // (interleaved medians; steps / window): c2 16 / 8 7.31 us, 16 / 4 7.42,
 // 8 / 4 7.70, 8 / 8 7.94, 32 / 4 8.47; c5 gate+up 12.69, 12.65, 13.04,
 // 14.38, 12.76.
-inline int PickSpw(const WeightView &w, int64_t M, int segs = 1) {
+inline int PickSpw(const WeightView &w, int64_t M) {
   for (int spw : {16, 32, 8})
-    if (ShapeFits(w, M, spw, 8, segs)) return spw;
+    if (ShapeFits(w, M, spw, 8)) return spw;
   return 0;
 }
 
-// K segments for up to 2 rows whose K is too long for one workgroup: the
-// fewest (at least 2) of whole units that fit a launch and give the groups
-// and segments 85% of the CUs (at most 16); 0 when none fits.
-inline int Segments(const WeightView &w, int64_t M) {
+// K segments for 1 or 2 rows too long for one workgroup: for 2, 3, ... 16
+// segments asked for, steps per wavefront in PickSpw's order, the segment
+// length rounded up to whole units and whole wavefronts (the last segment
+// takes the rest), every wavefront wholly inside the row or past its end; the
+// first shape with at most 16 wavefronts, the LDS image of one segment within
+// the limit, and groups x segments covering 85% of the CUs (any count at 16
+// asked for). segs = 0: none.
+struct SegShape {
+  int segs = 0, steps = 0, spw = 0;
+};
+inline SegShape SegmentShape(const WeightView &w, int64_t M) {
   const int T = static_cast<int>(w.K / 32);
   const int64_t groups = (w.N + 63) / 64;
   for (int sg = 2; sg <= 16; ++sg) {
-    if (T % (sg * kUnitSteps) != 0) continue;
-    if (sg < 16 && groups * sg * 100 < static_cast<int64_t>(w.num_cus) * 85) continue;
-    if (PickSpw(w, M, sg) > 0) return sg;
+    for (int spw : {16, 32, 8}) {
+      if ((M > 1 && spw == 32) || T % spw != 0) continue;  // the launches built for M = 2
+      const int gran = std::max(spw, kUnitSteps);
+      const int steps = ((T + sg - 1) / sg + gran - 1) / gran * gran;
+      const int segs = (T + steps - 1) / steps;
+      if (segs < 2 || steps / spw > kMaxWaves) continue;
+      if (sg < 16 && groups * segs * 100 < static_cast<int64_t>(w.num_cus) * 85) continue;
+      const int seg_nb = steps * 32 / static_cast<int>(w.block_size);
+      if (static_cast<size_t>(Layout(32 * steps, seg_nb, steps / spw, RowsBuilt(M)).bytes) >
+          kLdsLimit)
+        continue;
+      return SegShape{segs, steps, spw};
+    }
   }
-  return 0;
+  return SegShape{};
 }
 
 // Steps per wavefront with an RMSNorm input (0: none): M = 1 as PickSpw
@@ -634,29 +672,32 @@ bool GemvFragSegSupports(const WeightView &w, int64_t M) {
       w.block_size < 32 || w.block_size > 256 || (w.block_size & (w.block_size - 1)) != 0 ||
       (w.K % gf::kUnitK) != 0 || gf::PickSpw(w, M) > 0)
     return false;
-  const int segs = gf::Segments(w, M);
-  return segs > 1 && (w.K / 32) * 1024 < (int64_t{1} << 31) && w.nb * 256 < (int64_t{1} << 31) &&
-         M * w.K * 4 < (int64_t{1} << 31) && segs * M * w.N < (int64_t{1} << 29);
+  // K <= 2^20: the offsets of wavefronts past the end of a shorter last
+  // segment (up to one segment beyond the row and the weights' buffers) stay
+  // far below 2^31.
+  const int segs = gf::SegmentShape(w, M).segs;
+  return segs > 1 && w.K <= (int64_t{1} << 20) && segs * M * w.N < (int64_t{1} << 29);
 }
 
 size_t GemvFragSegWorkspaceBytes(const WeightView &w, int64_t M) {
-  const int segs = GemvFragSegSupports(w, M) ? gf::Segments(w, M) : 1;
+  const int segs = GemvFragSegSupports(w, M) ? gf::SegmentShape(w, M).segs : 1;
   return static_cast<size_t>(segs - 1) * static_cast<size_t>(M) * w.N * 4;
 }
 
 hipError_t LaunchGemvFragSeg(const WeightView &w, int64_t M, const float *A, float *Y, void *work,
                              hipStream_t s, const float *bias) {
   if (!GemvFragSegSupports(w, M) || work == nullptr) return hipErrorInvalidValue;
-  const int segs = gf::Segments(w, M);
-  const int spw = gf::PickSpw(w, M, segs);
+  const gf::SegShape sh = gf::SegmentShape(w, M);
   float *P = static_cast<float *>(work);
   const int m = static_cast<int>(M);
   const hipError_t e =
-      w.has_zp ? gf::LaunchZp<true>(w, m, A, Y, s, spw, 8, nullptr, nullptr, nullptr, 0.0f, segs, P)
-               : gf::LaunchZp<false>(w, m, A, Y, s, spw, 8, nullptr, nullptr, nullptr, 0.0f, segs, P);
+      w.has_zp ? gf::LaunchZp<true>(w, m, A, Y, s, sh.spw, 8, nullptr, nullptr, nullptr, 0.0f,
+                                    sh.segs, sh.steps, P)
+               : gf::LaunchZp<false>(w, m, A, Y, s, sh.spw, 8, nullptr, nullptr, nullptr, 0.0f,
+                                     sh.segs, sh.steps, P);
   if (e != hipSuccess) return e;
   // Y += the segments' partial sums in segment order, then the bias.
-  return LaunchSumPartials(Y, P, M * w.N, segs - 1, nullptr, s, bias, w.N);
+  return LaunchSumPartials(Y, P, M * w.N, sh.segs - 1, nullptr, s, bias, w.N);
 }
 
 } // namespace mnb

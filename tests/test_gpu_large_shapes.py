@@ -53,16 +53,19 @@ def test_long_k_narrow_weights(pkg, orc, cuda):
     _check_sampled(pkg, orc, cuda, 65536, 320, 64, True, (1, 2, 8, 40, 100), seed=6553)
 
 
+@pytest.mark.parametrize("K,N", [(28672, 8192), (18944, 3584)])
 @pytest.mark.parametrize("M", [1, 2])
-def test_k_segments_long_rows(pkg, orc, cuda, M):
-    """Llama-70B's down projection (K = 28672, N = 8192), rows too long for
-    one workgroup per group: the fragment-ordered GEMV with K split into
+def test_k_segments_long_rows(pkg, orc, cuda, K, N, M):
+    """Down projections with rows too long for one workgroup per group:
+    Llama-70B's (K = 28672, N = 8192: equal segments) and Qwen2-7B's
+    (K = 18944 = 74 units, N = 3584: a shorter last segment whose trailing
+    wavefronts add nothing). The fragment-ordered GEMV with K split into
     segments and their partial sums added in order (the bias after them),
     bit-identical from run to run; without a workspace the fp32-FMA GEMV
     serves it. Sampled columns against the fp64 oracle."""
     import ctypes
     import torch
-    K, N, bs = 28672, 8192, 128
+    bs = 128
     p = pkg.workloads.Projection("long", K, N, bs, True, 1.0, 0.005, 0.02)
     B, S, Z = pkg.workloads.make_weights(p, 7070)
     A = pkg.workloads.make_activations(M, K, 1.0, 7071 + M)
