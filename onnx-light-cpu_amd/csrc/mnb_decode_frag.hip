@@ -434,6 +434,14 @@ struct Shape {
 // 10.7); c1 four runs of 4 x 1 5.7 us (two runs of 4 x 2: 7.1); c3 (56
 // units) four runs of 7 x 2, one workgroup per CU, 17.9 us per call
 // against 18.5 for seven runs of 4 x 2 (1.75 workgroups per CU).
+// Unit counts with no such division into at most 16 runs (a prime 43 at
+// K = 11008, 74 = 2 x 37 at K = 18944, which the search above would give one
+// run per unit) take runs of one length with a shorter last run: the fewest
+// runs covering 85% of the CUs, each ceil(units / runs) units rounded up to
+// whole wavefronts (U = 2 before 1, at least 4 wavefronts before any). The
+// wavefronts past the last unit read only beyond the buffers of the weights,
+// scales, zero points, image and exponents (bounds-checked buffer loads:
+// zeros) and add exactly zero.
 inline Shape PickShape(const WeightView &w, int wpg_req, int u_req) {
   const int64_t groups = (w.N + 63) / 64;
   const int units = static_cast<int>(w.K / kUnitK);
@@ -444,7 +452,7 @@ inline Shape PickShape(const WeightView &w, int wpg_req, int u_req) {
     sh.segs = units / (sh.units_per_wave * sh.wpg);
     return sh;
   }
-  for (int segs = 1; segs <= units; ++segs) {
+  for (int segs = 1; segs <= std::min(units, 16); ++segs) {
     if (units % segs != 0) continue;
     const int per = units / segs;  // units per workgroup
     if (segs < units && groups * segs * 100 < static_cast<int64_t>(w.num_cus) * 85) continue;
@@ -452,6 +460,16 @@ inline Shape PickShape(const WeightView &w, int wpg_req, int u_req) {
       for (int U : {2, 1})
         for (int wpg : {8, 7, 6, 5, 4, 3, 2, 1})
           if (wpg >= min_wpg && wpg * U == per) return Shape{wpg, U, segs};
+  }
+  for (int segs = 2; segs <= units; ++segs) {
+    if (segs < units && groups * segs * 100 < static_cast<int64_t>(w.num_cus) * 85) continue;
+    for (int min_wpg : {4, 1})
+      for (int U : {2, 1}) {
+        const int per = ((units + segs - 1) / segs + U - 1) / U * U;  // units per run
+        const int wpg = per / U;
+        if (wpg < min_wpg || wpg > kMaxWaves || (units + per - 1) / per != segs) continue;
+        return Shape{wpg, U, segs};
+      }
   }
   return sh;
 }
@@ -554,8 +572,11 @@ hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, floa
                             const float *bias, const float *gamma, float eps) {
   const df::Shape sh = df::PickShape(w, wpg, units_per_wave);
   const int units = static_cast<int>(w.K / df::kUnitK);
+  // every unit in a run, no run empty (the last may be shorter)
   if (sh.wpg < 1 || sh.wpg > df::kMaxWaves || sh.segs < 1 ||
-      sh.segs * sh.wpg * sh.units_per_wave != units || (sh.units_per_wave != 1 && sh.units_per_wave != 2))
+      sh.segs * sh.wpg * sh.units_per_wave < units ||
+      (sh.segs - 1) * sh.wpg * sh.units_per_wave >= units ||
+      (sh.units_per_wave != 1 && sh.units_per_wave != 2))
     return hipErrorInvalidValue;
   if (gamma != nullptr && !DecodeFragTakesRms(w)) return hipErrorInvalidValue;
   if (gamma != nullptr && (reinterpret_cast<uintptr_t>(gamma) % 16) != 0) return hipErrorInvalidValue;

@@ -96,3 +96,32 @@ def test_k_segments_long_rows(pkg, orc, cuda, K, N, M):
         assert err0 <= GEMV_TOL
     finally:
         op.release()
+
+
+@pytest.mark.parametrize("K,N", [(11008, 4096), (18944, 3584)])
+@pytest.mark.parametrize("M", [4, 8, 16])
+def test_small_m_decode_uneven_units(pkg, orc, cuda, K, N, M):
+    """The small-M MFMA decode on unit counts with no even division into a
+    few runs: Llama-2-7B's down projection (K = 11008: 43 units, prime) and
+    Qwen2-7B's (K = 18944: 74 units), split into runs of one length and a
+    shorter last run whose trailing wavefronts add nothing. Sampled columns
+    against the fp64 oracle, bit-identical from run to run."""
+    import torch
+    bs = 128
+    p = pkg.workloads.Projection("uneven", K, N, bs, True, 1.0, 0.005, 0.02)
+    B, S, Z = pkg.workloads.make_weights(p, K + M)
+    A = pkg.workloads.make_activations(M, K, 1.0, K + M + 1)
+    cols = np.sort(np.random.default_rng(K).choice(N, size=512, replace=False))
+    y64 = orc.matmul_nbits_f64(A, B[cols], S[cols], Z[cols], K, len(cols), bs)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    try:
+        print(f"case uneven units K={K} N={N} M={M} kernel={op.kernel_name(M)}", flush=True)
+        assert op.kernel_name(M) == "DecodeFragKernel"
+        dA = torch.from_numpy(A).to(cuda)
+        Y = op(dA).cpu().numpy()
+        np.testing.assert_array_equal(op(dA).cpu().numpy(), Y)
+        err = orc.normwise_max_error(Y[:, cols], y64)
+        print(f"  normwise error vs fp64 {err:.2e}")
+        assert err <= GEMV_TOL
+    finally:
+        op.release()
