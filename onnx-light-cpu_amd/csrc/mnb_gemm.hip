@@ -1246,7 +1246,10 @@ __global__ __launch_bounds__(512) void StreamKernel(
   // The wavefronts' tiles meet in LDS; wavefront w then finishes the
   // fragments x = (tg, j) = w, w + wpg, ..., adding the wavefronts' tiles in
   // wavefront order. Lane l holds row 16 tg + (l & 15) and the 4 columns
-  // 64 g + 16 j + 4 (l >> 4) .. + 3.
+  // 64 g + 16 j + 4 (l >> 4) .. + 3. A wavefront past K (the end of a
+  // shorter last segment) ran on loads beyond the weights' buffers (zeros)
+  // and activations past its rows: it adds nothing.
+  const bool past_k = s0 >= T;
 #pragma unroll
   for (int tg = 0; tg < TG; ++tg)
 #pragma unroll
@@ -1256,7 +1259,7 @@ __global__ __launch_bounds__(512) void StreamKernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) t[q] = __builtin_amdgcn_ldexpf(t[q], -fw[tg]);
       }
-      sred[(wave * TG * 4 + tg * 4 + j) * 64 + lane] = t;
+      sred[(wave * TG * 4 + tg * 4 + j) * 64 + lane] = past_k ? floatx4{0.f, 0.f, 0.f, 0.f} : t;
     }
   __syncthreads();
   float *out = seg == 0 ? Y : partials + static_cast<size_t>(seg - 1) * M * N;
@@ -1298,12 +1301,21 @@ __global__ __launch_bounds__(512) void StreamKernel(
 
 struct StreamShape {
   int segs, wpg, spw;
+  bool ragged = false;  // a shorter last segment
 };
 
 // K segments, wavefronts per workgroup and steps per wavefront (segs * wpg *
 // spw = K / 32): the fewest segments whose workgroups cover 85% of the CUs
 // (else the most that leave a workgroup at least 16 steps), then 8
-// wavefronts before 4 and the longest spw in {16, 8, 4}.
+// wavefronts before 4 and the longest spw in {16, 8, 4}. Step counts with no
+// such division (K = 11008: 344 steps = 8 x 43) take segments of one length
+// and a shorter last one: for each segment count the least padded wpg x spw
+// of whole wavefronts (K / 32 a multiple of spw) that gives that count, the
+// fewest covering 85% of the CUs; the wavefronts past K add nothing. Such
+// shapes serve up to 32 rows (measured against GemmKernel, which took these
+// shapes before: K = 11008, N = 4096 at M = 17 / 24 / 32 22.4 / 22.8 / 23.3
+// -> 20.4 / 20.6 / 20.9 us, K = 18944, N = 3584 at M = 32 32.7 -> 29.8; at
+// M = 40-64 level or slower, up to +21%).
 inline StreamShape PickStreamShape(const WeightView &w, int segs_req, int spw_req) {
   const int64_t groups = (w.N + kSGroupRows - 1) / kSGroupRows;
   const int T = static_cast<int>(w.K / 32);
@@ -1323,6 +1335,19 @@ inline StreamShape PickStreamShape(const WeightView &w, int segs_req, int spw_re
     StreamShape sh = fit(T / segs);
     if (sh.wpg == 0) continue;
     sh.segs = segs;
+    best = sh;
+    if (groups * segs * 100 >= static_cast<int64_t>(w.num_cus) * 85) break;
+  }
+  if (best.wpg != 0) return best;
+  for (int segs = 1; segs <= kMaxSplits; ++segs) {
+    StreamShape sh{0, 0, 0};
+    for (int wpg : {8, 4})
+      for (int spw : {16, 8, 4}) {
+        const int per = wpg * spw;
+        if (T % spw != 0 || (T + per - 1) / per != segs) continue;
+        if (sh.wpg == 0 || per < sh.wpg * sh.spw) sh = StreamShape{segs, wpg, spw, true};
+      }
+    if (sh.wpg == 0) continue;
     best = sh;
     if (groups * segs * 100 >= static_cast<int64_t>(w.num_cus) * 85) break;
   }
@@ -1491,8 +1516,9 @@ size_t PrefillPartialBytes(const WeightView &w, int64_t M) {
 }
 
 bool StreamSupportsM(const WeightView &w, int64_t M) {
-  return M >= 17 && M <= 64 && PrefillSupportsShape(w) && w.K <= (int64_t{1} << 22) &&
-         PickStreamShape(w, 0, 0).segs > 0;
+  if (M < 17 || M > 64 || !PrefillSupportsShape(w) || w.K > (int64_t{1} << 22)) return false;
+  const StreamShape sh = PickStreamShape(w, 0, 0);
+  return sh.segs > 0 && (!sh.ragged || M <= 32);  // shorter last segment: up to 32 rows
 }
 
 size_t StreamPartialBytes(const WeightView &w, int64_t M, int segs) {
@@ -1520,8 +1546,10 @@ size_t StreamWorkspaceBytes(const WeightView &w, int64_t M, int segs, int spw) {
 // wavefront, so it needs wpg >= 4 to reach all 4 TG; at most 8 wavefronts.
 bool StreamShapeOk(const WeightView &w, int64_t M, int segs, int spw) {
   const StreamShape sh = PickStreamShape(w, segs, spw);
+  // every step in a segment, no segment empty (the last may be shorter)
+  const int64_t per = static_cast<int64_t>(sh.wpg) * sh.spw, T = w.K / 32;
   return StreamSupportsM(w, M) && sh.segs >= 1 && sh.segs <= kMaxSplits && sh.wpg >= 4 &&
-         sh.wpg <= 8 && sh.segs * sh.wpg * sh.spw == w.K / 32;
+         sh.wpg <= 8 && T % sh.spw == 0 && sh.segs * per >= T && (sh.segs - 1) * per < T;
 }
 
 // ConvertA (64-row tiling), the streaming kernel, and the ordered reduction

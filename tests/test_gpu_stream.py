@@ -34,6 +34,8 @@ def _weights(pkg, K, N, bs, zp, seed):
     (14336, 256, 32, True, 24, 7, 8),      # long K, 7 segments
     (2048, 512, 64, True, 32, 4, 4),       # 4 wavefronts per workgroup (the fewest served)
     (2560, 512, 1024, True, 40, 5, 4),     # ragged last block (512 of 1024 k), 5 segments
+    (11008, 4096, 128, False, 17, 0, 0),   # 344 steps (8 x 43): 6 segments of 64, the last of 24
+    (11008, 1024, 128, True, 32, 0, 0),    # 11 segments of 32 steps, the last of 24
 ])
 def test_stream_kernel_parity(pkg, orc, cuda, K, N, bs, zp, M, segs, spw):
     import torch
@@ -185,3 +187,18 @@ def test_fp16_conversion_bits(pkg, orc, cuda, M, kernel, segs, spw):
     bad = np.argwhere(y != expect)
     assert bad.size == 0, (f"{bad.shape[0]} outputs differ; first {tuple(bad[0])}: "
                            f"{y[tuple(bad[0])]!r} vs {expect[tuple(bad[0])]!r}")
+
+
+def test_stream_shorter_last_segment_serves_up_to_32_rows(pkg, cuda):
+    """K = 11008 (344 steps, no even division into segments of 8 or 4
+    wavefronts): the streaming GEMM with a shorter last segment serves 17-32
+    rows, the tiled GEMM from 33 on (where it is faster on these shapes)."""
+    p = pkg.workloads.Projection("uneven", 11008, 1024, 128, True)
+    op = pkg.MatMulNBits(p.K, p.N, 4, p.block_size).prepare(*pkg.workloads.make_weights(p, 5))
+    try:
+        names = {M: op.kernel_name(M) for M in (17, 32, 33, 64)}
+        print(f"case stream uneven K=11008 N=1024: {names}", flush=True)
+        assert names[17] == names[32] == "StreamKernel"
+        assert names[33] != "StreamKernel" and names[64] != "StreamKernel"
+    finally:
+        op.release()
