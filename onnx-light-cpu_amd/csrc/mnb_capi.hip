@@ -616,7 +616,7 @@ static bool UsesFragDecode(const mnb_plan *plan, int64_t M) {
 }
 
 // The K-segmented fragment-ordered GEMV (1 or 2 rows too long for one
-// workgroup): plain plans (its sums pass has no gate/up pairing), no RMSNorm
+// workgroup, 3 or 4 long rows on narrow weights): plain plans (its sums pass has no gate/up pairing), no RMSNorm
 // input (a segment sees only its part of each row's sum of squares).
 static bool UsesFragSegments(const mnb_plan *plan, int64_t M, bool rms) {
   return !rms && !plan->gate_up && mnb::GemvFragSegSupports(plan->view, M);
@@ -627,7 +627,8 @@ static bool UsesFragSegments(const mnb_plan *plan, int64_t M, bool rms) {
 // kDecFragGroups: a compact plan without the small-M kernel's workspace runs
 // the fragment-ordered GEMV on consecutive groups of up to 4 rows.
 // kDecGemvFragSeg: the fragment-ordered GEMV with K split into segments, for
-// 1 or 2 rows too long for one workgroup (and for GemvM1Kernel).
+// 1 or 2 rows too long for one workgroup (and for GemvM1Kernel), and 3 or 4
+// rows of K >= 5120 on weights up to 192 Mi elements.
 enum DecodeKernel {
   kDecM1, kDecGemvFrag, kDecFrag, kDecMfma, kDecSmallM, kDecGemv, kDecFragGroups, kDecGemvFragSeg
 };
@@ -645,17 +646,18 @@ static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
 // its 64-row groups cover most CUs (a fused RMSNorm input at M = 1 too); M = 1
 // otherwise GemvM1Kernel. Rows too long for both (K > 16384 at M = 1, K >
 // 8192 at M = 2) take that MFMA kernel with K segments when the workspace
-// holds their partial sums (plain plans, no RMSNorm input).
+// holds their partial sums (plain plans, no RMSNorm input), and so do 3 or 4
+// rows of K >= 5120 on narrow weights, ahead of the small-M MFMA decode.
 static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void *work,
                                      size_t work_bytes, bool rms = false) {
   if (mnb::GemvFragPreferred(plan->view, M, rms)) return kDecGemvFrag;
   if (M == 1 && mnb::GemvM1Supports(plan->view)) return kDecM1;
-  if (UsesFragDecode(plan, M) &&
-      HasWorkspace(work, work_bytes, mnb::DecodeFragWorkspaceBytes(plan->view, M)))
-    return kDecFrag;
   if (UsesFragSegments(plan, M, rms) &&
       HasWorkspace(work, work_bytes, mnb::GemvFragSegWorkspaceBytes(plan->view, M)))
     return kDecGemvFragSeg;
+  if (UsesFragDecode(plan, M) &&
+      HasWorkspace(work, work_bytes, mnb::DecodeFragWorkspaceBytes(plan->view, M)))
+    return kDecFrag;
   if (!mnb::DecodeFragSupports(plan->view, M) && UsesMfmaDecode(plan, M) &&
       HasWorkspace(work, work_bytes, mnb::GemvMfmaWorkspaceBytes(plan->view, M)))
     return kDecMfma;
@@ -681,8 +683,8 @@ static bool DecodeTakesRms(const mnb_plan *plan, DecodeKernel k) {
 static size_t DecodeNeed(const mnb_plan *plan, int64_t M, bool rms = false) {
   if (mnb::GemvFragPreferred(plan->view, M, rms)) return 0;
   if (M == 1 && mnb::GemvM1Supports(plan->view)) return 0;
-  if (UsesFragDecode(plan, M)) return mnb::DecodeFragWorkspaceBytes(plan->view, M);
   if (UsesFragSegments(plan, M, rms)) return mnb::GemvFragSegWorkspaceBytes(plan->view, M);
+  if (UsesFragDecode(plan, M)) return mnb::DecodeFragWorkspaceBytes(plan->view, M);
   if (!mnb::DecodeFragSupports(plan->view, M) && UsesMfmaDecode(plan, M))
     return mnb::GemvMfmaWorkspaceBytes(plan->view, M);
   return 0;
@@ -704,11 +706,13 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes) {
   // A gate/up plan adds the scratch sum in front of either.
   // The exact route (path 4) runs the decode kernels over groups of at most
   // 16 rows, one after another in the same workspace.
-  // Decode launches served by the fragment-ordered GEMV need none.
+  // Decode launches served by the fragment-ordered GEMV need none. The
+  // decode kernel of a fused RMSNorm input (mnb_run_rmsnorm passes this
+  // size on) may differ from the plain one: the size covers both.
   size_t need = 0;
   if (M > 0 && mnb::GemmSupports(plan->view, M)) need = mnb::GemmWorkspaceBytes(plan->view, M);
   const int64_t md = std::min<int64_t>(M, kExactGroupRows);
-  if (md > 0) need = std::max(need, DecodeNeed(plan, md));
+  if (md > 0) need = std::max({need, DecodeNeed(plan, md), DecodeNeed(plan, md, true)});
   *bytes = need + GateUpScratchBytes(plan, M);
   return MNB_OK;
 }

@@ -64,7 +64,8 @@
 //
 // K segments. Rows longer than 16 wavefronts of 32 steps (K > 16384) do not
 // fit one workgroup, and GemvM1Kernel (whose activation row must fit its LDS)
-// does not take them either. For up to 2 rows the launch then splits K into
+// does not take them either. For up to 2 rows (and for 3 or 4 rows of
+// K >= 5120 on weights up to 192 Mi elements, below) the launch splits K into
 // `segs` segments of whole units, all of one length but the last (shorter
 // when the units do not divide evenly: its wavefronts past the row's end read
 // only zeros beyond the weights' buffers and add nothing): workgroup
@@ -81,6 +82,14 @@
 // M = 1 11.0 against 22.5. Shorter rows stay with their kernels (the
 // segmented launch is slower there: c3 M = 1 11.5 against GemvM1Kernel's
 // 10.0 us, c1 7.2 against 4.4).
+//
+// At 3 or 4 rows (the 4-row launch) the segments serve narrow weights better
+// than DecodeFragKernel, the small-M MFMA decode: at M = 4, K = 24576,
+// N = 3072 13.6 us against 18.7; K = 18944, N = 3584 13.2 against 18.3;
+// K = 11008, N = 4096 9.9 against 12.5; K = 5120, N = 5120 8.2 against 10.8;
+// K = 8192, N = 8192 11.7 against 13.5. Not for K <= 4096 (K = N = 4096:
+// 8.0 against 7.1, the second launch) nor for the largest weights (K = 8192,
+// N = 28672: 33.3 against 31.0; K = 28672, N = 8192: 33.1 against 32.3).
 #include "mnb_decode_common.h"
 
 #include <algorithm>
@@ -474,7 +483,8 @@ hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipSt
   hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, WINV, MTV, RMSV>), grid, block, lds, s, \
                      A, w.Bp, w.Sd, w.Zd, Y, H, bias, gamma, eps, M, N, K, nb, segs, seg_steps, P)
   if (segs > 1) {
-    // K segments: 1 or 2 rows, window 8, no RMSNorm input (checked by the caller)
+    // K segments: window 8, no RMSNorm input, 8 steps per wavefront at 4 rows
+    // with 32-k blocks (checked by the caller)
 #define MNB_GF_LAUNCH_SEG(SPWV, MTV)                                                         \
   hipLaunchKernelGGL((GemvFragKernel<HAS_ZP, SPB, SPWV, 8, MTV, false, true>), grid, block, lds, \
                      s, A, w.Bp, w.Sd, w.Zd, Y, nullptr, nullptr, nullptr, 0.0f, M, N, K, nb, segs,     \
@@ -485,9 +495,12 @@ hipError_t LaunchSpw(const WeightView &w, int M, const float *A, float *Y, hipSt
       case 16: MNB_GF_LAUNCH_SEG(16, 1); break;
       default: MNB_GF_LAUNCH_SEG(32, 1); break;
       }
-    } else {
+    } else if (mt == 2) {
       if (spw == 8) MNB_GF_LAUNCH_SEG(8, 2);
       else MNB_GF_LAUNCH_SEG(16, 2);
+    } else {
+      if (spw == 8) MNB_GF_LAUNCH_SEG(8, 4);
+      else if constexpr (SPB > 1) MNB_GF_LAUNCH_SEG(16, 4);
     }
 #undef MNB_GF_LAUNCH_SEG
     return hipGetLastError();
@@ -591,7 +604,8 @@ inline SegShape SegmentShape(const WeightView &w, int64_t M) {
   const int64_t groups = (w.N + 63) / 64;
   for (int sg = 2; sg <= 16; ++sg) {
     for (int spw : {16, 32, 8}) {
-      if ((M > 1 && spw == 32) || T % spw != 0) continue;  // the launches built for M = 2
+      if ((M > 1 && spw == 32) || T % spw != 0) continue;  // the launches built for M > 1
+      if (RowsBuilt(M) == 4 && w.block_size == 32 && spw != 8) continue;
       const int gran = std::max(spw, kUnitSteps);
       const int steps = ((T + sg - 1) / sg + gran - 1) / gran * gran;
       const int segs = (T + steps - 1) / steps;
@@ -666,11 +680,17 @@ hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float 
 }
 
 bool GemvFragSegSupports(const WeightView &w, int64_t M) {
-  // As GemvFragSupports, for 1 or 2 rows too long for one workgroup (no
-  // single-workgroup launch fits), K split into segments of whole units.
-  if (M < 1 || M > 2 || w.Bp == nullptr || w.Sd == nullptr || (w.has_zp && w.Zd == nullptr) ||
+  // As GemvFragSupports, K split into segments of whole units: 1 or 2 rows
+  // too long for one workgroup (no single-workgroup launch fits); 3 or 4
+  // rows of at least 5120 on weights of at most 192 Mi elements, where the
+  // segments beat the small-M MFMA decode (shorter rows pay more for the
+  // partial sums' second launch than they gain; the largest weights fill the
+  // CUs with the decode's own split).
+  if (M < 1 || M > 4 || w.Bp == nullptr || w.Sd == nullptr || (w.has_zp && w.Zd == nullptr) ||
       w.block_size < 32 || w.block_size > 256 || (w.block_size & (w.block_size - 1)) != 0 ||
-      (w.K % gf::kUnitK) != 0 || gf::PickSpw(w, M) > 0)
+      (w.K % gf::kUnitK) != 0)
+    return false;
+  if (M <= 2 ? gf::PickSpw(w, M) > 0 : (w.K < 5120 || w.K * w.N > (int64_t{192} << 20)))
     return false;
   // K <= 2^20: the offsets of wavefronts past the end of a shorter last
   // segment (up to one segment beyond the row and the weights' buffers) stay

@@ -82,7 +82,7 @@ def test_graph_narrow_plan(pkg, cuda, M):
         op.release()
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3])
 def test_graph_k_segments(pkg, cuda, M):
     import torch
     K, N = 20480, 512

@@ -53,28 +53,19 @@ def test_long_k_narrow_weights(pkg, orc, cuda):
     _check_sampled(pkg, orc, cuda, 65536, 320, 64, True, (1, 2, 8, 40, 100), seed=6553)
 
 
-@pytest.mark.parametrize("K,N", [(28672, 8192), (18944, 3584)])
-@pytest.mark.parametrize("M", [1, 2])
-def test_k_segments_long_rows(pkg, orc, cuda, K, N, M):
-    """Down projections with rows too long for one workgroup per group:
-    Llama-70B's (K = 28672, N = 8192: equal segments) and Qwen2-7B's
-    (K = 18944 = 74 units, N = 3584: a shorter last segment whose trailing
-    wavefronts add nothing). The fragment-ordered GEMV with K split into
-    segments and their partial sums added in order (the bias after them),
-    bit-identical from run to run; without a workspace the fp32-FMA GEMV
-    serves it. Sampled columns against the fp64 oracle."""
+def _check_segments(pkg, orc, cuda, K, N, bs, zp, M):
     import ctypes
     import torch
-    bs = 128
-    p = pkg.workloads.Projection("long", K, N, bs, True, 1.0, 0.005, 0.02)
+    p = pkg.workloads.Projection("long", K, N, bs, zp, 1.0, 0.005, 0.02)
     B, S, Z = pkg.workloads.make_weights(p, 7070)
     A = pkg.workloads.make_activations(M, K, 1.0, 7071 + M)
     cols = np.sort(np.random.default_rng(7072).choice(N, size=512, replace=False))
-    y64 = orc.matmul_nbits_f64(A, B[cols], S[cols], Z[cols], K, len(cols), bs)
+    Zc = Z[cols] if Z is not None else None
+    y64 = orc.matmul_nbits_f64(A, B[cols], S[cols], Zc, K, len(cols), bs)
     bias = np.random.default_rng(7073).standard_normal(N).astype(np.float32)
     op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
     try:
-        print(f"case k-segments K={K} N={N} M={M} kernel={op.kernel_name(M)} "
+        print(f"case k-segments K={K} N={N} bs={bs} zp={zp} M={M} kernel={op.kernel_name(M)} "
               f"(no workspace: {op.kernel_name(M, 0)})", flush=True)
         assert op.kernel_name(M) == "GemvFragKernel (K segments)"
         assert op.kernel_name(M, 0) in ("GemvKernel", "GemvSmallMKernel")
@@ -98,14 +89,43 @@ def test_k_segments_long_rows(pkg, orc, cuda, K, N, M):
         op.release()
 
 
+@pytest.mark.parametrize("K,N", [(28672, 8192), (18944, 3584)])
+@pytest.mark.parametrize("M", [1, 2])
+def test_k_segments_long_rows(pkg, orc, cuda, K, N, M):
+    """Down projections with rows too long for one workgroup per group:
+    Llama-70B's (K = 28672, N = 8192: equal segments) and Qwen2-7B's
+    (K = 18944 = 74 units, N = 3584: a shorter last segment whose trailing
+    wavefronts add nothing). The fragment-ordered GEMV with K split into
+    segments and their partial sums added in order (the bias after them),
+    bit-identical from run to run; without a workspace the fp32-FMA GEMV
+    serves it. Sampled columns against the fp64 oracle."""
+    _check_segments(pkg, orc, cuda, K, N, 128, True, M)
+
+
+@pytest.mark.parametrize("K,N,bs,zp,M", [
+    (24576, 3072, 128, True, 3),   # Gemma-7B's down projection: 4 rows built, 3 used
+    (24576, 3072, 128, True, 4),
+    (18944, 3584, 128, True, 4),   # Qwen2-7B's: a shorter last segment
+    (11008, 4096, 32, False, 4),   # a block scale per step (8 steps per wavefront)
+    (14336, 4096, 64, False, 3),
+    (5120, 5120, 128, True, 4),    # the shortest rows the 4-row segments take
+])
+def test_k_segments_four_rows(pkg, orc, cuda, K, N, bs, zp, M):
+    """3 or 4 rows on narrow weights with rows of at least 5120: the
+    segmented GEMV's 4-row launch, ahead of the small-M MFMA decode; the
+    same checks as for 1 or 2 rows."""
+    _check_segments(pkg, orc, cuda, K, N, bs, zp, M)
+
+
 @pytest.mark.parametrize("K,N", [(11008, 4096), (18944, 3584)])
-@pytest.mark.parametrize("M", [4, 8, 16])
+@pytest.mark.parametrize("M", [8, 16])
 def test_small_m_decode_uneven_units(pkg, orc, cuda, K, N, M):
     """The small-M MFMA decode on unit counts with no even division into a
     few runs: Llama-2-7B's down projection (K = 11008: 43 units, prime) and
     Qwen2-7B's (K = 18944: 74 units), split into runs of one length and a
-    shorter last run whose trailing wavefronts add nothing. Sampled columns
-    against the fp64 oracle, bit-identical from run to run."""
+    shorter last run whose trailing wavefronts add nothing (at 4 rows and
+    fewer these shapes take K segments). Sampled columns against the fp64
+    oracle, bit-identical from run to run."""
     import torch
     bs = 128
     p = pkg.workloads.Projection("uneven", K, N, bs, True, 1.0, 0.005, 0.02)

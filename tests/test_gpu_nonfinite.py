@@ -13,8 +13,8 @@ must be bit-identical to the same kernel's run without the non-finite values
 
 "mixed" puts +inf and -inf into one row, so that both signs and NaN occur
 among its outputs. Rows too long for one workgroup (K = 20480) take the
-fragment-ordered GEMV with K segments at M <= 2: there the +inf and the -inf
-of "mixed" fall into different segments.
+fragment-ordered GEMV with K segments at M = 1, 2 and 4: there the +inf and
+the -inf of "mixed" fall into different segments.
 """
 import numpy as np
 import pytest
@@ -108,11 +108,11 @@ def test_non_finite_rows(pkg, orc, cuda, cfg, M, bad):
     _check_row(pkg, orc, cuda, p.K, p.N, p.block_size, B, S, Z, A, M, bad, cfg)
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 4])
 @pytest.mark.parametrize("bad", BADS)
 def test_non_finite_rows_k_segments(pkg, orc, cuda, M, bad):
-    """Rows too long for one workgroup (K = 20480): the fragment-ordered GEMV
-    splits K into segments, each giving the reference's sum over its part of
+    """Rows too long for one workgroup (K = 20480; at 4 rows on these narrow
+    weights as well): the fragment-ordered GEMV splits K into segments, each giving the reference's sum over its part of
     the row, and the ordered sum of the segments keeps the reference's kinds
     ("mixed" puts its +inf and -inf into different segments)."""
     W = pkg.workloads
