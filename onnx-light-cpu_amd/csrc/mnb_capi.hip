@@ -616,7 +616,7 @@ static bool UsesFragDecode(const mnb_plan *plan, int64_t M) {
 }
 
 // The K-segmented fragment-ordered GEMV (1 or 2 rows too long for one
-// workgroup, 3 or 4 long rows on narrow weights): plain plans (its sums pass has no gate/up pairing), no RMSNorm
+// workgroup, 2 to 4 long rows on narrow weights): plain plans (its sums pass has no gate/up pairing), no RMSNorm
 // input (a segment sees only its part of each row's sum of squares).
 static bool UsesFragSegments(const mnb_plan *plan, int64_t M, bool rms) {
   return !rms && !plan->gate_up && mnb::GemvFragSegSupports(plan->view, M);
@@ -627,8 +627,8 @@ static bool UsesFragSegments(const mnb_plan *plan, int64_t M, bool rms) {
 // kDecFragGroups: a compact plan without the small-M kernel's workspace runs
 // the fragment-ordered GEMV on consecutive groups of up to 4 rows.
 // kDecGemvFragSeg: the fragment-ordered GEMV with K split into segments, for
-// 1 or 2 rows too long for one workgroup (and for GemvM1Kernel), and 3 or 4
-// rows of K >= 5120 on weights up to 192 Mi elements.
+// 1 or 2 rows too long for one workgroup (and for GemvM1Kernel), and 2 to 4
+// rows of K >= 5120 on weights up to 192 Mi elements (2 rows from 48 Mi).
 enum DecodeKernel {
   kDecM1, kDecGemvFrag, kDecFrag, kDecMfma, kDecSmallM, kDecGemv, kDecFragGroups, kDecGemvFragSeg
 };
@@ -646,8 +646,9 @@ static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
 // its 64-row groups cover most CUs (a fused RMSNorm input at M = 1 too); M = 1
 // otherwise GemvM1Kernel. Rows too long for both (K > 16384 at M = 1, K >
 // 8192 at M = 2) take that MFMA kernel with K segments when the workspace
-// holds their partial sums (plain plans, no RMSNorm input), and so do 3 or 4
-// rows of K >= 5120 on narrow weights, ahead of the small-M MFMA decode.
+// holds their partial sums (plain plans, no RMSNorm input), and so do 2 to 4
+// rows of K >= 5120 on narrow weights (2 rows from 48 Mi elements), ahead of
+// the small-M MFMA decode and the fp32-FMA GEMV.
 static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void *work,
                                      size_t work_bytes, bool rms = false) {
   if (mnb::GemvFragPreferred(plan->view, M, rms)) return kDecGemvFrag;

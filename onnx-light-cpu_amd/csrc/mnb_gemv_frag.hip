@@ -64,8 +64,8 @@
 //
 // K segments. Rows longer than 16 wavefronts of 32 steps (K > 16384) do not
 // fit one workgroup, and GemvM1Kernel (whose activation row must fit its LDS)
-// does not take them either. For up to 2 rows (and for 3 or 4 rows of
-// K >= 5120 on weights up to 192 Mi elements, below) the launch splits K into
+// does not take them either. For up to 2 rows (and for 2 to 4 rows of
+// K >= 5120 on narrow weights, below) the launch splits K into
 // `segs` segments of whole units, all of one length but the last (shorter
 // when the units do not divide evenly: its wavefronts past the row's end read
 // only zeros beyond the weights' buffers and add nothing): workgroup
@@ -90,6 +90,10 @@
 // K = 8192, N = 8192 11.7 against 13.5. Not for K <= 4096 (K = N = 4096:
 // 8.0 against 7.1, the second launch) nor for the largest weights (K = 8192,
 // N = 28672: 33.3 against 31.0; K = 28672, N = 8192: 33.1 against 32.3).
+// At 2 rows they beat GemvSmallMKernel, the fp32-FMA GEMV, on such weights
+// of 48 Mi elements and more: K = 5120, N = 13824 11.9 us against 17.0;
+// K = N = 8192 11.1 against 14.1 (K = 8192, N = 3072: 7.8 against 7.3;
+// K = N = 6144: 10.0 against 9.6).
 #include "mnb_decode_common.h"
 
 #include <algorithm>
@@ -685,12 +689,16 @@ bool GemvFragSegSupports(const WeightView &w, int64_t M) {
   // rows of at least 5120 on weights of at most 192 Mi elements, where the
   // segments beat the small-M MFMA decode (shorter rows pay more for the
   // partial sums' second launch than they gain; the largest weights fill the
-  // CUs with the decode's own split).
+  // CUs with the decode's own split); 2 such rows on weights of at least
+  // 48 Mi elements, where they beat the fp32-FMA GEMV.
   if (M < 1 || M > 4 || w.Bp == nullptr || w.Sd == nullptr || (w.has_zp && w.Zd == nullptr) ||
       w.block_size < 32 || w.block_size > 256 || (w.block_size & (w.block_size - 1)) != 0 ||
       (w.K % gf::kUnitK) != 0)
     return false;
-  if (M <= 2 ? gf::PickSpw(w, M) > 0 : (w.K < 5120 || w.K * w.N > (int64_t{192} << 20)))
+  const int64_t kn = w.K * w.N;
+  const bool long_narrow = w.K >= 5120 && kn <= (int64_t{192} << 20);
+  const bool too_long = M <= 2 && gf::PickSpw(w, M) == 0;
+  if (!too_long && !(M >= 3 && long_narrow) && !(M == 2 && long_narrow && kn >= (int64_t{48} << 20)))
     return false;
   // K <= 2^20: the offsets of wavefronts past the end of a shorter last
   // segment (up to one segment beyond the row and the weights' buffers) stay

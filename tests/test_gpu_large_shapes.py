@@ -109,11 +109,13 @@ def test_k_segments_long_rows(pkg, orc, cuda, K, N, M):
     (11008, 4096, 32, False, 4),   # a block scale per step (8 steps per wavefront)
     (14336, 4096, 64, False, 3),
     (5120, 5120, 128, True, 4),    # the shortest rows the 4-row segments take
+    (8192, 8192, 128, True, 2),    # 2 rows: weights of 48 Mi elements and more
+    (5120, 13824, 64, False, 2),
 ])
-def test_k_segments_four_rows(pkg, orc, cuda, K, N, bs, zp, M):
-    """3 or 4 rows on narrow weights with rows of at least 5120: the
-    segmented GEMV's 4-row launch, ahead of the small-M MFMA decode; the
-    same checks as for 1 or 2 rows."""
+def test_k_segments_narrow_weights(pkg, orc, cuda, K, N, bs, zp, M):
+    """2 to 4 rows on narrow weights with rows of at least 5120: the
+    segmented GEMV (its 4-row launch for 3 or 4), ahead of the small-M MFMA
+    decode and the fp32-FMA GEMV; the same checks as for longer rows."""
     _check_segments(pkg, orc, cuda, K, N, bs, zp, M)
 
 
