@@ -593,19 +593,28 @@ inline int PickSpw(const WeightView &w, int64_t M) {
   return 0;
 }
 
-// K segments for 1 or 2 rows too long for one workgroup: for 2, 3, ... 16
-// segments asked for, steps per wavefront in PickSpw's order, the segment
-// length rounded up to whole units and whole wavefronts (the last segment
-// takes the rest), every wavefront wholly inside the row or past its end; the
-// first shape with at most 16 wavefronts, the LDS image of one segment within
-// the limit, and groups x segments covering 85% of the CUs (any count at 16
-// asked for). segs = 0: none.
+// K segments: for 2, 3, ... 16 segments asked for, steps per wavefront in
+// PickSpw's order, the segment length rounded up to whole units and whole
+// wavefronts (the last segment takes the rest), every wavefront wholly inside
+// the row or past its end; among the shapes with at most 16 wavefronts and
+// the LDS image of one segment within the limit, the least work on the
+// busiest CU: ceil(groups x segs / CUs) workgroups of `steps` steps, each
+// costing 16 steps more for its staging, sums and launch share, fewer
+// segments on a tie. Against the first shape covering 85% of the CUs:
+// K = 27648, N = 5120 at M = 2 6 segments of 144 steps instead of 4 of 224
+// (64 CUs with two workgroups), 22.7 -> 19.9 us; K = 8192, N = 10240 at
+// M = 2 3 segments of 88 steps instead of 2 of 128, 14.9 -> 13.0 us;
+// K = 20480, N = 512 at M = 1 (8 groups) 16 segments of 40 steps instead of
+// 14 of 48, 6.46 -> 6.65 us. segs = 0: none.
 struct SegShape {
   int segs = 0, steps = 0, spw = 0;
 };
 inline SegShape SegmentShape(const WeightView &w, int64_t M) {
   const int T = static_cast<int>(w.K / 32);
   const int64_t groups = (w.N + 63) / 64;
+  const int64_t cus = std::max<int64_t>(1, w.num_cus);
+  SegShape best;
+  int64_t best_cost = 0;
   for (int sg = 2; sg <= 16; ++sg) {
     for (int spw : {16, 32, 8}) {
       if ((M > 1 && spw == 32) || T % spw != 0) continue;  // the launches built for M > 1
@@ -614,15 +623,18 @@ inline SegShape SegmentShape(const WeightView &w, int64_t M) {
       const int steps = ((T + sg - 1) / sg + gran - 1) / gran * gran;
       const int segs = (T + steps - 1) / steps;
       if (segs < 2 || steps / spw > kMaxWaves) continue;
-      if (sg < 16 && groups * segs * 100 < static_cast<int64_t>(w.num_cus) * 85) continue;
       const int seg_nb = steps * 32 / static_cast<int>(w.block_size);
       if (static_cast<size_t>(Layout(32 * steps, seg_nb, steps / spw, RowsBuilt(M)).bytes) >
           kLdsLimit)
         continue;
-      return SegShape{segs, steps, spw};
+      const int64_t cost = (groups * segs + cus - 1) / cus * (steps + 16);
+      if (best.segs == 0 || cost < best_cost || (cost == best_cost && segs < best.segs)) {
+        best = SegShape{segs, steps, spw};
+        best_cost = cost;
+      }
     }
   }
-  return SegShape{};
+  return best;
 }
 
 // Steps per wavefront with an RMSNorm input (0: none): M = 1 as PickSpw
