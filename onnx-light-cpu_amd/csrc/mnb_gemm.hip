@@ -1484,6 +1484,30 @@ bool PrefillSupportsM(const WeightView &w, int64_t M) {
          (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN) * kMaxSplits < (int64_t{1} << 31);
 }
 
+// Whether the streaming kernel's launch for M rows (M > 32) holds more than
+// three workgroups per CU: each workgroup stages its K segment of every
+// activation row, so with three or four 16-row token groups such launches
+// fall behind the prefill kernel's 128 x 256 tiles, from 33 rows when K is
+// split (the partial sums add their own traffic), from 49 when it is not.
+// Measured on MI355X, us per call at M = 33 / 48 / 64, streaming against
+// prefill: K = 5120, N = 13824 (1080 workgroups)
+// 35.5 / 37.3 / 45.7 against 29.4 / 31.0 / 32.2; K = 3584, N = 18944 (2072)
+// 29.5 / 32.5 / 45.8 against 28.5 / 30.0 / 31.7; K = 28672, N = 8192 (896)
+// 74.1 / 75.7 / 89.5 against 68.7 / 71.7 / 74.5; K = 8192, N = 28672 (896)
+// 68.3 / 70.4 / 83.2 against 66.9 / 65.4 / 73.8; K = 8192, N = 128256
+// (4008) 257 / 264 / 317 against 242 / 248 / 253; K = 4096, N = 128256
+// (2004, one segment) 127.8 / 129.6 / 155.3 against 130.9 / 134.3 / 137.7.
+// Launches of
+// up to 1.75 workgroups per CU stay faster streamed (K = 4096, N = 28672:
+// 34.5 / 34.8 / 41.2 against 39.3 / 40.9 / 41.5; c2, c4, K = N = 8192,
+// K = 14336, N = 4096 and K = 24576, N = 3072 by 15-40%).
+bool StreamCrowded(const WeightView &w, int64_t M) {
+  const StreamShape sh = PickStreamShape(w, 0, 0);
+  const int64_t groups = (w.N + kSGroupRows - 1) / kSGroupRows;
+  return M > 32 && sh.segs > 0 && (sh.segs > 1 || M > 48) &&
+         groups * sh.segs > 3 * static_cast<int64_t>(w.num_cus);
+}
+
 // The prefill kernel serves the automatic GEMM path
 // - when its 128 x 256 tiles alone fill at least one wave of CUs and the
 //   last wave is at least half full: no split-K, one workgroup per CU (c5
@@ -1498,9 +1522,10 @@ bool PrefillSupportsM(const WeightView &w, int64_t M) {
 // 162.7 -> 125.9, c4 60.2 -> 52.6; M = 512 qkv 55.1 -> 46.3, down 96.4 ->
 // 77.2, o and c4 within 3%; M = 256 gate+up 84.8 -> 63.8, qkv 34.6 -> about
 // 32, down 56.8 -> 50.0; with fewer than 12 k-tiles per split (o and c4 at
-// M <= 256, qkv at M = 128) GemmKernel's smaller tiles were 1-2 us faster.
+// M <= 256, qkv at M = 128) GemmKernel's smaller tiles were 1-2 us faster;
+// - from 33 rows where the streaming kernel's launch is crowded (above).
 bool UsePrefill(const WeightView &w, int64_t M) {
-  if (M < 65 || !PrefillSupportsM(w, M)) return false;
+  if (!PrefillSupportsM(w, M) || (M < 65 && !StreamCrowded(w, M))) return false;
   const int64_t tiles = (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN);
   const int64_t cus = w.num_cus;
   if (tiles < cus) {
@@ -1517,6 +1542,7 @@ size_t PrefillPartialBytes(const WeightView &w, int64_t M) {
 
 bool StreamSupportsM(const WeightView &w, int64_t M) {
   if (M < 17 || M > 64 || !PrefillSupportsShape(w) || w.K > (int64_t{1} << 22)) return false;
+  if (StreamCrowded(w, M)) return false;
   const StreamShape sh = PickStreamShape(w, 0, 0);
   return sh.segs > 0 && (!sh.ragged || M <= 32);  // shorter last segment: up to 32 rows
 }

@@ -1,7 +1,7 @@
 """GPU: parity at the largest shapes the configurations reach.
 
 Llama-3-8B's LM head (K = 4096, N = 128256: 2004 row groups, 282 MB of
-constants) at decode and prefill row counts, and a long K (65536, 256 units
+constants) at decode, streaming and prefill row counts, and a long K (65536, 256 units
 per row) on narrow weights. Output column n of MatMulNBits depends only on
 weight row n, so each case checks a seeded sample of columns against the
 fp64 oracle run on the same rows of B, scales and zero points, at the bound
@@ -46,7 +46,8 @@ def _check_sampled(pkg, orc, cuda, K, N, bs, zp, Ms, seed, ncols=512):
 
 
 def test_lm_head_shape(pkg, orc, cuda):
-    _check_sampled(pkg, orc, cuda, 4096, 128256, 128, True, (1, 3, 16, 130), seed=8128)
+    # 48 rows streamed in one segment, 64 through the prefill kernel
+    _check_sampled(pkg, orc, cuda, 4096, 128256, 128, True, (1, 3, 16, 48, 64, 130), seed=8128)
 
 
 def test_long_k_narrow_weights(pkg, orc, cuda):
@@ -147,3 +148,22 @@ def test_small_m_decode_uneven_units(pkg, orc, cuda, K, N, M):
         assert err <= GEMV_TOL
     finally:
         op.release()
+
+
+@pytest.mark.parametrize("K,N", [(3584, 18944), (5120, 13824)])
+def test_crowded_streaming_launches_take_prefill(pkg, orc, cuda, K, N):
+    """Weights whose streaming-GEMM launch holds more than three workgroups
+    per CU (K = 3584, N = 18944: 7 segments x 296 groups; K = 5120,
+    N = 13824: 5 x 216): streamed up to 32 rows, the prefill kernel (split
+    K) from 33. Sampled columns against the fp64 oracle on each side."""
+    import torch  # noqa: F401  (the device tensors)
+    p = pkg.workloads.Projection("crowded", K, N, 128, True, 1.0, 0.005, 0.02)
+    op = pkg.MatMulNBits(K, N, 4, 128).prepare(*pkg.workloads.make_weights(p, K))
+    try:
+        names = {M: op.kernel_name(M) for M in (17, 32, 33, 64)}
+        print(f"case crowded stream K={K} N={N}: {names}", flush=True)
+        assert names[17] == names[32] == "StreamKernel"
+        assert names[33] == names[64] == "PrefillKernel"
+    finally:
+        op.release()
+    _check_sampled(pkg, orc, cuda, K, N, 128, True, (32, 33, 64), seed=K + 1)
