@@ -648,14 +648,15 @@ static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
 // 8192 at M = 2) take that MFMA kernel with K segments when the workspace
 // holds their partial sums (plain plans, no RMSNorm input), and so do 2 to 4
 // rows of K >= 5120 on narrow weights (2 rows from 48 Mi elements), ahead of
-// the small-M MFMA decode and the fp32-FMA GEMV.
+// the small-M MFMA decode and the fp32-FMA GEMV, and wide weights whose
+// single-workgroup launch would leave a second round on a few CUs.
 static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void *work,
                                      size_t work_bytes, bool rms = false) {
-  if (mnb::GemvFragPreferred(plan->view, M, rms)) return kDecGemvFrag;
-  if (M == 1 && mnb::GemvM1Supports(plan->view)) return kDecM1;
   if (UsesFragSegments(plan, M, rms) &&
       HasWorkspace(work, work_bytes, mnb::GemvFragSegWorkspaceBytes(plan->view, M)))
     return kDecGemvFragSeg;
+  if (mnb::GemvFragPreferred(plan->view, M, rms)) return kDecGemvFrag;
+  if (M == 1 && mnb::GemvM1Supports(plan->view)) return kDecM1;
   if (UsesFragDecode(plan, M) &&
       HasWorkspace(work, work_bytes, mnb::DecodeFragWorkspaceBytes(plan->view, M)))
     return kDecFrag;
@@ -682,9 +683,9 @@ static bool DecodeTakesRms(const mnb_plan *plan, DecodeKernel k) {
 // Workspace bytes the decode kernel PickDecodeKernel chooses for M rows when
 // the caller passes enough: 0 for the kernels that need none.
 static size_t DecodeNeed(const mnb_plan *plan, int64_t M, bool rms = false) {
+  if (UsesFragSegments(plan, M, rms)) return mnb::GemvFragSegWorkspaceBytes(plan->view, M);
   if (mnb::GemvFragPreferred(plan->view, M, rms)) return 0;
   if (M == 1 && mnb::GemvM1Supports(plan->view)) return 0;
-  if (UsesFragSegments(plan, M, rms)) return mnb::GemvFragSegWorkspaceBytes(plan->view, M);
   if (UsesFragDecode(plan, M)) return mnb::DecodeFragWorkspaceBytes(plan->view, M);
   if (!mnb::DecodeFragSupports(plan->view, M) && UsesMfmaDecode(plan, M))
     return mnb::GemvMfmaWorkspaceBytes(plan->view, M);

@@ -609,6 +609,9 @@ inline int PickSpw(const WeightView &w, int64_t M) {
 struct SegShape {
   int segs = 0, steps = 0, spw = 0;
 };
+inline int64_t SegCost(int64_t groups, int segs, int steps, int64_t cus) {
+  return (groups * segs + cus - 1) / cus * (steps + 16);
+}
 inline SegShape SegmentShape(const WeightView &w, int64_t M) {
   const int T = static_cast<int>(w.K / 32);
   const int64_t groups = (w.N + 63) / 64;
@@ -627,7 +630,7 @@ inline SegShape SegmentShape(const WeightView &w, int64_t M) {
       if (static_cast<size_t>(Layout(32 * steps, seg_nb, steps / spw, RowsBuilt(M)).bytes) >
           kLdsLimit)
         continue;
-      const int64_t cost = (groups * segs + cus - 1) / cus * (steps + 16);
+      const int64_t cost = SegCost(groups, segs, steps, cus);
       if (best.segs == 0 || cost < best_cost || (cost == best_cost && segs < best.segs)) {
         best = SegShape{segs, steps, spw};
         best_cost = cost;
@@ -695,6 +698,21 @@ hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float 
                          : gf::LaunchZp<false>(w, m, A, Y, s, spw, win, H, bias, gamma, eps);
 }
 
+// Wide weights whose single-workgroup launch (one per 64-row group, one per
+// CU at a time) leaves a second round on a few CUs: K segments when the
+// busiest CU's work (SegmentShape's measure, the sum pass counted as 60
+// steps) drops by more than 10%. Measured at M = 1: K = 7168, N = 18432
+// (288 groups) 18.2 -> 16.3 us with 4 segments; the shapes it takes have
+// 272 to 384 groups and rows of 7168 and more.
+static bool SegmentsBalance(const WeightView &w, int64_t M) {
+  if (!GemvFragPreferred(w, M, false)) return false;
+  const gf::SegShape sh = gf::SegmentShape(w, M);
+  if (sh.segs < 2) return false;
+  const int64_t groups = (w.N + 63) / 64, cus = std::max<int64_t>(1, w.num_cus);
+  const int64_t single = gf::SegCost(groups, 1, static_cast<int>(w.K / 32), cus);
+  return (gf::SegCost(groups, sh.segs, sh.steps, cus) + 60) * 10 < single * 9;
+}
+
 bool GemvFragSegSupports(const WeightView &w, int64_t M) {
   // As GemvFragSupports, K split into segments of whole units: 1 or 2 rows
   // too long for one workgroup (no single-workgroup launch fits); 3 or 4
@@ -710,7 +728,8 @@ bool GemvFragSegSupports(const WeightView &w, int64_t M) {
   const int64_t kn = w.K * w.N;
   const bool long_narrow = w.K >= 5120 && kn <= (int64_t{192} << 20);
   const bool too_long = M <= 2 && gf::PickSpw(w, M) == 0;
-  if (!too_long && !(M >= 3 && long_narrow) && !(M == 2 && long_narrow && kn >= (int64_t{48} << 20)))
+  if (!too_long && !(M >= 3 && long_narrow) &&
+      !(M == 2 && long_narrow && kn >= (int64_t{48} << 20)) && !SegmentsBalance(w, M))
     return false;
   // K <= 2^20: the offsets of wavefronts past the end of a shorter last
   // segment (up to one segment beyond the row and the weights' buffers) stay

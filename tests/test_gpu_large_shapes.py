@@ -54,7 +54,8 @@ def test_long_k_narrow_weights(pkg, orc, cuda):
     _check_sampled(pkg, orc, cuda, 65536, 320, 64, True, (1, 2, 8, 40, 100), seed=6553)
 
 
-def _check_segments(pkg, orc, cuda, K, N, bs, zp, M):
+def _check_segments(pkg, orc, cuda, K, N, bs, zp, M,
+                    fallbacks=("GemvKernel", "GemvSmallMKernel")):
     import ctypes
     import torch
     p = pkg.workloads.Projection("long", K, N, bs, zp, 1.0, 0.005, 0.02)
@@ -69,7 +70,7 @@ def _check_segments(pkg, orc, cuda, K, N, bs, zp, M):
         print(f"case k-segments K={K} N={N} bs={bs} zp={zp} M={M} kernel={op.kernel_name(M)} "
               f"(no workspace: {op.kernel_name(M, 0)})", flush=True)
         assert op.kernel_name(M) == "GemvFragKernel (K segments)"
-        assert op.kernel_name(M, 0) in ("GemvKernel", "GemvSmallMKernel")
+        assert op.kernel_name(M, 0) in fallbacks
         dA = torch.from_numpy(A).to(cuda)
         Y = op(dA).cpu().numpy()
         np.testing.assert_array_equal(op(dA).cpu().numpy(), Y)
@@ -118,6 +119,18 @@ def test_k_segments_narrow_weights(pkg, orc, cuda, K, N, bs, zp, M):
     segmented GEMV (its 4-row launch for 3 or 4), ahead of the small-M MFMA
     decode and the fp32-FMA GEMV; the same checks as for longer rows."""
     _check_segments(pkg, orc, cuda, K, N, bs, zp, M)
+
+
+@pytest.mark.parametrize("K,N,bs,zp,M", [
+    (7168, 18432, 128, True, 1),   # 288 groups: one workgroup per group leaves 32 CUs a second
+    (8192, 18432, 64, False, 2),
+    (14336, 24576, 128, True, 1),  # 384 groups, 2 segments
+])
+def test_k_segments_balance_wide_weights(pkg, orc, cuda, K, N, bs, zp, M):
+    """Wide weights whose one-workgroup-per-group launch leaves a second
+    round on some CUs: K segments spread the work (without the workspace
+    the single-workgroup launch serves them); the same checks as above."""
+    _check_segments(pkg, orc, cuda, K, N, bs, zp, M, fallbacks=("GemvFragKernel",))
 
 
 @pytest.mark.parametrize("K,N", [(11008, 4096), (18944, 3584)])
