@@ -649,14 +649,19 @@ static bool HasWorkspace(const void *work, size_t bytes, size_t need) {
 // holds their partial sums (plain plans, no RMSNorm input), and so do 2 to 4
 // rows of K >= 5120 on narrow weights (2 rows from 48 Mi elements), ahead of
 // the small-M MFMA decode and the fp32-FMA GEMV, and wide weights whose
-// single-workgroup launch would leave a second round on a few CUs.
+// single-workgroup launch would leave a second round on a few CUs. Wide
+// weights with rows too long for one workgroup take the segments ahead of
+// GemvM1Kernel (K = 11008, N = 17408: 22.9 against 29.5 us; K = 13824,
+// N = 20480 31.8 against 38.4; K = 8960, N = 14336 16.4 against 19.4);
+// narrower ones keep it (K = 11008, N = 4096 and K = 13824, N = 5120).
 static DecodeKernel PickDecodeKernel(const mnb_plan *plan, int64_t M, const void *work,
                                      size_t work_bytes, bool rms = false) {
-  if (UsesFragSegments(plan, M, rms) &&
-      HasWorkspace(work, work_bytes, mnb::GemvFragSegWorkspaceBytes(plan->view, M)))
-    return kDecGemvFragSeg;
-  if (mnb::GemvFragPreferred(plan->view, M, rms)) return kDecGemvFrag;
+  const bool segs = UsesFragSegments(plan, M, rms) &&
+                    HasWorkspace(work, work_bytes, mnb::GemvFragSegWorkspaceBytes(plan->view, M));
+  if (mnb::GemvFragPreferred(plan->view, M, rms)) return segs ? kDecGemvFragSeg : kDecGemvFrag;
+  if (segs && mnb::GemvFragWide(plan->view)) return kDecGemvFragSeg;
   if (M == 1 && mnb::GemvM1Supports(plan->view)) return kDecM1;
+  if (segs) return kDecGemvFragSeg;
   if (UsesFragDecode(plan, M) &&
       HasWorkspace(work, work_bytes, mnb::DecodeFragWorkspaceBytes(plan->view, M)))
     return kDecFrag;
@@ -683,9 +688,12 @@ static bool DecodeTakesRms(const mnb_plan *plan, DecodeKernel k) {
 // Workspace bytes the decode kernel PickDecodeKernel chooses for M rows when
 // the caller passes enough: 0 for the kernels that need none.
 static size_t DecodeNeed(const mnb_plan *plan, int64_t M, bool rms = false) {
-  if (UsesFragSegments(plan, M, rms)) return mnb::GemvFragSegWorkspaceBytes(plan->view, M);
-  if (mnb::GemvFragPreferred(plan->view, M, rms)) return 0;
+  const bool segs = UsesFragSegments(plan, M, rms);
+  if (mnb::GemvFragPreferred(plan->view, M, rms))
+    return segs ? mnb::GemvFragSegWorkspaceBytes(plan->view, M) : 0;
+  if (segs && mnb::GemvFragWide(plan->view)) return mnb::GemvFragSegWorkspaceBytes(plan->view, M);
   if (M == 1 && mnb::GemvM1Supports(plan->view)) return 0;
+  if (segs) return mnb::GemvFragSegWorkspaceBytes(plan->view, M);
   if (UsesFragDecode(plan, M)) return mnb::DecodeFragWorkspaceBytes(plan->view, M);
   if (!mnb::DecodeFragSupports(plan->view, M) && UsesMfmaDecode(plan, M))
     return mnb::GemvMfmaWorkspaceBytes(plan->view, M);

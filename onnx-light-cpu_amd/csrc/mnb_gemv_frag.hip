@@ -673,13 +673,16 @@ bool GemvFragShapeOk(const WeightView &w, int64_t M, int spw, int win) {
                                                   win == 0 ? 8 : win);
 }
 
+bool GemvFragWide(const WeightView &w) {
+  return ((w.N + 63) / 64) * 100 >= static_cast<int64_t>(w.num_cus) * 85;
+}
+
 bool GemvFragPreferred(const WeightView &w, int64_t M, bool rms) {
   // One workgroup per 64-row group: worth it where the groups cover most of
   // the CUs. The RMSNorm input: not 32 steps per wavefront with 32-k blocks
   // (the launch that would spill registers).
   if (rms && gf::RmsSpw(w, M) == 0) return false;
-  return GemvFragSupports(w, M) &&
-         ((w.N + 63) / 64) * 100 >= static_cast<int64_t>(w.num_cus) * 85;
+  return GemvFragSupports(w, M) && GemvFragWide(w);
 }
 
 hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s,
@@ -705,7 +708,6 @@ hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float 
 // (288 groups) 18.2 -> 16.3 us with 4 segments; the shapes it takes have
 // 272 to 384 groups and rows of 7168 and more.
 static bool SegmentsBalance(const WeightView &w, int64_t M) {
-  if (!GemvFragPreferred(w, M, false)) return false;
   const gf::SegShape sh = gf::SegmentShape(w, M);
   if (sh.segs < 2) return false;
   const int64_t groups = (w.N + 63) / 64, cus = std::max<int64_t>(1, w.num_cus);
@@ -728,8 +730,9 @@ bool GemvFragSegSupports(const WeightView &w, int64_t M) {
   const int64_t kn = w.K * w.N;
   const bool long_narrow = w.K >= 5120 && kn <= (int64_t{192} << 20);
   const bool too_long = M <= 2 && gf::PickSpw(w, M) == 0;
-  if (!too_long && !(M >= 3 && long_narrow) &&
-      !(M == 2 && long_narrow && kn >= (int64_t{48} << 20)) && !SegmentsBalance(w, M))
+  if (GemvFragPreferred(w, M, false) ? !SegmentsBalance(w, M)
+                                     : !too_long && !(M >= 3 && long_narrow) &&
+                                           !(M == 2 && long_narrow && kn >= (int64_t{48} << 20)))
     return false;
   // K <= 2^20: the offsets of wavefronts past the end of a shorter last
   // segment (up to one segment beyond the row and the weights' buffers) stay

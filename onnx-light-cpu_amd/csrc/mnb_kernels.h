@@ -141,6 +141,8 @@ bool GemvFragShapeOk(const WeightView &w, int64_t M, int steps_per_wave, int win
 // Whether the auto path takes it: its groups cover most CUs (with `rms`, for
 // a fused RMSNorm input).
 bool GemvFragPreferred(const WeightView &w, int64_t M, bool rms = false);
+// Whether the 64-row groups cover 85% of the CUs (one workgroup per group).
+bool GemvFragWide(const WeightView &w);
 hipError_t LaunchGemvFrag(const WeightView &w, int64_t M, const float *A, float *Y, hipStream_t s,
                           int steps_per_wave, int window, float *H, const float *bias,
                           const float *gamma = nullptr, float eps = 0.0f);

@@ -121,16 +121,18 @@ def test_k_segments_narrow_weights(pkg, orc, cuda, K, N, bs, zp, M):
     _check_segments(pkg, orc, cuda, K, N, bs, zp, M)
 
 
-@pytest.mark.parametrize("K,N,bs,zp,M", [
-    (7168, 18432, 128, True, 1),   # 288 groups: one workgroup per group leaves 32 CUs a second
-    (8192, 18432, 64, False, 2),
-    (14336, 24576, 128, True, 1),  # 384 groups, 2 segments
+@pytest.mark.parametrize("K,N,bs,zp,M,fallback", [
+    (7168, 18432, 128, True, 1, "GemvFragKernel"),   # 288 groups: one workgroup per group
+    (8192, 18432, 64, False, 2, "GemvFragKernel"),   # leaves 32 CUs a second round
+    (14336, 24576, 128, True, 1, "GemvFragKernel"),  # 384 groups, 2 segments
+    (11008, 17408, 128, True, 1, "GemvM1Kernel"),    # rows too long for one workgroup
 ])
-def test_k_segments_balance_wide_weights(pkg, orc, cuda, K, N, bs, zp, M):
+def test_k_segments_balance_wide_weights(pkg, orc, cuda, K, N, bs, zp, M, fallback):
     """Wide weights whose one-workgroup-per-group launch leaves a second
-    round on some CUs: K segments spread the work (without the workspace
-    the single-workgroup launch serves them); the same checks as above."""
-    _check_segments(pkg, orc, cuda, K, N, bs, zp, M, fallbacks=("GemvFragKernel",))
+    round on some CUs, or whose rows it cannot hold: K segments spread the
+    work (without the workspace the single-workgroup launch or the M = 1
+    GEMV serves them); the same checks as above."""
+    _check_segments(pkg, orc, cuda, K, N, bs, zp, M, fallbacks=(fallback,))
 
 
 @pytest.mark.parametrize("K,N", [(11008, 4096), (18944, 3584)])
