@@ -140,8 +140,9 @@ __global__ __launch_bounds__(64) void SplitActKernel(const float *__restrict__ A
   const int ch = threadIdx.x & 31;
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, M * K * 4, 0x00020000);
-  // tokens past M read past the end of the buffer: zeros
-  const int vo = t < M ? (t * K + kUnitK * u + 8 * ch) * 4 : M * K * 4;
+  // tokens past M, and k past K in a last unit that K does not fill, read
+  // past the end of the buffer: zeros
+  const int vo = t < M && kUnitK * u + 8 * ch < K ? (t * K + kUnitK * u + 8 * ch) * 4 : M * K * 4;
   floatx4 v0 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo, 0, 0));
   floatx4 v1 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, vo + 16, 0, 0));
   if constexpr (RMS) {
@@ -209,6 +210,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
   const int g = static_cast<int>(blockIdx.x) / segs;
   const int seg = static_cast<int>(blockIdx.x) - g * segs;
   const int T = K / 32;
+  const int Tp = (K + kUnitK - 1) / kUnitK * kUnitSteps;  // steps of whole units (image, exponents)
   const int u0 = (seg * wpg + wave) * U;  // first unit of this wavefront
   const int s0 = u0 * kUnitSteps;         // first step
 
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(Bp + static_cast<size_t>(g) * T * 1024), 0, T * 1024, 0x00020000);
   const __amdgpu_buffer_rsrc_t ri =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4 *>(img), 0, T * kSB, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4 *>(img), 0, Tp * kSB, 0x00020000);
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float *>(Sd + static_cast<size_t>(g) * nb * 64), 0, nb * 256, 0x00020000);
   const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
@@ -241,7 +243,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void DecodeFragKernel(
   // kTPL qd + kTPL - 1.
   int4 ue[U];
   const __amdgpu_buffer_rsrc_t re = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int *>(exps), 0, (T / kUnitSteps) * 64, 0x00020000);
+      const_cast<int *>(exps), 0, (Tp / kUnitSteps) * 64, 0x00020000);
 #pragma unroll
   for (int uu = 0; uu < U; ++uu) {
     if constexpr (TOKS == 16) {
@@ -442,9 +444,14 @@ struct Shape {
 // wavefronts past the last unit read only beyond the buffers of the weights,
 // scales, zero points, image and exponents (bounds-checked buffer loads:
 // zeros) and add exactly zero.
+// Units of 256 k; a K that is not a whole number of them ends in a last
+// unit whose steps past K read zero weights (beyond the group's records) and
+// zero activations (masked by SplitActKernel).
+inline int Units(const WeightView &w) { return static_cast<int>((w.K + kUnitK - 1) / kUnitK); }
+
 inline Shape PickShape(const WeightView &w, int wpg_req, int u_req) {
   const int64_t groups = (w.N + 63) / 64;
-  const int units = static_cast<int>(w.K / kUnitK);
+  const int units = Units(w);
   Shape sh{1, 1, units};
   if (wpg_req > 0 || u_req > 0) {
     sh.units_per_wave = u_req > 0 ? u_req : 1;
@@ -474,9 +481,11 @@ inline Shape PickShape(const WeightView &w, int wpg_req, int u_req) {
   return sh;
 }
 
-inline size_t ImageBytes(const WeightView &w) { return static_cast<size_t>(w.K / 32) * kStepBytes; }
+inline size_t ImageBytes(const WeightView &w) {
+  return static_cast<size_t>(Units(w)) * kUnitSteps * kStepBytes;
+}
 inline size_t ExpBytes(const WeightView &w) {
-  return (static_cast<size_t>(w.K / kUnitK) * kTok * 4 + 255) / 256 * 256;
+  return (static_cast<size_t>(Units(w)) * kTok * 4 + 255) / 256 * 256;
 }
 // The per-unit sums of squares of a fused RMSNorm input: the same size.
 inline size_t SqBytes(const WeightView &w) { return ExpBytes(w); }
@@ -534,7 +543,7 @@ hipError_t LaunchZp(const WeightView &w, int64_t M, const Work &wk, float *Y, fl
 } // namespace df
 
 bool DecodeFragLayoutWanted(const WeightView &w) {
-  return (w.K % df::kUnitK) == 0 && w.block_size >= 32 &&
+  return (w.K % 32) == 0 && w.block_size >= 32 &&
          (w.block_size & (w.block_size - 1)) == 0 && w.K <= (int64_t{1} << 24) &&
          w.N < (int64_t{1} << 22) && w.nb * 256 < (int64_t{1} << 31);
 }
@@ -559,7 +568,9 @@ bool DecodeFragSupports(const WeightView &w, int64_t M) {
          (w.K / 32) * df::kStepBytes < (int64_t{1} << 31);
 }
 
-bool DecodeFragTakesRms(const WeightView &w) { return w.K <= df::kMaxSqUnits * df::kUnitK; }
+bool DecodeFragTakesRms(const WeightView &w) {
+  return w.K <= df::kMaxSqUnits * df::kUnitK && (w.K % df::kUnitK) == 0;
+}
 
 size_t DecodeFragWorkspaceBytes(const WeightView &w, int64_t M, int wpg, int units_per_wave) {
   const df::Shape sh = df::PickShape(w, wpg, units_per_wave);
@@ -571,7 +582,7 @@ hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, floa
                             hipStream_t s, float *H, int wpg, int units_per_wave,
                             const float *bias, const float *gamma, float eps) {
   const df::Shape sh = df::PickShape(w, wpg, units_per_wave);
-  const int units = static_cast<int>(w.K / df::kUnitK);
+  const int units = df::Units(w);
   // every unit in a run, no run empty (the last may be shorter)
   if (sh.wpg < 1 || sh.wpg > df::kMaxWaves || sh.segs < 1 ||
       sh.segs * sh.wpg * sh.units_per_wave < units ||

@@ -195,7 +195,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) void GemvFragKernel(
   for (int p = 0; p < kPasses; ++p) {
     const int it = min(2 * p + (lane >> 5), kItems - 1);
     const int ul = it / MT, m = min(it % MT, M - 1);
-    const int off = (m * K + (u0 + ul) * kUnitK + 8 * (lane & 31)) * 4;
+    const int kk = (u0 + ul) * kUnitK + 8 * (lane & 31);
+    // SEG: k past a K that does not fill its last unit reads past the end
+    // of the buffer (zeros), not the next row
+    const int off = !SEG || kk < K ? (m * K + kk) * 4 : M * K * 4;
     va[p][0] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
     va[p][1] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16, 0, 0));
     if constexpr (RMS) {
@@ -613,7 +616,9 @@ inline int64_t SegCost(int64_t groups, int segs, int steps, int64_t cus) {
   return (groups * segs + cus - 1) / cus * (steps + 16);
 }
 inline SegShape SegmentShape(const WeightView &w, int64_t M) {
-  const int T = static_cast<int>(w.K / 32);
+  // steps of whole units: a K that does not fill its last unit ends in steps
+  // that read zeros (weights beyond the group's records, masked activations)
+  const int T = static_cast<int>((w.K + kUnitK - 1) / kUnitK * kUnitSteps);
   const int64_t groups = (w.N + 63) / 64;
   const int64_t cus = std::max<int64_t>(1, w.num_cus);
   SegShape best;
@@ -725,11 +730,15 @@ bool GemvFragSegSupports(const WeightView &w, int64_t M) {
   // 48 Mi elements, where they beat the fp32-FMA GEMV.
   if (M < 1 || M > 4 || w.Bp == nullptr || w.Sd == nullptr || (w.has_zp && w.Zd == nullptr) ||
       w.block_size < 32 || w.block_size > 256 || (w.block_size & (w.block_size - 1)) != 0 ||
-      (w.K % gf::kUnitK) != 0)
+      (w.K % 32) != 0)
     return false;
   const int64_t kn = w.K * w.N;
   const bool long_narrow = w.K >= 5120 && kn <= (int64_t{192} << 20);
-  const bool too_long = M <= 2 && gf::PickSpw(w, M) == 0;
+  // Rows too long for one workgroup; with a K that is not a whole number of
+  // units (no single-workgroup launch at all) those past the M = 1 GEMV's
+  // limit at M = 1 and past 8192 at M = 2, as for whole units.
+  const bool too_long =
+      M <= 2 && ((w.K % gf::kUnitK) != 0 ? w.K > (M == 1 ? 16384 : 8192) : gf::PickSpw(w, M) == 0);
   if (GemvFragPreferred(w, M, false) ? !SegmentsBalance(w, M)
                                      : !too_long && !(M >= 3 && long_narrow) &&
                                            !(M == 2 && long_narrow && kn >= (int64_t{48} << 20)))

@@ -104,8 +104,11 @@ __device__ __forceinline__ void DotHalf(const float *a, const uint32_t *hz, int 
 
 // Slice i of A: MT * 512 float4, thread t of the W-wavefront workgroup holds
 // slots s = 64 W p + t (W divides 8 MT):
-// token s / 512, chunk 64 i + (s / 8) % 64 (clamped to the last chunk),
-// float4 v = s % 8 of it; stored at LDS slot (token, chunk c, v ^ ((c ^ c >> 3) & 7)).
+// token s / 512, chunk 64 i + (s / 8) % 64 (zeros past the last chunk: the
+// load re-reads the last chunk in bounds, and its values, an infinity among
+// them, must not reach the products that the zero scale of those lanes
+// multiplies), float4 v = s % 8 of it; stored at LDS slot (token, chunk c,
+// v ^ ((c ^ c >> 3) & 7)).
 template <int MT, int W>
 __device__ __forceinline__ void LoadSlice(f32x4 (&st)[MT * 8 / W], const f32x4 *a4, int K4, int i,
                                           int nchunks) {
@@ -114,7 +117,8 @@ __device__ __forceinline__ void LoadSlice(f32x4 (&st)[MT * 8 / W], const f32x4 *
     const int sl = 64 * W * p + threadIdx.x;
     const int m = sl >> 9, cl = (sl >> 3) & 63, v = sl & 7;
     const int c = min(64 * i + cl, nchunks - 1);
-    st[p] = a4[static_cast<size_t>(m) * K4 + c * 8 + v];
+    const f32x4 x = a4[static_cast<size_t>(m) * K4 + c * 8 + v];
+    st[p] = 64 * i + cl < nchunks ? x : f32x4{0.f, 0.f, 0.f, 0.f};
   }
 }
 template <int MT, int W>

@@ -182,3 +182,32 @@ def test_crowded_streaming_launches_take_prefill(pkg, orc, cuda, K, N):
     finally:
         op.release()
     _check_sampled(pkg, orc, cuda, K, N, 128, True, (32, 33, 64), seed=K + 1)
+
+
+@pytest.mark.parametrize("K,N,bs,zp,kernels", [
+    # Qwen2.5-72B's down projection: 115.5 units of 256 k
+    (29568, 8192, 128, True, {1: "GemvFragKernel (K segments)", 2: "GemvFragKernel (K segments)",
+                              4: "DecodeFragKernel", 16: "DecodeFragKernel"}),
+    (20608, 512, 64, False, {1: "GemvFragKernel (K segments)", 2: "GemvFragKernel (K segments)",
+                             3: "GemvFragKernel (K segments)", 5: "DecodeFragKernel",
+                             16: "DecodeFragKernel"}),
+    (1152, 1024, 32, True, {8: "DecodeFragKernel", 16: "DecodeFragKernel"}),
+])
+def test_k_not_whole_units(pkg, orc, cuda, K, N, bs, zp, kernels):
+    """K that is not a multiple of 256 (the activation exponent's unit): the
+    last unit's steps past K read zero weights (beyond each group's records)
+    and zero activations (masked in the staging and the split pass), so the
+    fragment-ordered kernels serve these shapes; sampled columns against the
+    fp64 oracle at the decode bound, bit-identical from run to run."""
+    import torch
+    p = pkg.workloads.Projection("partial-unit", K, N, bs, zp, 1.0, 0.005, 0.02)
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(*pkg.workloads.make_weights(p, K + 3))
+    try:
+        names = {M: op.kernel_name(M) for M in kernels}
+        print(f"case partial unit K={K} N={N} bs={bs} zp={zp}: {names}", flush=True)
+        assert names == kernels
+        dA = torch.from_numpy(pkg.workloads.make_activations(2, K, 1.0, K)).to(cuda)
+        np.testing.assert_array_equal(op(dA).cpu().numpy(), op(dA).cpu().numpy())
+    finally:
+        op.release()
+    _check_sampled(pkg, orc, cuda, K, N, bs, zp, tuple(kernels), seed=K + 3)

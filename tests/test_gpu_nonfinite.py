@@ -120,3 +120,19 @@ def test_non_finite_rows_k_segments(pkg, orc, cuda, M, bad):
     B, S, Z = W.make_weights(p, 2048)
     A = W.make_activations(M, p.K, 1.0, 2049 + M)
     _check_row(pkg, orc, cuda, p.K, p.N, p.block_size, B, S, Z, A, M, bad, "K=20480 N=512")
+
+
+@pytest.mark.parametrize("K,M", [(20608, 1), (20608, 2), (20608, 3), (20608, 8), (1152, 1),
+                                 (1152, 2), (1152, 8)])
+@pytest.mark.parametrize("bad", BADS)
+def test_non_finite_rows_partial_unit(pkg, orc, cuda, K, M, bad):
+    """K = 20608 (80.5 units of 256 k, 10 slices of 2048 and part of an
+    eleventh) and 1152 (4.5 units): the K segments (M <= 3), the small-M
+    decode (M = 8), the M = 1 GEMV and the fp32-FMA kernels with a last unit
+    or slice that K partly fills ("mixed" puts its -inf there); the other
+    rows, and the tails past K, must stay finite."""
+    W = pkg.workloads
+    p = W.Projection("partial-unit", K, 512, 128, True, 1.0, 0.005, 0.02)
+    B, S, Z = W.make_weights(p, K + 2)
+    A = W.make_activations(M, p.K, 1.0, K + 3 + M)
+    _check_row(pkg, orc, cuda, p.K, p.N, p.block_size, B, S, Z, A, M, bad, f"K={K} N=512")
