@@ -1524,8 +1524,17 @@ bool StreamCrowded(const WeightView &w, int64_t M) {
 // 32, down 56.8 -> 50.0; with fewer than 12 k-tiles per split (o and c4 at
 // M <= 256, qkv at M = 128) GemmKernel's smaller tiles were 1-2 us faster;
 // - from 33 rows where the streaming kernel's launch is crowded (above).
+bool StreamSupportsM(const WeightView &w, int64_t M);
+
 bool UsePrefill(const WeightView &w, int64_t M) {
-  if (!PrefillSupportsM(w, M) || (M < 65 && !StreamCrowded(w, M))) return false;
+  if (!PrefillSupportsM(w, M)) return false;
+  // 17-64 rows the streaming kernel does not serve, on weights of 192 Mi
+  // elements and more: the prefill kernel's tiles over GemmKernel's (K =
+  // 29568, N = 8192 at M = 17 / 32 / 64: 66.5 / 67.2 / 74.1 against 80.2 /
+  // 81.6 / 92.3 us; smaller weights stay: K = 20608, N = 2048 45 against 27).
+  const bool large_unstreamed = M >= 17 && !StreamSupportsM(w, M) &&
+                                w.K * w.N >= (int64_t{192} << 20);
+  if (M < 65 && !StreamCrowded(w, M) && !large_unstreamed) return false;
   const int64_t tiles = (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN);
   const int64_t cus = w.num_cus;
   if (tiles < cus) {

@@ -187,7 +187,8 @@ def test_crowded_streaming_launches_take_prefill(pkg, orc, cuda, K, N):
 @pytest.mark.parametrize("K,N,bs,zp,kernels", [
     # Qwen2.5-72B's down projection: 115.5 units of 256 k
     (29568, 8192, 128, True, {1: "GemvFragKernel (K segments)", 2: "GemvFragKernel (K segments)",
-                              4: "DecodeFragKernel", 16: "DecodeFragKernel"}),
+                              4: "DecodeFragKernel", 16: "DecodeFragKernel",
+                              17: "PrefillKernel", 64: "PrefillKernel"}),
     (20608, 512, 64, False, {1: "GemvFragKernel (K segments)", 2: "GemvFragKernel (K segments)",
                              3: "GemvFragKernel (K segments)", 5: "DecodeFragKernel",
                              16: "DecodeFragKernel"}),
