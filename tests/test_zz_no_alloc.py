@@ -36,6 +36,8 @@ def _no_alloc(pkg, op, A, cols):
     (2048, 768, 32, False, (16, 1), 0),       # MFMA decode, then the M = 1 GEMV
     (1024, 512, 64, True, (40, 17), 1),       # exact route (groups of 16) twice
     (4096, 4096, 128, False, (64, 32), 0),    # small-M GEMM: image + K-split partials, then own conversion
+    (20608, 512, 128, True, (3, 1), 0),       # GEMV with K segments (a partial last unit): partials
+    (5120, 13824, 128, False, (64, 2), 0),    # prefill with split K (crowded stream), K segments
 ])
 def test_no_alloc_matches_run_with_workspace(pkg, orc, cuda, K, N, bs, zp, Ms, level):
     import torch
