@@ -193,6 +193,10 @@ def test_crowded_streaming_launches_take_prefill(pkg, orc, cuda, K, N):
                              3: "GemvFragKernel (K segments)", 5: "DecodeFragKernel",
                              16: "DecodeFragKernel"}),
     (1152, 1024, 32, True, {8: "DecodeFragKernel", 16: "DecodeFragKernel"}),
+    # 256-k blocks: the last block is half past K (its scale in range)
+    (20608, 512, 256, True, {1: "GemvFragKernel (K segments)", 3: "GemvFragKernel (K segments)",
+                             8: "DecodeFragKernel"}),
+    (20608, 512, 256, False, {2: "GemvFragKernel (K segments)", 16: "DecodeFragKernel"}),
 ])
 def test_k_not_whole_units(pkg, orc, cuda, K, N, bs, zp, kernels):
     """K that is not a multiple of 256 (the activation exponent's unit): the
