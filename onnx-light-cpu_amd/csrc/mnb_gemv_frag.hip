@@ -721,7 +721,10 @@ static bool SegmentsBalance(const WeightView &w, int64_t M) {
 }
 
 bool GemvFragSegSupports(const WeightView &w, int64_t M) {
-  // As GemvFragSupports, K split into segments of whole units: 1 or 2 rows
+  // As GemvFragSupports, K split into segments of whole units (a K that is
+  // not a multiple of 256 ends in a partly filled unit). Where the single-
+  // workgroup launch is the automatic choice (GemvFragPreferred): only where
+  // the segments balance the CUs (SegmentsBalance). Elsewhere: 1 or 2 rows
   // too long for one workgroup (no single-workgroup launch fits); 3 or 4
   // rows of at least 5120 on weights of at most 192 Mi elements, where the
   // segments beat the small-M MFMA decode (shorter rows pay more for the
