@@ -449,7 +449,43 @@ struct Shape {
 // zero activations (masked by SplitActKernel).
 inline int Units(const WeightView &w) { return static_cast<int>((w.K + kUnitK - 1) / kUnitK); }
 
+// Four units per wavefront (U = 4) give wide weights with 4096 < K <= 8192
+// one run where two units need two (K = 5120: 5 x 4 units, not 10 x 2 past
+// the 8-wavefront bound). Taken where it lowers the busiest CU's work,
+// ceil(workgroups / CUs) x 8 U steps plus 12 for the partial-sum pass of a
+// split run, fewer runs on a tie: measured (us, M = 5 / 8 / 16) K = 5120,
+// N = 27648 26.2 / 26.4 / 34.8 -> 20.2 / 21.0 / 29.2; K = 6144, N = 16384
+// at M = 8 17.9 -> 15.5; K = 8192, N = 28672 at M = 16 43.4 -> 39.2;
+// K = 14336, N = 24576 (two runs instead of four) at M = 8 / 16 47.1 /
+// 62.4 -> 43.0 / 57.5. Not where one run leaves a second round on a few
+// CUs (K = 7168, N = 18432, 288 groups: 22.3 / 30.8 at M = 5 / 16 with two
+// runs of two units against 24.6 / 31.9).
+inline int64_t ShapeCost(const Shape &sh, int64_t groups, int64_t cus) {
+  return (groups * sh.segs + cus - 1) / cus * (sh.units_per_wave * kUnitSteps) +
+         (sh.segs > 1 ? 12 : 0);
+}
+
+inline Shape PickShapeU12(const WeightView &w, int wpg_req, int u_req);
+
 inline Shape PickShape(const WeightView &w, int wpg_req, int u_req) {
+  Shape best = PickShapeU12(w, wpg_req, u_req);
+  if (wpg_req > 0 || u_req > 0) return best;
+  const int64_t groups = (w.N + 63) / 64, cus = std::max<int64_t>(1, w.num_cus);
+  const int units = Units(w);
+  for (int segs = 1; segs <= std::min(units, 16); ++segs) {
+    if (units % segs != 0 || (units / segs) % 4 != 0) continue;
+    const int wpg = units / segs / 4;
+    if (wpg < 4 || wpg > kMaxWaves) continue;
+    if (segs < units && groups * segs * 100 < cus * 85) continue;
+    const Shape u4{wpg, 4, segs};
+    const int64_t c4 = ShapeCost(u4, groups, cus), cb = ShapeCost(best, groups, cus);
+    if (c4 < cb || (c4 == cb && segs < best.segs)) best = u4;
+    break;  // the fewest runs
+  }
+  return best;
+}
+
+inline Shape PickShapeU12(const WeightView &w, int wpg_req, int u_req) {
   const int64_t groups = (w.N + 63) / 64;
   const int units = Units(w);
   Shape sh{1, 1, units};
@@ -523,10 +559,12 @@ template <bool HAS_ZP, int SPB>
 hipError_t LaunchU(const WeightView &w, int64_t M, const Work &wk, float *Y, float *H,
                    const float *bias, const Shape &sh, hipStream_t s) {
   if (M <= 8)
-    return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2, 8>(w, M, wk, Y, H, bias, sh, s)
-                                  : LaunchMain<HAS_ZP, SPB, 1, 8>(w, M, wk, Y, H, bias, sh, s);
-  return sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2, 16>(w, M, wk, Y, H, bias, sh, s)
-                                : LaunchMain<HAS_ZP, SPB, 1, 16>(w, M, wk, Y, H, bias, sh, s);
+    return sh.units_per_wave == 4   ? LaunchMain<HAS_ZP, SPB, 4, 8>(w, M, wk, Y, H, bias, sh, s)
+           : sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2, 8>(w, M, wk, Y, H, bias, sh, s)
+                                    : LaunchMain<HAS_ZP, SPB, 1, 8>(w, M, wk, Y, H, bias, sh, s);
+  return sh.units_per_wave == 4   ? LaunchMain<HAS_ZP, SPB, 4, 16>(w, M, wk, Y, H, bias, sh, s)
+         : sh.units_per_wave == 2 ? LaunchMain<HAS_ZP, SPB, 2, 16>(w, M, wk, Y, H, bias, sh, s)
+                                  : LaunchMain<HAS_ZP, SPB, 1, 16>(w, M, wk, Y, H, bias, sh, s);
 }
 
 template <bool HAS_ZP>
@@ -587,7 +625,7 @@ hipError_t LaunchDecodeFrag(const WeightView &w, int64_t M, const float *A, floa
   if (sh.wpg < 1 || sh.wpg > df::kMaxWaves || sh.segs < 1 ||
       sh.segs * sh.wpg * sh.units_per_wave < units ||
       (sh.segs - 1) * sh.wpg * sh.units_per_wave >= units ||
-      (sh.units_per_wave != 1 && sh.units_per_wave != 2))
+      (sh.units_per_wave != 1 && sh.units_per_wave != 2 && sh.units_per_wave != 4))
     return hipErrorInvalidValue;
   if (gamma != nullptr && !DecodeFragTakesRms(w)) return hipErrorInvalidValue;
   if (gamma != nullptr && (reinterpret_cast<uintptr_t>(gamma) % 16) != 0) return hipErrorInvalidValue;

@@ -216,3 +216,37 @@ def test_k_not_whole_units(pkg, orc, cuda, K, N, bs, zp, kernels):
     finally:
         op.release()
     _check_sampled(pkg, orc, cuda, K, N, bs, zp, tuple(kernels), seed=K + 3)
+
+
+@pytest.mark.parametrize("K,N,bs,zp,old", [
+    (5120, 14336, 128, True, (5, 2)),   # 20 units: one run of 5 x 4 (two runs of 5 x 2 before)
+    (8192, 14336, 64, False, (8, 2)),   # 32 units: one run of 8 x 4 (two of 8 x 2)
+])
+def test_small_m_decode_four_units_per_wavefront(pkg, orc, cuda, K, N, bs, zp, old):
+    """Wide weights with 4096 < K <= 8192 at 5-16 rows: the small-M MFMA
+    decode with four units per wavefront covers each row in one run (no
+    partial sums); sampled columns against the fp64 oracle, bit-identical
+    from run to run, and within the bound of the two-run shape forced."""
+    import torch
+    p = pkg.workloads.Projection("u4", K, N, bs, zp, 1.0, 0.005, 0.02)
+    B, S, Z = pkg.workloads.make_weights(p, K + 4)
+    cols = np.sort(np.random.default_rng(K).choice(N, size=512, replace=False))
+    Zc = Z[cols] if Z is not None else None
+    op = pkg.MatMulNBits(K, N, 4, bs).prepare(B, S, Z)
+    try:
+        for M in (5, 8, 16):
+            print(f"case four units K={K} N={N} bs={bs} zp={zp} M={M} kernel={op.kernel_name(M)}",
+                  flush=True)
+            assert op.kernel_name(M) == "DecodeFragKernel"
+            A = pkg.workloads.make_activations(M, K, 1.0, K + M)
+            dA = torch.from_numpy(A).to(cuda)
+            Y = op(dA).cpu().numpy()
+            np.testing.assert_array_equal(op(dA).cpu().numpy(), Y)
+            y64 = orc.matmul_nbits_f64(A, B[cols], S[cols], Zc, K, len(cols), bs)
+            err = orc.normwise_max_error(Y[:, cols], y64)
+            Yo = op.run_kernel(dA, pkg.KERNEL_DECODE_FRAG, *old).cpu().numpy()
+            err_old = orc.normwise_max_error(Yo[:, cols], y64)
+            print(f"  normwise error vs fp64 {err:.2e} (two runs forced: {err_old:.2e})")
+            assert err <= GEMV_TOL and err_old <= GEMV_TOL
+    finally:
+        op.release()
