@@ -843,16 +843,20 @@ def main():
         # (K = 29568: not a whole number of 256-k units), Gemma-7B's at 4
         # rows (K = 24576, N = 3072: K segments on narrow weights) and a
         # wide projection whose row groups (288) leave a second round on a
-        # few CUs (K = 7168, N = 18432: K segments to balance them)
+        # few CUs (K = 7168, N = 18432: K segments to balance them), and a
+        # Qwen2.5-14B-shaped gate+up projection at 8 rows (K = 5120 = 20 units:
+        # one run of four units per wavefront in the small-M decode)
         tp8 = {"c2/tp8": W.Projection("c2/tp8", 4096, 14336 // 8, 128, True),
                "c3/tp8": W.Projection("c3/tp8", 14336 // 8, 4096, 32, True, 0.5, 0.002, 0.01),
                "70b_down": W.Projection("70b_down", 28672, 8192, 128, True),
                "qwen72b_down": W.Projection("qwen72b_down", 29568, 8192, 128, True),
                "gemma7b_down": W.Projection("gemma7b_down", 24576, 3072, 128, True),
-               "wide_7168": W.Projection("wide_7168", 7168, 18432, 128, True)}
+               "wide_7168": W.Projection("wide_7168", 7168, 18432, 128, True),
+               "gate_up_5120": W.Projection("gate_up_5120", 5120, 27648, 128, True)}
         for cname, Ms in (("c1", (1,)), ("c2", (4, 16)), ("c3", (1, 2, 8, 16)),
                           ("c2/tp8", (1, 16)), ("c3/tp8", (1, 16)), ("70b_down", (1, 2)),
-                          ("qwen72b_down", (1, 16)), ("gemma7b_down", (4,)), ("wide_7168", (1,))):
+                          ("qwen72b_down", (1, 16)), ("gemma7b_down", (4,)), ("wide_7168", (1,)),
+                          ("gate_up_5120", (8,))):
             p = tp8[cname] if cname in tp8 else W.CONFIGS[cname].projections[0]
             for M in Ms:
                 r = decode_leg(torch, pkg, dev, p, M, max(3, args.steps // 4), 2, 17 + M, stream)
