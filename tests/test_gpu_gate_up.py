@@ -44,6 +44,8 @@ CASES = [
     (1536, 150, 64, True, (1, 2, 5, 33)),      # ragged: N = 300 rows, odd band sizes
     (512, 256, 32, False, (1, 8)),             # one 512-k range in the MFMA decode
     (2048, 2048, 32, False, (2048,)),          # GEMM with one split: fused stores
+    (5120, 7168, 128, True, (8, 16)),          # small-M decode, one run of 4 units per wavefront:
+                                               # the activation in its epilogue
 ]
 
 
