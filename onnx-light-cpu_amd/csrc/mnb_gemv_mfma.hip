@@ -415,6 +415,13 @@ __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
   if constexpr (VEC) {
     const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
     if (i >= mn) return;
+    // the bias is loaded with the sums (added after them: a separate bias
+    // pass; N % 4 == 0 here)
+    floatx4 b = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (bias != nullptr) {
+      const int64_t n = i % N;
+      b = floatx4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
+    }
     floatx4 y = *reinterpret_cast<const floatx4 *>(Y + i);
     for (int p = 0; p < parts; p += kBatch) {
       floatx4 v[kBatch];
@@ -426,10 +433,7 @@ __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
       for (int q = 0; q < kBatch; ++q)
         if (p + q < parts) y += v[q];
     }
-    if (bias != nullptr) {  // after the sum, as a separate bias pass; N % 4 == 0 here
-      const int64_t n = i % N;
-      y += floatx4{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
-    }
+    if (bias != nullptr) y += b;
     if (H != nullptr) {
       // gate/up pairs (N even, so a pair never straddles rows)
       *reinterpret_cast<float2 *>(H + i / 2) = make_float2(SiluMul(y[0], y[1]), SiluMul(y[2], y[3]));
@@ -439,6 +443,7 @@ __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
   } else {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     if (i >= mn) return;
+    const float b = bias != nullptr ? bias[i % N] : 0.f;
     float y = Y[i];
     for (int p = 0; p < parts; p += kBatch) {
       float v[kBatch];
@@ -449,7 +454,7 @@ __global__ __launch_bounds__(256) void SumPartialsKernel(float *__restrict__ Y,
       for (int q = 0; q < kBatch; ++q)
         if (p + q < parts) y += v[q];
     }
-    if (bias != nullptr) y += bias[i % N];
+    if (bias != nullptr) y += b;
     if (H != nullptr) {
       // mn is even: lanes i and i ^ 1 are both in range, in the same wavefront
       const float other = PairSwap(y);
