@@ -1413,7 +1413,13 @@ hipError_t LaunchStreamZp(const WeightView &w, int64_t M, const uint4 *Ah, const
 // Splits of a prefill launch: as many as keep the workgroups within one per
 // CU when the tiles alone do not fill the chip (a second, partial wave costs
 // a whole k-loop), at most kPrefillMaxSplits, each split at least 8 k-tiles.
-constexpr int kPrefillMaxSplits = 8;
+// Up to 16 splits serve long rows on few tiles (against 8: K = 14336,
+// N = 4096 at M = 65 / 128 38.1 / 40.4 -> 33.1 / 38.4 us; K = 14336,
+// N = 2048 at M = 128 38.2 -> 31.8; K = 11008, N = 4096 at M = 65 33.0 ->
+// 30.2; c4, c5 qkv and o unchanged). Whether the prefill kernel takes such
+// rows at all is judged at 8 splits (UsePrefill, kPrefillCheckSplits).
+constexpr int kPrefillMaxSplits = 16;
+constexpr int kPrefillCheckSplits = 8;
 inline int PrefillSplits(const WeightView &w, int64_t M) {
   const int64_t tiles = (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN);
   const int ktiles = static_cast<int>(w.K / kBK);
@@ -1538,7 +1544,7 @@ bool UsePrefill(const WeightView &w, int64_t M) {
   const int64_t tiles = (M + kPTM - 1) / kPTM * ((w.N + kPTN - 1) / kPTN);
   const int64_t cus = w.num_cus;
   if (tiles < cus) {
-    const int64_t splits = std::min<int64_t>(cus / tiles, kPrefillMaxSplits);
+    const int64_t splits = std::min<int64_t>(cus / tiles, kPrefillCheckSplits);
     return w.K / kBK >= 12 * splits;
   }
   const int64_t last = tiles - (tiles - 1) / cus * cus;  // workgroups in the last wave
