@@ -457,6 +457,16 @@ __global__ __launch_bounds__(256, 2) void GemmKernel(const uint4 *__restrict__ A
   if (kt < ktiles) step(kt, std::integral_constant<int, 0>{});
   if (kt + 1 < ktiles) step(kt + 1, std::integral_constant<int, 1>{});
   if (kt + 2 < ktiles) step(kt + 2, std::integral_constant<int, 2>{});
+  // The remainder steps' B loads feed no later tile, so the compiler would
+  // drop them, and from the second remainder step on the wait at a step's
+  // top (which counts kBOps loads per step) would no longer cover that step's
+  // A copy: a wavefront could read an A stage before the copy landed (seen as
+  // one 8-row x 64-column block of an output tile off by a k-tile's share,
+  // intermittently, with split K). Using the registers here keeps every load.
+#pragma unroll
+  for (int p = 0; p < kPD; ++p)
+    __asm__ volatile("" ::"v"(rb[p].b.x), "v"(rb[p].b.y), "v"(rb[p].b.z), "v"(rb[p].b.w),
+                     "v"(rb[p].s), "v"(rb[p].z));
   // No copy into this workgroup's LDS may land after it exits.
   WaitVm<0>();
 
