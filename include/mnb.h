@@ -158,8 +158,10 @@ int mnb_workspace_bytes(const mnb_plan *plan, int64_t M, size_t *bytes);
  * 2 fp16, 3 bf16, 4 int8): at level 1, M > 16 runs the exact-product decode
  * kernels 16 rows at a time (path 4) instead of the fp16 GEMM; levels 0
  * (unset, this library's default) and 2-4 take the GEMM, whose 11-bit
- * activations meet what levels 2-4 permit. The launch is asynchronous on
- * `stream`. */
+ * activations meet what levels 2-4 permit. M > 16 with K an odd multiple
+ * of 32, which the GEMM kernels do not take, runs path 4 at every level;
+ * K not a multiple of 32 runs the generic kernel (path 3). The launch is
+ * asynchronous on `stream`. */
 int mnb_run(const mnb_plan *plan, int64_t M, const float *dA, float *dY, void *dWorkspace,
             size_t workspace_bytes, void *stream);
 

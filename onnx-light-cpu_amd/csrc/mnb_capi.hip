@@ -747,7 +747,9 @@ static int SelectPath(const mnb_plan *plan, int64_t M, const float *dA) {
   if (a_aligned && DecodeSupported(plan, M)) return 1;
   if (Fp32ActivationsOnly(plan)) return ExactGroupsSupported(plan, a_aligned) ? 4 : 3;
   if (a_aligned && mnb::GemmSupports(plan->view, M)) return 2;
-  return 3;
+  // Rows the GEMM kernels cannot take (K an odd multiple of 32): the decode
+  // kernels 16 rows at a time rather than one wavefront per output.
+  return ExactGroupsSupported(plan, a_aligned) ? 4 : 3;
 }
 
 // Workspace the automatic path (mnb_run) takes for M rows of dA: the chosen

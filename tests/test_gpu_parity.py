@@ -126,6 +126,23 @@ def test_gemm_split_k(pkg, orc, cuda, K, N, bs, zp, M, y_offset):
     op.release()
 
 
+@pytest.mark.parametrize("K,N,bs,zp", [(1056, 300, 32, True), (4128, 1000, 128, False),
+                                       (2080, 64, 64, True)])
+@pytest.mark.parametrize("M", [17, 40, 100])
+def test_odd_k_tiles_exact_groups(pkg, orc, cuda, K, N, bs, zp, M):
+    """K an odd multiple of 32 above 16 rows: the GEMM kernels take K in
+    64-k tiles, so the automatic path runs the decode kernels over groups of
+    16 rows (path 4), within the decode bound and equal to the forced run."""
+    p, B, S, Z = _case(pkg, K, N, bs, zp, seed=K + N + M)
+    A = pkg.workloads.make_activations(M, K, 1.0, seed=M + 5)
+    Y, path = _run(pkg, cuda, K, N, bs, B, S, Z, A)
+    assert path == pkg.PATH_EXACT
+    Y4, _ = _run(pkg, cuda, K, N, bs, B, S, Z, A, path=pkg.PATH_EXACT)
+    np.testing.assert_array_equal(Y, Y4)
+    y64 = orc.matmul_nbits_f64(A, B, S, Z, K, N, bs)
+    assert orc.normwise_max_error(Y, y64) <= GEMV_TOL
+
+
 @pytest.mark.parametrize("K,N,bs,zp", [(100, 37, 32, True), (33, 5, 16, False),
                                        (1000, 64, 128, True), (4095, 19, 64, False)])
 @pytest.mark.parametrize("M", [1, 5, 20])
